@@ -1,0 +1,232 @@
+"""deepfuse_amd -- MI355X-native fp8 Linear path of DeepFuse, Python side.
+
+The product is the C ABI in ``include/df_capi.h`` implemented by
+``deepfuse_amd/libdeepfuse_amd.so`` (hand-written HIP for gfx950).  This module
+binds it with ctypes and offers thin helpers over torch device tensors (torch
+is only the allocator and stream provider here).  Nothing in this package has
+a CPU fallback: if the HIP library is missing, :func:`lib` raises.
+
+Reference mapping (SensorVista/DeepFuse):
+  - ``DType`` mirrors ``OnnxLoader::DType`` (dnn/utils/onnx_loader.cuh:16-22),
+    extended with the 1-byte fp8 formats.
+  - ``fc_forward`` / ``fc_backward`` mirror ``FullyConnectedLayer<T>::forward``
+    / ``backward`` (dnn/layers/fully_connected_layer.cu:164-357) in fp8 compute.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdeepfuse_amd.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "df_capi.h")
+
+
+class DType(enum.IntEnum):
+    FLOAT32 = 0
+    HALF = 1
+    INT8 = 2
+    UINT8 = 3
+    BFLOAT16 = 4
+    FP8E4M3 = 5
+    FP8E5M2 = 6
+    INT32 = 7
+
+
+class Fmt(enum.IntEnum):
+    E4M3 = 0
+    E5M2 = 1
+
+
+FMAX = {Fmt.E4M3: 448.0, Fmt.E5M2: 57344.0}
+
+
+class DFError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} failed with status {status}: {msg}")
+        self.status = status
+
+
+_c_int, _c_i64, _c_sz, _c_f = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+_vp = ctypes.c_void_p
+
+# name -> (restype, argtypes); every function declared in df_capi.h
+_SIGS = {
+    "df_last_error_string": (ctypes.c_char_p, []),
+    "df_version": (_c_int, []),
+    "df_device_arch_ok": (_c_int, []),
+    "df_absmax_workspace_bytes": (_c_sz, []),
+    "df_absmax_f32": (_c_int, [_vp, _c_i64, _vp, _vp, _c_sz, _vp]),
+    "df_absmax_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _c_sz, _vp]),
+    "df_absmax_scale_f32": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "df_absmax_scale_bf16": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "df_compute_scale": (_c_int, [_vp, _c_int, _vp, _vp]),
+    "df_quantize_f32_e4m3": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_quantize_f32_e5m2": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_quantize_bf16_e4m3": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_quantize_bf16_e5m2": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_dequantize_e4m3_f32": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_dequantize_e5m2_f32": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_dequantize_e4m3_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_dequantize_e5m2_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "df_quantize_2d": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
+                                _vp, _c_int, _vp]),
+    "df_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
+                                _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp]),
+    "df_fp8_gemm_fwd": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                 _c_int, _vp, _c_int, _vp, _c_int, _vp]),
+    "df_fp8_gemm_bwd_dx": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                    _c_int, _vp, _c_int, _vp]),
+    "df_fp8_gemm_bwd_dw": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                    _c_int, _vp, _c_int, _vp]),
+    "df_fill": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp]),
+    "df_add": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
+    "df_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
+    "df_approx_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_f, _vp]),
+}
+
+_lib = None
+
+
+def header_functions() -> list[str]:
+    """Names of the functions include/df_capi.h declares."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(df_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdeepfuse_amd.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(make -C deepfuse_amd); there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != 0:
+        msg = lib().df_last_error_string()
+        raise DFError(fn, status, msg.decode() if msg else "")
+
+
+def call(fn: str, *args) -> None:
+    check(fn, getattr(lib(), fn)(*args))
+
+
+# ----------------------------------------------------------------------------
+# torch helpers (device memory + current stream); the compute is the C ABI
+# ----------------------------------------------------------------------------
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    torch = _torch()
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _in_dtype(t) -> DType:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return DType.FLOAT32
+    if t.dtype == torch.bfloat16:
+        return DType.BFLOAT16
+    raise TypeError(f"unsupported input dtype {t.dtype}")
+
+
+_WS = {}
+
+
+def _workspace(device):
+    torch = _torch()
+    key = str(device)
+    if key not in _WS:
+        _WS[key] = torch.empty(lib().df_absmax_workspace_bytes(), dtype=torch.uint8, device=device)
+    return _WS[key]
+
+
+def absmax_scale(x, fmt: Fmt):
+    """(absmax, scale) as 1-element fp32 device tensors, contract D1/D2."""
+    torch = _torch()
+    am = torch.empty(1, dtype=torch.float32, device=x.device)
+    sc = torch.empty(1, dtype=torch.float32, device=x.device)
+    ws = _workspace(x.device)
+    fn = "df_absmax_scale_f32" if _in_dtype(x) == DType.FLOAT32 else "df_absmax_scale_bf16"
+    call(fn, _ptr(x), x.numel(), int(fmt), _ptr(am), _ptr(sc), _ptr(ws), ws.numel(), _stream())
+    return am, sc
+
+
+def quantize(x, scale, fmt: Fmt):
+    """Flat quantize of a contiguous fp32/bf16 tensor -> uint8 codes (same shape)."""
+    torch = _torch()
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    src = "f32" if _in_dtype(x) == DType.FLOAT32 else "bf16"
+    fn = f"df_quantize_{src}_{'e4m3' if fmt == Fmt.E4M3 else 'e5m2'}"
+    call(fn, _ptr(x), x.numel(), _ptr(scale), _ptr(q), _stream())
+    return q
+
+
+def dequantize(q, scale, fmt: Fmt, out_dtype):
+    torch = _torch()
+    out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+    dst = "f32" if out_dtype == torch.float32 else "bf16"
+    fn = f"df_dequantize_{'e4m3' if fmt == Fmt.E4M3 else 'e5m2'}_{dst}"
+    call(fn, _ptr(q), q.numel(), _ptr(scale), _ptr(out), _stream())
+    return out
+
+
+def round16(v: int) -> int:
+    return (v + 15) // 16 * 16
+
+
+def quantize_2d(x, scale, fmt: Fmt, want_q=True, want_qt=False):
+    """2-D quantize into GEMM operand layout: returns (q [R, ceil16(C)],
+    qt [C, ceil16(R)]) with zero padding; either may be None."""
+    torch = _torch()
+    rows, cols = x.shape
+    q = torch.empty((rows, round16(cols)), dtype=torch.uint8, device=x.device) if want_q else None
+    qt = torch.empty((cols, round16(rows)), dtype=torch.uint8, device=x.device) if want_qt else None
+    call("df_quantize_2d", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), int(fmt), _ptr(scale),
+         _ptr(q), q.shape[1] if q is not None else 0, _ptr(qt), qt.shape[1] if qt is not None else 0,
+         _stream())
+    return q, qt
+
+
+def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dtype=None):
+    """C[M,N] = (A[M,:K] . B[N,:K]^T) * sa * sb + bias on fp8 MFMA."""
+    torch = _torch()
+    out_dtype = out_dtype or torch.float32
+    M, N = a_q.shape[0], b_q.shape[0]
+    c = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
+    bias_dt = int(DType.FLOAT32) if bias is None or bias.dtype == torch.float32 else int(DType.BFLOAT16)
+    c_dt = int(DType.FLOAT32) if out_dtype == torch.float32 else int(DType.BFLOAT16)
+    call("df_fp8_gemm_nt", int(fmt_a), _ptr(a_q), a_q.stride(0), int(fmt_b), _ptr(b_q), b_q.stride(0),
+         M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _stream())
+    return c
+
+
+def colsum(x):
+    torch = _torch()
+    out = torch.empty(x.shape[1], dtype=torch.float32, device=x.device)
+    call("df_colsum", int(_in_dtype(x)), _ptr(x), x.shape[0], x.shape[1], x.stride(0), _ptr(out),
+         _stream())
+    return out

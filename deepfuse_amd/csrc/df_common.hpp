@@ -1,0 +1,122 @@
+// df_common.hpp -- shared host/device helpers for libdeepfuse_amd (gfx950).
+//
+// Device side: the OCP OFP8 v1.0 codec (e4m3 / e5m2), round-to-nearest-even
+// and saturating, written for the VALU (integer-domain significand rounding,
+// one v_rndne for subnormal targets), plus bf16 rounding.  The contract it
+// implements (scale rule, NaN/inf policy, subnormals) is the one stated at the
+// top of include/df_capi.h.
+//
+// Host side: the thread-local error string behind df_last_error_string() and
+// the argument-check macros every C-ABI entry point uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/df_capi.h"
+
+namespace dfk {
+
+// native clang vectors (the nontemporal builtins take these, not HIP's
+// HIP_vector_type wrappers)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- formats --
+enum : int { E4M3 = DF_FMT_E4M3, E5M2 = DF_FMT_E5M2 };
+
+template <int FMT> struct Fp8;
+template <> struct Fp8<E4M3> {
+    static constexpr int mbits = 3, bias = 7;
+    static constexpr uint32_t max_bits = 0x43E00000u;  // 448.0f
+    static constexpr uint32_t max_code = 0x7Eu;
+    static constexpr float fmax = 448.0f;
+};
+template <> struct Fp8<E5M2> {
+    static constexpr int mbits = 2, bias = 15;
+    static constexpr uint32_t max_bits = 0x47600000u;  // 57344.0f
+    static constexpr uint32_t max_code = 0x7Bu;
+    static constexpr float fmax = 57344.0f;
+};
+
+// ----------------------------------------------------------------- encode --
+// binary32 -> fp8 code in the low byte.  |v| >= max (inf included) saturates,
+// NaN gives sign|0x7F.  Normal targets round the re-biased significand in
+// the integer domain; subnormal targets scale by 2^(bias-1+mbits) (exact)
+// and round to an integer with v_rndne_f32.
+template <int FMT>
+__device__ __forceinline__ uint32_t encode_fp8(float v) {
+    using T = Fp8<FMT>;
+    constexpr int sh = 23 - T::mbits;
+    constexpr uint32_t min_normal_bits = (uint32_t)(128 - T::bias) << 23;
+    constexpr float sub_scale = (float)(1u << (T::bias - 1 + T::mbits));
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7FFFFFFFu;
+    const uint32_t ac = a < T::max_bits ? a : T::max_bits;
+    uint32_t r = ac - ((uint32_t)(127 - T::bias) << 23);
+    r = (r + ((1u << (sh - 1)) - 1u) + ((r >> sh) & 1u)) >> sh;
+    const uint32_t rs = (uint32_t)__builtin_rintf(__uint_as_float(ac) * sub_scale);
+    uint32_t code = ac < min_normal_bits ? rs : r;
+    code = a > 0x7F800000u ? 0x7Fu : code;
+    return code | sign;
+}
+
+// ----------------------------------------------------------------- decode --
+// fp8 code (low byte) -> binary32, exact.  The magnitude bits shifted into
+// the binary32 exponent/significand position are the value times
+// 2^-(127-bias) for normal and subnormal codes alike (binary32 subnormals
+// are honoured), so one multiply by 2^(127-bias) restores it.
+template <int FMT>
+__device__ __forceinline__ float decode_fp8(uint32_t q) {
+    using T = Fp8<FMT>;
+    constexpr float up = (FMT == E4M3) ? 0x1p120f : 0x1p112f;
+    const uint32_t mag = q & 0x7Fu;
+    const uint32_t sign = (q & 0x80u) << 24;
+    float v = __uint_as_float(mag << (23 - T::mbits)) * up;
+    uint32_t bits = __float_as_uint(v) | sign;
+    if (FMT == E4M3) {
+        bits = mag == 0x7Fu ? (sign | 0x7FC00000u) : bits;
+    } else {
+        bits = mag == 0x7Cu ? (sign | 0x7F800000u) : bits;
+        bits = mag > 0x7Cu ? (sign | 0x7FC00000u) : bits;
+    }
+    return __uint_as_float(bits);
+}
+
+// dequantized value: decode(q) * s, NaN codes -> canonical quiet NaN.
+template <int FMT>
+__device__ __forceinline__ float dequant_fp8(uint32_t q, float s) {
+    const uint32_t mag = q & 0x7Fu;
+    const bool is_nan = (FMT == E4M3) ? (mag == 0x7Fu) : (mag > 0x7Cu);
+    const float v = decode_fp8<FMT>(q) * s;
+    return is_nan ? __uint_as_float(((q & 0x80u) << 24) | 0x7FC00000u) : v;
+}
+
+// ------------------------------------------------------------------- bf16 --
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    return (u & 0x7FFFFFFFu) > 0x7F800000u ? (((u >> 16) & 0x8000u) | 0x7FC0u) : r;
+}
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// ------------------------------------------------------------- host side --
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+int launch_status(const char* what);  // DF_OK or DF_ERR_HIP (checks hipGetLastError)
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace dfk
+
+#define DF_CHECK(cond, code, ...)          \
+    do {                                   \
+        if (!(cond)) {                     \
+            ::dfk::set_error(__VA_ARGS__); \
+            return (code);                 \
+        }                                  \
+    } while (0)

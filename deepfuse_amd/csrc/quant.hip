@@ -1,0 +1,545 @@
+// quant.hip -- absmax, scale, quantize and dequantize kernels (gfx950).
+//
+// All four are HBM-bandwidth kernels.  Layout: flat, contiguous tensors.
+// Each thread moves 16 bytes per global load (dwordx4) on the wide side of
+// the conversion, a wave covers 1 KiB contiguous per instruction, and the
+// grid is a fixed multiple of the CU count with a grid-stride loop so every
+// CU keeps several loads in flight.
+//
+// Reference: the reference has no quantizer (README.md:16 claim only; fp8 is
+// a type at dnn/core/tensor.cu:489-498).  Semantics: include/df_capi.h.
+#include <hip/hip_runtime.h>
+
+#include "df_common.hpp"
+
+namespace dfk {
+
+constexpr int kThreads = 256;
+constexpr int kMaxReduceBlocks = 2048;  // partials in the absmax workspace
+
+// ------------------------------------------------------------------ absmax --
+// |x| over finite values as an unsigned max of the sign-cleared bit patterns
+// (monotone for non-negative binary32); inf/NaN patterns (>= 0x7F800000)
+// contribute 0.
+__device__ __forceinline__ uint32_t fold_f32(uint32_t m, uint32_t bits) {
+    const uint32_t a = bits & 0x7FFFFFFFu;
+    return max(m, a < 0x7F800000u ? a : 0u);
+}
+// two bf16 in one dword: widen each to its binary32 pattern
+__device__ __forceinline__ uint32_t fold_bf16x2(uint32_t m, uint32_t w) {
+    const uint32_t hi = w & 0x7FFF0000u;
+    const uint32_t lo = (w << 16) & 0x7FFF0000u;
+    m = max(m, hi < 0x7F800000u ? hi : 0u);
+    return max(m, lo < 0x7F800000u ? lo : 0u);
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t m) {
+    __shared__ uint32_t red[kThreads / 64];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 1; w < kThreads / 64; ++w) m = max(m, red[w]);
+    }
+    return m;  // valid in thread 0
+}
+
+// Stage 1, fp32: 16-byte loads, four in flight per thread per iteration.
+__global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __restrict__ x,
+                                                               int64_t n,
+                                                               uint32_t* __restrict__ partial) {
+    uint32_t m = 0;
+    const int64_t nvec = n >> 2;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+        u32x4 v0 = __builtin_nontemporal_load(xv + i);
+        u32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
+        u32x4 v2 = __builtin_nontemporal_load(xv + i + 2 * stride);
+        u32x4 v3 = __builtin_nontemporal_load(xv + i + 3 * stride);
+        m = fold_f32(m, v0.x); m = fold_f32(m, v0.y); m = fold_f32(m, v0.z); m = fold_f32(m, v0.w);
+        m = fold_f32(m, v1.x); m = fold_f32(m, v1.y); m = fold_f32(m, v1.z); m = fold_f32(m, v1.w);
+        m = fold_f32(m, v2.x); m = fold_f32(m, v2.y); m = fold_f32(m, v2.z); m = fold_f32(m, v2.w);
+        m = fold_f32(m, v3.x); m = fold_f32(m, v3.y); m = fold_f32(m, v3.z); m = fold_f32(m, v3.w);
+    }
+    for (; i < nvec; i += stride) {
+        u32x4 v = xv[i];
+        m = fold_f32(m, v.x); m = fold_f32(m, v.y); m = fold_f32(m, v.z); m = fold_f32(m, v.w);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3))
+        m = fold_f32(m, __float_as_uint(x[(nvec << 2) + threadIdx.x]));
+    m = block_max_u32(m);
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+// Stage 1, bf16: 16-byte loads hold 8 values.
+__global__ __launch_bounds__(kThreads) void absmax_bf16_stage1(const uint16_t* __restrict__ x,
+                                                                int64_t n,
+                                                                uint32_t* __restrict__ partial) {
+    uint32_t m = 0;
+    const int64_t nvec = n >> 3;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+        u32x4 v0 = __builtin_nontemporal_load(xv + i);
+        u32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
+        u32x4 v2 = __builtin_nontemporal_load(xv + i + 2 * stride);
+        u32x4 v3 = __builtin_nontemporal_load(xv + i + 3 * stride);
+        m = fold_bf16x2(m, v0.x); m = fold_bf16x2(m, v0.y); m = fold_bf16x2(m, v0.z); m = fold_bf16x2(m, v0.w);
+        m = fold_bf16x2(m, v1.x); m = fold_bf16x2(m, v1.y); m = fold_bf16x2(m, v1.z); m = fold_bf16x2(m, v1.w);
+        m = fold_bf16x2(m, v2.x); m = fold_bf16x2(m, v2.y); m = fold_bf16x2(m, v2.z); m = fold_bf16x2(m, v2.w);
+        m = fold_bf16x2(m, v3.x); m = fold_bf16x2(m, v3.y); m = fold_bf16x2(m, v3.z); m = fold_bf16x2(m, v3.w);
+    }
+    for (; i < nvec; i += stride) {
+        u32x4 v = xv[i];
+        m = fold_bf16x2(m, v.x); m = fold_bf16x2(m, v.y); m = fold_bf16x2(m, v.z); m = fold_bf16x2(m, v.w);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 7))
+        m = fold_f32(m, (uint32_t)x[(nvec << 3) + threadIdx.x] << 16);
+    m = block_max_u32(m);
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+// scale rule D1/D2: s = absmax / fmax (IEEE division); absmax == 0 or a
+// scale that is not a positive finite number gives 1.
+__device__ __forceinline__ float scale_from_absmax(float am, int fmt) {
+    const float fmax = fmt == E4M3 ? Fp8<E4M3>::fmax : Fp8<E5M2>::fmax;
+    if (!(am > 0.0f) || !(am <= 3.4028234663852886e38f)) return 1.0f;
+    const float s = am / fmax;
+    return (s > 0.0f && s <= 3.4028234663852886e38f) ? s : 1.0f;
+}
+
+// Stage 2: one block folds the partials, writes absmax and (optionally) scale.
+__global__ __launch_bounds__(kThreads) void absmax_stage2(const uint32_t* __restrict__ partial,
+                                                           int nparts, int fmt,
+                                                           float* __restrict__ absmax_out,
+                                                           float* __restrict__ scale_out) {
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
+    m = block_max_u32(m);
+    if (threadIdx.x == 0) {
+        const float am = __uint_as_float(m);
+        if (absmax_out) absmax_out[0] = am;
+        if (scale_out) scale_out[0] = scale_from_absmax(am, fmt);
+    }
+}
+
+__global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* __restrict__ scale) {
+    if (threadIdx.x == 0) scale[0] = scale_from_absmax(absmax[0], fmt);
+}
+
+// ---------------------------------------------------------------- quantize --
+// x / s with IEEE binary32 division (contract D1), then the fp8 encoder.
+template <int FMT>
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float s) {
+    return encode_fp8<FMT>(a / s) | (encode_fp8<FMT>(b / s) << 8) |
+           (encode_fp8<FMT>(c / s) << 16) | (encode_fp8<FMT>(d / s) << 24);
+}
+
+// fp32 -> fp8: one 16-byte load -> one 4-byte store per thread per step.
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __restrict__ x,
+                                                                 int64_t n,
+                                                                 const float* __restrict__ scale,
+                                                                 uint8_t* __restrict__ q) {
+    const float s = scale[0];
+    const int64_t nvec = n >> 2;
+    const f32x4* xv = reinterpret_cast<const f32x4*>(x);
+    uint32_t* qv = reinterpret_cast<uint32_t*>(q);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i + stride < nvec; i += 2 * stride) {
+        f32x4 v0 = __builtin_nontemporal_load(xv + i);
+        f32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
+        __builtin_nontemporal_store(quant4<FMT>(v0.x, v0.y, v0.z, v0.w, s), qv + i);
+        __builtin_nontemporal_store(quant4<FMT>(v1.x, v1.y, v1.z, v1.w, s), qv + i + stride);
+    }
+    for (; i < nvec; i += stride) {
+        f32x4 v = xv[i];
+        qv[i] = quant4<FMT>(v.x, v.y, v.z, v.w, s);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const int64_t j = (nvec << 2) + threadIdx.x;
+        q[j] = (uint8_t)encode_fp8<FMT>(x[j] / s);
+    }
+}
+
+// bf16 -> fp8: one 16-byte load (8 values) -> one 8-byte store.
+template <int FMT>
+__device__ __forceinline__ uint32_t quant_bf16x4(uint32_t w0, uint32_t w1, float s) {
+    return quant4<FMT>(bf16_to_f32(w0 & 0xFFFFu), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xFFFFu),
+                       bf16_to_f32(w1 >> 16), s);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t* __restrict__ x,
+                                                                  int64_t n,
+                                                                  const float* __restrict__ scale,
+                                                                  uint8_t* __restrict__ q) {
+    const float s = scale[0];
+    const int64_t nvec = n >> 3;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    u32x2* qv = reinterpret_cast<u32x2*>(q);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i + stride < nvec; i += 2 * stride) {
+        u32x4 v0 = __builtin_nontemporal_load(xv + i);
+        u32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
+        u32x2 o0, o1;
+        o0.x = quant_bf16x4<FMT>(v0.x, v0.y, s);
+        o0.y = quant_bf16x4<FMT>(v0.z, v0.w, s);
+        o1.x = quant_bf16x4<FMT>(v1.x, v1.y, s);
+        o1.y = quant_bf16x4<FMT>(v1.z, v1.w, s);
+        __builtin_nontemporal_store(o0, qv + i);
+        __builtin_nontemporal_store(o1, qv + i + stride);
+    }
+    for (; i < nvec; i += stride) {
+        u32x4 v = xv[i];
+        u32x2 o;
+        o.x = quant_bf16x4<FMT>(v.x, v.y, s);
+        o.y = quant_bf16x4<FMT>(v.z, v.w, s);
+        qv[i] = o;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
+        const int64_t j = (nvec << 3) + threadIdx.x;
+        q[j] = (uint8_t)encode_fp8<FMT>(bf16_to_f32(x[j]) / s);
+    }
+}
+
+// -------------------------------------------------------------- dequantize --
+// fp8 -> fp32: one 4-byte load (4 codes) -> one 16-byte store.
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void dequantize_f32_kernel(const uint8_t* __restrict__ q,
+                                                                   int64_t n,
+                                                                   const float* __restrict__ scale,
+                                                                   float* __restrict__ out) {
+    const float s = scale[0];
+    const int64_t nvec = n >> 2;
+    const uint32_t* qv = reinterpret_cast<const uint32_t*>(q);
+    f32x4* ov = reinterpret_cast<f32x4*>(out);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
+        const uint32_t w = __builtin_nontemporal_load(qv + i);
+        f32x4 o;
+        o.x = dequant_fp8<FMT>(w & 0xFFu, s);
+        o.y = dequant_fp8<FMT>((w >> 8) & 0xFFu, s);
+        o.z = dequant_fp8<FMT>((w >> 16) & 0xFFu, s);
+        o.w = dequant_fp8<FMT>(w >> 24, s);
+        __builtin_nontemporal_store(o, ov + i);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const int64_t j = (nvec << 2) + threadIdx.x;
+        out[j] = dequant_fp8<FMT>(q[j], s);
+    }
+}
+
+// fp8 -> bf16: one 8-byte load (8 codes) -> one 16-byte store.
+template <int FMT>
+__device__ __forceinline__ uint32_t deq_bf16x2(uint32_t c0, uint32_t c1, float s) {
+    return f32_to_bf16_rne(dequant_fp8<FMT>(c0, s)) | (f32_to_bf16_rne(dequant_fp8<FMT>(c1, s)) << 16);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t* __restrict__ q,
+                                                                    int64_t n,
+                                                                    const float* __restrict__ scale,
+                                                                    uint16_t* __restrict__ out) {
+    const float s = scale[0];
+    const int64_t nvec = n >> 3;
+    const u32x2* qv = reinterpret_cast<const u32x2*>(q);
+    u32x4* ov = reinterpret_cast<u32x4*>(out);
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
+        const u32x2 w = __builtin_nontemporal_load(qv + i);
+        u32x4 o;
+        o.x = deq_bf16x2<FMT>(w.x & 0xFFu, (w.x >> 8) & 0xFFu, s);
+        o.y = deq_bf16x2<FMT>((w.x >> 16) & 0xFFu, w.x >> 24, s);
+        o.z = deq_bf16x2<FMT>(w.y & 0xFFu, (w.y >> 8) & 0xFFu, s);
+        o.w = deq_bf16x2<FMT>((w.y >> 16) & 0xFFu, w.y >> 24, s);
+        __builtin_nontemporal_store(o, ov + i);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
+        const int64_t j = (nvec << 3) + threadIdx.x;
+        out[j] = (uint16_t)f32_to_bf16_rne(dequant_fp8<FMT>(q[j], s));
+    }
+}
+
+// ------------------------------------------------------- 2-D + transposed --
+// One 64x64 tile per block: 256 threads, thread t owns rows t/16 + 16*i
+// (i < 4) and the 4 columns starting at 4*(t%16).  Codes go straight to q
+// (4-byte stores) and through an LDS tile to qt (16-byte stores along the
+// transposed rows).  Out-of-range elements encode as 0 so the padding
+// columns of q and qt are written in the same pass.
+constexpr int kT2 = 64;
+
+template <typename InT>
+__device__ __forceinline__ float load_elem(const InT* x, int64_t idx);
+template <>
+__device__ __forceinline__ float load_elem<float>(const float* x, int64_t idx) { return x[idx]; }
+template <>
+__device__ __forceinline__ float load_elem<uint16_t>(const uint16_t* x, int64_t idx) {
+    return bf16_to_f32(x[idx]);
+}
+
+template <typename InT, int FMT>
+__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
+                                                                int cols, int ldx,
+                                                                const float* __restrict__ scale,
+                                                                uint8_t* __restrict__ q, int ldq,
+                                                                uint8_t* __restrict__ qt, int ldqt) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2][kT2 + 16];  // [col][row]
+    const float s = scale[0];
+    const int r0 = blockIdx.y * kT2, c0 = blockIdx.x * kT2;
+    const int tc = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tr = (threadIdx.x >> 4) + 16 * i;
+        const int r = r0 + tr, c = c0 + tc;
+        uint32_t packed = 0;
+        if (r < rows) {
+            const int64_t base = (int64_t)r * ldx + c;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (c + j < cols) packed |= encode_fp8<FMT>(load_elem<InT>(x, base + j) / s) << (8 * j);
+        }
+        if (q && r < rows && c < ldq) *reinterpret_cast<uint32_t*>(q + (int64_t)r * ldq + c) = packed;
+        if (qt) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tile[tc + j][tr] = (uint8_t)(packed >> (8 * j));
+        }
+    }
+    if (!qt) return;
+    __syncthreads();
+    const int tcol = threadIdx.x >> 2;          // transposed row = column of x
+    const int trow = (threadIdx.x & 3) * 16;    // 16 codes along rows of x
+    const int c = c0 + tcol, r = r0 + trow;
+    if (c < cols && r < ldqt)
+        *reinterpret_cast<uint4*>(qt + (int64_t)c * ldqt + r) =
+            *reinterpret_cast<const uint4*>(&tile[tcol][trow]);
+}
+
+// ------------------------------------------------------------------ colsum --
+// out[c] = sum_r x[r,c]: a block owns 64 columns; its 4 waves take every 4th
+// row (coalesced 64-column rows), then fold through LDS.
+template <typename InT>
+__global__ __launch_bounds__(kThreads) void colsum_kernel(const InT* __restrict__ x, int rows,
+                                                           int cols, int ldx,
+                                                           float* __restrict__ out) {
+    __shared__ float part[4][64];
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int w = threadIdx.x >> 6;
+    float acc = 0.0f;
+    if (c < cols)
+        for (int r = w; r < rows; r += 4) acc += load_elem<InT>(x, (int64_t)r * ldx + c);
+    part[w][threadIdx.x & 63] = acc;
+    __syncthreads();
+    if (w == 0 && c < cols)
+        out[c] = (part[0][threadIdx.x] + part[1][threadIdx.x]) + (part[2][threadIdx.x] + part[3][threadIdx.x]);
+}
+
+// --------------------------------------------------------------- launchers --
+static int grid_for(int64_t units, int64_t per_block_unit_cap) {
+    int64_t blocks = (units + kThreads - 1) / kThreads;
+    if (blocks > per_block_unit_cap) blocks = per_block_unit_cap;
+    return blocks < 1 ? 1 : (int)blocks;
+}
+
+}  // namespace dfk
+
+using namespace dfk;
+
+// Grid for streaming kernels: 256 CUs x 8 blocks, grid-stride beyond that.
+static constexpr int64_t kStreamBlocks = 2048;
+
+extern "C" size_t df_absmax_workspace_bytes(void) { return kMaxReduceBlocks * sizeof(uint32_t); }
+
+static int absmax_impl(int in_dtype, const void* x, int64_t n, int fmt, float* absmax_dev,
+                       float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    DF_CHECK(n >= 0, DF_ERR_INVALID, "absmax: n < 0");
+    DF_CHECK(x || n == 0, DF_ERR_INVALID, "absmax: x is NULL");
+    DF_CHECK(absmax_dev || scale_dev, DF_ERR_INVALID, "absmax: no output");
+    DF_CHECK(ws, DF_ERR_WORKSPACE, "absmax: workspace is NULL");
+    DF_CHECK(ws_bytes >= df_absmax_workspace_bytes(), DF_ERR_WORKSPACE,
+             "absmax: workspace %zu bytes < %zu", ws_bytes, df_absmax_workspace_bytes());
+    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "absmax: bad fp8 format %d", fmt);
+    DF_CHECK(aligned16(x) && aligned4(ws), DF_ERR_ALIGN, "absmax: x must be 16-byte aligned");
+    hipStream_t st = as_stream(stream);
+    uint32_t* part = static_cast<uint32_t*>(ws);
+    const int per = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 8;
+    int blocks = grid_for((n / per + 3) / 4, kMaxReduceBlocks);
+    if (in_dtype == DF_DTYPE_FLOAT32)
+        absmax_f32_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), n, part);
+    else if (in_dtype == DF_DTYPE_BFLOAT16)
+        absmax_bf16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
+    else
+        DF_CHECK(false, DF_ERR_UNSUPPORTED, "absmax: dtype %d not supported", in_dtype);
+    absmax_stage2<<<1, kThreads, 0, st>>>(part, blocks, fmt, absmax_dev, scale_dev);
+    return launch_status("absmax");
+}
+
+extern "C" int df_absmax_f32(const float* x, int64_t n, float* absmax_dev, void* ws,
+                             size_t ws_bytes, void* stream) {
+    DF_CHECK(absmax_dev, DF_ERR_INVALID, "df_absmax_f32: absmax_dev is NULL");
+    return absmax_impl(DF_DTYPE_FLOAT32, x, n, E4M3, absmax_dev, nullptr, ws, ws_bytes, stream);
+}
+extern "C" int df_absmax_bf16(const uint16_t* x, int64_t n, float* absmax_dev, void* ws,
+                              size_t ws_bytes, void* stream) {
+    DF_CHECK(absmax_dev, DF_ERR_INVALID, "df_absmax_bf16: absmax_dev is NULL");
+    return absmax_impl(DF_DTYPE_BFLOAT16, x, n, E4M3, absmax_dev, nullptr, ws, ws_bytes, stream);
+}
+extern "C" int df_absmax_scale_f32(const float* x, int64_t n, int fmt, float* absmax_dev,
+                                   float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
+    return absmax_impl(DF_DTYPE_FLOAT32, x, n, fmt, absmax_dev, scale_dev, ws, ws_bytes, stream);
+}
+extern "C" int df_absmax_scale_bf16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
+                                    float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
+    return absmax_impl(DF_DTYPE_BFLOAT16, x, n, fmt, absmax_dev, scale_dev, ws, ws_bytes, stream);
+}
+
+extern "C" int df_compute_scale(const float* absmax_dev, int fmt, float* scale_dev, void* stream) {
+    clear_error();
+    DF_CHECK(absmax_dev && scale_dev, DF_ERR_INVALID, "df_compute_scale: NULL pointer");
+    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "df_compute_scale: bad format %d", fmt);
+    scale_kernel<<<1, 64, 0, as_stream(stream)>>>(absmax_dev, fmt, scale_dev);
+    return launch_status("df_compute_scale");
+}
+
+template <int FMT>
+static int quantize_f32_impl(const float* x, int64_t n, const float* scale, uint8_t* q, void* stream,
+                             const char* name) {
+    clear_error();
+    DF_CHECK(n >= 0, DF_ERR_INVALID, "%s: n < 0", name);
+    if (n == 0) return DF_OK;
+    DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
+    DF_CHECK(aligned16(x) && aligned4(q), DF_ERR_ALIGN, "%s: x must be 16-byte and q 4-byte aligned", name);
+    const int blocks = grid_for(n / 4 + 1, kStreamBlocks);
+    quantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
+    return launch_status(name);
+}
+
+template <int FMT>
+static int quantize_bf16_impl(const uint16_t* x, int64_t n, const float* scale, uint8_t* q,
+                              void* stream, const char* name) {
+    clear_error();
+    DF_CHECK(n >= 0, DF_ERR_INVALID, "%s: n < 0", name);
+    if (n == 0) return DF_OK;
+    DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
+    DF_CHECK(aligned16(x) && (((uintptr_t)q & 7u) == 0), DF_ERR_ALIGN,
+             "%s: x must be 16-byte and q 8-byte aligned", name);
+    const int blocks = grid_for(n / 8 + 1, kStreamBlocks);
+    quantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
+    return launch_status(name);
+}
+
+extern "C" int df_quantize_f32_e4m3(const float* x, int64_t n, const float* s, uint8_t* q, void* st) {
+    return quantize_f32_impl<E4M3>(x, n, s, q, st, "df_quantize_f32_e4m3");
+}
+extern "C" int df_quantize_f32_e5m2(const float* x, int64_t n, const float* s, uint8_t* q, void* st) {
+    return quantize_f32_impl<E5M2>(x, n, s, q, st, "df_quantize_f32_e5m2");
+}
+extern "C" int df_quantize_bf16_e4m3(const uint16_t* x, int64_t n, const float* s, uint8_t* q, void* st) {
+    return quantize_bf16_impl<E4M3>(x, n, s, q, st, "df_quantize_bf16_e4m3");
+}
+extern "C" int df_quantize_bf16_e5m2(const uint16_t* x, int64_t n, const float* s, uint8_t* q, void* st) {
+    return quantize_bf16_impl<E5M2>(x, n, s, q, st, "df_quantize_bf16_e5m2");
+}
+
+template <int FMT>
+static int dequantize_f32_impl(const uint8_t* q, int64_t n, const float* scale, float* out,
+                               void* stream, const char* name) {
+    clear_error();
+    DF_CHECK(n >= 0, DF_ERR_INVALID, "%s: n < 0", name);
+    if (n == 0) return DF_OK;
+    DF_CHECK(q && scale && out, DF_ERR_INVALID, "%s: NULL pointer", name);
+    DF_CHECK(aligned4(q) && aligned16(out), DF_ERR_ALIGN, "%s: q must be 4-byte and out 16-byte aligned",
+             name);
+    const int blocks = grid_for(n / 4 + 1, kStreamBlocks);
+    dequantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
+    return launch_status(name);
+}
+
+template <int FMT>
+static int dequantize_bf16_impl(const uint8_t* q, int64_t n, const float* scale, uint16_t* out,
+                                void* stream, const char* name) {
+    clear_error();
+    DF_CHECK(n >= 0, DF_ERR_INVALID, "%s: n < 0", name);
+    if (n == 0) return DF_OK;
+    DF_CHECK(q && scale && out, DF_ERR_INVALID, "%s: NULL pointer", name);
+    DF_CHECK((((uintptr_t)q & 7u) == 0) && aligned16(out), DF_ERR_ALIGN,
+             "%s: q must be 8-byte and out 16-byte aligned", name);
+    const int blocks = grid_for(n / 8 + 1, kStreamBlocks);
+    dequantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
+    return launch_status(name);
+}
+
+extern "C" int df_dequantize_e4m3_f32(const uint8_t* q, int64_t n, const float* s, float* o, void* st) {
+    return dequantize_f32_impl<E4M3>(q, n, s, o, st, "df_dequantize_e4m3_f32");
+}
+extern "C" int df_dequantize_e5m2_f32(const uint8_t* q, int64_t n, const float* s, float* o, void* st) {
+    return dequantize_f32_impl<E5M2>(q, n, s, o, st, "df_dequantize_e5m2_f32");
+}
+extern "C" int df_dequantize_e4m3_bf16(const uint8_t* q, int64_t n, const float* s, uint16_t* o, void* st) {
+    return dequantize_bf16_impl<E4M3>(q, n, s, o, st, "df_dequantize_e4m3_bf16");
+}
+extern "C" int df_dequantize_e5m2_bf16(const uint8_t* q, int64_t n, const float* s, uint16_t* o, void* st) {
+    return dequantize_bf16_impl<E5M2>(q, n, s, o, st, "df_dequantize_e5m2_bf16");
+}
+
+extern "C" int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                              const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
+                              void* stream) {
+    clear_error();
+    DF_CHECK(rows >= 0 && cols >= 0 && ldx >= cols, DF_ERR_INVALID,
+             "df_quantize_2d: bad shape rows=%d cols=%d ldx=%d", rows, cols, ldx);
+    DF_CHECK(q || qt, DF_ERR_INVALID, "df_quantize_2d: no output");
+    DF_CHECK(scale_dev && (x || rows * (int64_t)cols == 0), DF_ERR_INVALID, "df_quantize_2d: NULL pointer");
+    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "df_quantize_2d: bad format %d", fmt);
+    DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
+             "df_quantize_2d: dtype %d not supported", in_dtype);
+    if (q) {
+        DF_CHECK(ldq >= cols && ldq % 16 == 0, DF_ERR_ALIGN, "df_quantize_2d: ldq=%d must be >= cols and a multiple of 16", ldq);
+        DF_CHECK(aligned16(q), DF_ERR_ALIGN, "df_quantize_2d: q must be 16-byte aligned");
+    }
+    if (qt) {
+        DF_CHECK(ldqt >= rows && ldqt % 16 == 0, DF_ERR_ALIGN, "df_quantize_2d: ldqt=%d must be >= rows and a multiple of 16", ldqt);
+        DF_CHECK(aligned16(qt), DF_ERR_ALIGN, "df_quantize_2d: qt must be 16-byte aligned");
+    }
+    const int row_ext = qt ? (rows > ldqt ? rows : ldqt) : rows;
+    const int col_ext = q ? (cols > ldq ? cols : ldq) : cols;
+    if (row_ext == 0 || col_ext == 0) return DF_OK;
+    dim3 grid((col_ext + kT2 - 1) / kT2, (row_ext + kT2 - 1) / kT2);
+    hipStream_t st = as_stream(stream);
+    if (in_dtype == DF_DTYPE_FLOAT32) {
+        auto* xp = static_cast<const float*>(x);
+        if (fmt == E4M3) quantize_2d_kernel<float, E4M3><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
+        else quantize_2d_kernel<float, E5M2><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
+    } else {
+        auto* xp = static_cast<const uint16_t*>(x);
+        if (fmt == E4M3) quantize_2d_kernel<uint16_t, E4M3><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
+        else quantize_2d_kernel<uint16_t, E5M2><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
+    }
+    return launch_status("df_quantize_2d");
+}
+
+extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx, float* out,
+                         void* stream) {
+    clear_error();
+    DF_CHECK(rows >= 0 && cols >= 0 && ldx >= cols, DF_ERR_INVALID, "df_colsum: bad shape");
+    if (cols == 0) return DF_OK;
+    DF_CHECK(out && (x || rows == 0), DF_ERR_INVALID, "df_colsum: NULL pointer");
+    hipStream_t st = as_stream(stream);
+    const int blocks = (cols + 63) / 64;
+    if (in_dtype == DF_DTYPE_FLOAT32)
+        colsum_kernel<float><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), rows, cols, ldx, out);
+    else if (in_dtype == DF_DTYPE_BFLOAT16)
+        colsum_kernel<uint16_t><<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), rows, cols, ldx, out);
+    else
+        DF_CHECK(false, DF_ERR_UNSUPPORTED, "df_colsum: dtype %d not supported", in_dtype);
+    return launch_status("df_colsum");
+}

@@ -1,0 +1,178 @@
+/*
+ * df_capi.h -- C ABI of the MI355X-native fp8 Linear path (libdeepfuse_amd.so).
+ *
+ * The reference (SensorVista/DeepFuse) has no C ABI: its host code calls
+ * CUDA kernels directly from C++ (dnn/layers/fully_connected_layer.cu:164-357,
+ * dnn/core/tensor.cu:77-462).  Each entry point below names the reference
+ * function or kernel it replaces.  The C++ drop-in API (deepfuse_amd/dnn/...,
+ * namespace dnn) calls only these entry points for device work.
+ *
+ * Conventions
+ *  - Pointers named *_dev, x, q, out, A, B, C, ws are DEVICE pointers.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Every call only enqueues work; nothing synchronises the host.
+ *  - Return value: DF_OK (0) or a negative df_status.  Nothing throws across
+ *    the ABI.  df_last_error_string() gives the calling thread's last message.
+ *  - Element counts are int64_t; matrix dimensions are int (the reference's
+ *    tensor uses int shapes, dnn/core/tensor.cuh:26-28).
+ *  - Calls on different streams are independent and thread-safe; a workspace
+ *    or output buffer must not be shared by calls that may overlap.
+ *  - Per-tensor scale (contract D1/D2): s = absmax / FMAX with FMAX = 448
+ *    (e4m3) or 57344 (e5m2); absmax is over finite values; absmax == 0 gives
+ *    s = 1.  Quantize: q = sat_rne(x / s) (IEEE binary32 division, then
+ *    round-to-nearest-even into OCP fp8, saturating; NaN -> sign|0x7F,
+ *    +-inf -> +-max).  Dequantize: decode(q) * s in binary32; bf16 output is
+ *    the RNE rounding of that binary32; NaN codes give the canonical quiet NaN.
+ */
+#ifndef DF_CAPI_H
+#define DF_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+typedef enum {
+    DF_OK = 0,
+    DF_ERR_INVALID = -1,     /* null pointer, negative or inconsistent size */
+    DF_ERR_UNSUPPORTED = -2, /* dtype / format combination not provided */
+    DF_ERR_HIP = -3,         /* HIP runtime reported an error */
+    DF_ERR_ALIGN = -4,       /* pointer or leading dimension misaligned */
+    DF_ERR_WORKSPACE = -5    /* workspace too small */
+} df_status;
+
+/* ---- fp8 formats (OCP OFP8 v1.0) ---- */
+typedef enum { DF_FMT_E4M3 = 0, DF_FMT_E5M2 = 1 } df_fp8_format;
+
+/* ---- element types: values 0-4 are the reference's own enum
+ * OnnxLoader::DType (dnn/utils/onnx_loader.cuh:16-22); 5 and 6 extend it
+ * with the two 1-byte fp8 formats; 7 is int32 (the reference's tensor<int>,
+ * dnn/core/tensor.cu:486). ---- */
+typedef enum {
+    DF_DTYPE_FLOAT32 = 0,
+    DF_DTYPE_HALF = 1,
+    DF_DTYPE_INT8 = 2,
+    DF_DTYPE_UINT8 = 3,
+    DF_DTYPE_BFLOAT16 = 4,
+    DF_DTYPE_FP8E4M3 = 5,
+    DF_DTYPE_FP8E5M2 = 6,
+    DF_DTYPE_INT32 = 7
+} df_dtype;
+
+/* ---- library ---- */
+const char* df_last_error_string(void);   /* thread-local, never NULL */
+int df_version(void);                     /* 100 * major + minor */
+int df_device_arch_ok(void);              /* 1 when the current device is gfx950 */
+
+/* ---- absmax / scale (new: the reference has no quantizer, README.md:16) ----
+ * Two-stage reduction: a grid pass writes per-block maxima into `ws`, a
+ * single-block pass folds them and writes absmax and the scale.  `ws` must
+ * hold df_absmax_workspace_bytes() bytes. */
+size_t df_absmax_workspace_bytes(void);
+int df_absmax_f32(const float* x, int64_t n, float* absmax_dev,
+                  void* ws, size_t ws_bytes, void* stream);
+int df_absmax_bf16(const uint16_t* x, int64_t n, float* absmax_dev,
+                   void* ws, size_t ws_bytes, void* stream);
+/* absmax and the scale for `fmt` in one call (scale_dev may equal NULL). */
+int df_absmax_scale_f32(const float* x, int64_t n, int fmt, float* absmax_dev,
+                        float* scale_dev, void* ws, size_t ws_bytes, void* stream);
+int df_absmax_scale_bf16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
+                         float* scale_dev, void* ws, size_t ws_bytes, void* stream);
+/* scale from an absmax already on the device */
+int df_compute_scale(const float* absmax_dev, int fmt, float* scale_dev, void* stream);
+
+/* ---- quantize (new; element type of the reference's fp8 instantiations,
+ * dnn/core/tensor.cu:489-498, made 1 byte per value) ----
+ * x and q must be 16-byte aligned for the vector path; any n >= 0. */
+int df_quantize_f32_e4m3(const float* x, int64_t n, const float* scale_dev,
+                         uint8_t* q, void* stream);
+int df_quantize_f32_e5m2(const float* x, int64_t n, const float* scale_dev,
+                         uint8_t* q, void* stream);
+int df_quantize_bf16_e4m3(const uint16_t* x, int64_t n, const float* scale_dev,
+                          uint8_t* q, void* stream);
+int df_quantize_bf16_e5m2(const uint16_t* x, int64_t n, const float* scale_dev,
+                          uint8_t* q, void* stream);
+
+/* ---- dequantize (new) ---- */
+int df_dequantize_e4m3_f32(const uint8_t* q, int64_t n, const float* scale_dev,
+                           float* out, void* stream);
+int df_dequantize_e5m2_f32(const uint8_t* q, int64_t n, const float* scale_dev,
+                           float* out, void* stream);
+int df_dequantize_e4m3_bf16(const uint8_t* q, int64_t n, const float* scale_dev,
+                            uint16_t* out, void* stream);
+int df_dequantize_e5m2_bf16(const uint8_t* q, int64_t n, const float* scale_dev,
+                            uint16_t* out, void* stream);
+
+/* ---- 2-D quantize into GEMM operand layout (new) ----
+ * x: row-major [rows, cols] with leading dimension ldx (elements), dtype
+ * DF_DTYPE_FLOAT32 or DF_DTYPE_BFLOAT16.  Writes, when non-NULL:
+ *   q  [rows, ldq]  : q[r*ldq + c] = code(x[r,c]); columns [cols, ldq) = 0
+ *   qt [cols, ldqt] : qt[c*ldqt + r] = code(x[r,c]); columns [rows, ldqt) = 0
+ * ldq and ldqt must be multiples of 16 (the GEMM's K granule).  qt is the
+ * transposed copy the backward GEMMs read (dX needs W^T, dW needs dY^T and
+ * X^T), produced in the same pass as q. */
+int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx,
+                   int fmt, const float* scale_dev, uint8_t* q, int ldq,
+                   uint8_t* qt, int ldqt, void* stream);
+
+/* ---- column sums (replaces fc_backward_bias,
+ * dnn/layers/fully_connected_layer.cu:91-106) ----
+ * out[c] = sum_r x[r, c] in fp32 (tree order, not the reference's
+ * sequential order); overwrites out. */
+int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
+              float* out, void* stream);
+
+/* ---- fp8 GEMM, "NT": C[m,n] = (sum_k A[m,k] * B[n,k]) * sa * sb + bias[n]
+ *   A [M, lda] fp8 (fmt_a), B [N, ldb] fp8 (fmt_b), both row-major with the
+ *   reduction dimension contiguous; lda, ldb multiples of 16 and >= K;
+ *   A, B 16-byte aligned; sa, sb device scalars; bias NULL or [N] of
+ *   bias_dtype (FLOAT32 or BFLOAT16); C [M, ldc] of c_dtype (FLOAT32 or
+ *   BFLOAT16), overwritten.  fp32 accumulation on CDNA4 fp8 MFMA.
+ *   When K is not a multiple of 16, columns [K, roundup(K,16)) of A and B
+ *   must hold zero codes (df_quantize_2d writes its padding that way).
+ * Replaces fully_connected_forward_kernel (fully_connected_layer.cu:14-41). */
+int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda,
+                   int fmt_b, const uint8_t* B, int ldb,
+                   int M, int N, int K,
+                   const float* scale_a_dev, const float* scale_b_dev,
+                   int bias_dtype, const void* bias,
+                   int c_dtype, void* C, int ldc, void* stream);
+
+/* Forward: Y[M,N] = X_q[M,K] . W_q[N,K]^T * sx * sw + b  (e4m3 x e4m3).
+ * Replaces fully_connected_forward_kernel (fully_connected_layer.cu:14-41). */
+int df_fp8_gemm_fwd(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw,
+                    int M, int N, int K, const float* sx_dev, const float* sw_dev,
+                    int bias_dtype, const void* bias, int y_dtype, void* Y, int ldy,
+                    void* stream);
+/* dX[M,K] = dY_q[M,N] . W[N,K]  (e5m2 x e4m3), given W^T quantized as
+ * Wt_q[K, ldwt] (df_quantize_2d's qt).  Replaces fc_backward_input
+ * (fully_connected_layer.cu:43-65). */
+int df_fp8_gemm_bwd_dx(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
+                       int M, int N, int K, const float* sdy_dev, const float* sw_dev,
+                       int dx_dtype, void* dX, int lddx, void* stream);
+/* dW[N,K] = dY^T . X, given dY^T quantized as dYt_q[N, ldyt] (e5m2) and X^T
+ * as Xt_q[K, ldxt] (e4m3); M tokens is the reduction.  Overwrites dW, like
+ * fc_backward_weights (fully_connected_layer.cu:67-89, :85-87). */
+int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ldxt,
+                       int M, int N, int K, const float* sdy_dev, const float* sx_dev,
+                       int dw_dtype, void* dW, int lddw, void* stream);
+
+/* ---- tensor utilities behind dnn::tensor (dnn/core/tensor.cu:18-52) ---- */
+/* fill_kernel (tensor.cu:19): n elements of elem_bytes (1, 2 or 4) = *value */
+int df_fill(void* dst, int64_t n, int elem_bytes, const void* value_host, void* stream);
+/* add_kernel / add_inplace_kernel (tensor.cu:27-36): out = a + b (out may be a) */
+int df_add(int dtype, const void* a, const void* b, void* out, int64_t n, void* stream);
+/* equal_kernel (tensor.cu:39): mask[i] = bitwise a[i] == b[i] (per element) */
+int df_equal_mask(int dtype, const void* a, const void* b, uint8_t* mask, int64_t n,
+                  void* stream);
+/* approx_equal_kernel (tensor.cu:46): mask[i] = |a[i]-b[i]| <= atol, in fp32 */
+int df_approx_equal_mask(int dtype, const void* a, const void* b, uint8_t* mask,
+                         int64_t n, float atol, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,192 @@
+"""GPU parity of the fp8 Linear GEMMs (forward, dX, dW) and db.
+
+Bar (contract D6): the GPU output is within
+normwise relative error 1e-4 (max|y - r| / max|r|) of the reference's
+fp32-accumulated product of the same dequantized operands, computed by the
+oracle's restatement of dnn/layers/fully_connected_layer.cu:14-106.  Codes
+feeding the GEMM are first checked bit-exact.  bf16 outputs are checked to
+be the round-to-nearest-even image of the fp32 result of the same kernel.
+At full configuration sizes the oracle runs on a seeded sample of rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+import deepfuse_amd as df
+from deepfuse_amd import Fmt, synth
+from oracle import pyoracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def dev_f32(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
+
+
+def quant_operand(x, fmt, dev, want_q=True, want_qt=False):
+    """GPU absmax/scale/2-D quantize of a host fp32 matrix; returns the
+    device codes plus the oracle's scale and dequantized matrix (after
+    checking the GPU codes and scale bit-exact)."""
+    xd = dev_f32(x, dev)
+    am, sc = df.absmax_scale(xd, fmt)
+    q, qt = df.quantize_2d(xd, sc, fmt, want_q=want_q, want_qt=want_qt)
+    s = orc.scale(orc.absmax(x), int(fmt))
+    assert sc.cpu().numpy().view(np.uint32)[0] == np.float32(s).view(np.uint32)
+    codes = orc.quantize(x, s, int(fmt))
+    rows, cols = x.shape
+    if q is not None:
+        assert np.array_equal(q.cpu().numpy()[:, :cols], codes)
+    if qt is not None:
+        assert np.array_equal(qt.cpu().numpy()[:, :rows], np.ascontiguousarray(codes.T))
+    deq = orc.dequantize(codes, s, int(fmt), "f32")
+    return q, qt, sc, deq
+
+
+def check_bf16_image(c32, c16):
+    exp = synth.f32_to_bf16_bits(c32.cpu().numpy())
+    got = c16.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, exp)
+
+
+def forward_case(dev, M, K, N, seed, bias=True, rows=None):
+    X = synth.normal((M, K), 1.0, seed=seed)
+    W = synth.normal((N, K), 0.02, seed=seed + 1)
+    b = synth.normal((N,), 0.1, seed=seed + 2) if bias else None
+    xq, _, sx, Xd = quant_operand(X, Fmt.E4M3, dev)
+    wq, _, sw, Wd = quant_operand(W, Fmt.E4M3, dev)
+    bd = dev_f32(b, dev) if bias else None
+    Y = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd)
+    Yh = Y.cpu().numpy()
+    idx = np.arange(M) if rows is None else np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+    ref = orc.fc_forward(Xd[idx], Wd, b)
+    err = orc.rel_err(Yh[idx], ref)
+    assert err <= TOL, f"forward M={M} K={K} N={N}: rel err {err:.3e}"
+    Y16 = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd, out_dtype=torch.bfloat16)
+    check_bf16_image(Y, Y16)
+    return err
+
+
+def test_reference_known_answer(dev):
+    """fully_connected_layer_test.cu:266-284: W={1,2,3,4}, b={.5,-.5}, x={1,2}."""
+    X = np.array([[1, 2]], np.float32)
+    W = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([0.5, -0.5], np.float32)
+    xq, _, sx, Xd = quant_operand(X, Fmt.E4M3, dev)
+    wq, _, sw, Wd = quant_operand(W, Fmt.E4M3, dev)
+    Y = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, 2, sx, sw, bias=dev_f32(b, dev)).cpu().numpy()
+    ref = orc.fc_forward(Xd, Wd, b)
+    assert orc.rel_err(Y, ref) <= TOL
+    assert np.all(Y != 0.0)  # NonzeroInputGivesNonzeroOutput
+    # fp8 e4m3 rounds W[1,0] = 3 -> 336 (tie) -> 320: y1 = 20/7 + 8 - 0.5
+    np.testing.assert_allclose(Y[0], [5.5, 20.0 / 7.0 + 7.5], rtol=1e-6)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4, 3), (1, 5, 2), (3, 7, 5), (64, 768, 3072), (100, 40, 50),
+                                   (129, 272, 257), (256, 128, 128), (17, 1600, 33)])
+def test_forward_shapes(dev, M, K, N):
+    forward_case(dev, M, K, N, seed=M * 7 + K * 3 + N)
+
+
+def test_forward_no_bias(dev):
+    forward_case(dev, 70, 96, 130, seed=5, bias=False)
+
+
+def backward_case(dev, M, K, N, seed, rows=None, wrows=None, wcols=None):
+    """dX = dY . W (e5m2 x e4m3) and dW = dY^T . X; db = column sums of dY."""
+    X = synth.normal((M, K), 1.0, seed=seed)
+    W = synth.normal((N, K), 0.02, seed=seed + 1)
+    dY = synth.normal((M, N), 1e-3, seed=seed + 2)
+    _, xt, sx, Xd = quant_operand(X, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    _, wt, sw, Wd = quant_operand(W, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    dyq, dyt, sdy, dYd = quant_operand(dY, Fmt.E5M2, dev, want_q=True, want_qt=True)
+    # dX[M,K]: A = dY [M, N], B = W^T [K, N]
+    dX = df.gemm_nt(dyq, Fmt.E5M2, wt, Fmt.E4M3, N, sdy, sw).cpu().numpy()
+    idx = np.arange(M) if rows is None else np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+    ref = orc.fc_backward_input(dYd[idx], Wd)
+    err = orc.rel_err(dX[idx], ref)
+    assert err <= TOL, f"dX M={M} K={K} N={N}: {err:.3e}"
+    # dW[N,K]: A = dY^T [N, M], B = X^T [K, M]
+    dW = df.gemm_nt(dyt, Fmt.E5M2, xt, Fmt.E4M3, M, sdy, sx).cpu().numpy()
+    o_idx = np.arange(N) if wrows is None else np.sort(np.random.default_rng(seed + 9).choice(N, wrows, replace=False))
+    i_idx = np.arange(K) if wcols is None else np.sort(np.random.default_rng(seed + 8).choice(K, wcols, replace=False))
+    refw = orc.fc_backward_weights(np.ascontiguousarray(dYd[:, o_idx]), np.ascontiguousarray(Xd[:, i_idx]))
+    errw = orc.rel_err(dW[np.ix_(o_idx, i_idx)], refw)
+    assert errw <= TOL, f"dW M={M} K={K} N={N}: {errw:.3e}"
+    # db from the fp32 upstream gradient (fc_backward_bias, :91-106)
+    db = df.colsum(dev_f32(dY, dev)).cpu().numpy()
+    assert orc.rel_err(db, orc.fc_backward_bias(dY)) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4, 3), (1, 5, 2), (64, 768, 3072), (100, 40, 50), (129, 272, 257),
+                                   (512, 1600, 64)])
+def test_backward_shapes(dev, M, K, N):
+    backward_case(dev, M, K, N, seed=M * 11 + K + N * 5)
+
+
+def test_backward_entry_points_match_nt(dev):
+    """df_fp8_gemm_bwd_dx / _bwd_dw are the NT kernel with the documented
+    operand roles: their outputs equal the direct NT calls bit for bit."""
+    M, K, N = 192, 160, 96
+    X = synth.normal((M, K), 1.0, seed=1)
+    W = synth.normal((N, K), 0.02, seed=2)
+    dY = synth.normal((M, N), 1e-3, seed=3)
+    _, xt, sx, _ = quant_operand(X, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    _, wt, sw, _ = quant_operand(W, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    dyq, dyt, sdy, _ = quant_operand(dY, Fmt.E5M2, dev, want_q=True, want_qt=True)
+    dX_nt = df.gemm_nt(dyq, Fmt.E5M2, wt, Fmt.E4M3, N, sdy, sw)
+    dW_nt = df.gemm_nt(dyt, Fmt.E5M2, xt, Fmt.E4M3, M, sdy, sx)
+    dX = torch.empty((M, K), dtype=torch.float32, device=dev)
+    dW = torch.empty((N, K), dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    df.call("df_fp8_gemm_bwd_dx", dyq.data_ptr(), dyq.stride(0), wt.data_ptr(), wt.stride(0), M, N, K,
+            sdy.data_ptr(), sw.data_ptr(), int(df.DType.FLOAT32), dX.data_ptr(), K, st)
+    df.call("df_fp8_gemm_bwd_dw", dyt.data_ptr(), dyt.stride(0), xt.data_ptr(), xt.stride(0), M, N, K,
+            sdy.data_ptr(), sx.data_ptr(), int(df.DType.FLOAT32), dW.data_ptr(), K, st)
+    assert torch.equal(dX, dX_nt)
+    assert torch.equal(dW, dW_nt)
+
+
+GPT2_SMALL = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+GPT2_XL = [(1600, 4800), (1600, 1600), (1600, 6400), (6400, 1600)]
+
+
+@pytest.mark.parametrize("K,N", GPT2_SMALL)
+def test_config3_forward_bf16(dev, K, N):
+    """Config 3: M = 8192 tokens, bf16 activations and weights quantized to
+    e4m3, bf16 output with fused bias; oracle on 48 sampled rows."""
+    M = 8192
+    seed = synth.SEED_BASE + 3 + K + N
+    Xb = synth.f32_to_bf16_bits(synth.normal((M, K), 1.0, seed=seed))
+    Wb = synth.f32_to_bf16_bits(synth.normal((N, K), 0.02, seed=seed + 1))
+    bb = synth.f32_to_bf16_bits(synth.normal((N,), 0.1, seed=seed + 2))
+    tob = lambda a: torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
+    Xd, Wd, bd = tob(Xb), tob(Wb), tob(bb)
+    _, sx = df.absmax_scale(Xd, Fmt.E4M3)
+    _, sw = df.absmax_scale(Wd, Fmt.E4M3)
+    xq, _ = df.quantize_2d(Xd, sx, Fmt.E4M3)
+    wq, _ = df.quantize_2d(Wd, sw, Fmt.E4M3)
+    Y32 = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd)
+    Y16 = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd, out_dtype=torch.bfloat16)
+    check_bf16_image(Y32, Y16)
+    s_x = orc.scale(orc.absmax(Xb), 0)
+    s_w = orc.scale(orc.absmax(Wb), 0)
+    assert sx.item() == np.float32(s_x) and sw.item() == np.float32(s_w)
+    idx = np.sort(np.random.default_rng(seed).choice(M, 48, replace=False))
+    cx = orc.quantize(Xb[idx], s_x, 0)
+    assert np.array_equal(xq.cpu().numpy()[idx][:, :K], cx)
+    cw = orc.quantize(Wb, s_w, 0)
+    assert np.array_equal(wq.cpu().numpy()[:, :K], cw)
+    ref = orc.fc_forward(orc.dequantize(cx, s_x, 0), orc.dequantize(cw, s_w, 0), orc.bf16_to_f32(bb))
+    err = orc.rel_err(Y32.cpu().numpy()[idx], ref)
+    assert err <= TOL, f"config3 {K}->{N}: {err:.3e}"
+
+
+@pytest.mark.parametrize("K,N", GPT2_XL)
+def test_config4_forward_backward(dev, K, N):
+    """Config 4: M = 16384 tokens, forward e4m3 x e4m3, backward dY ~
+    N(0, 1e-3) as e5m2; oracle on sampled rows of Y / dX and of dW."""
+    M = 16384
+    backward_case(dev, M, K, N, seed=synth.SEED_BASE + 4 + K + N, rows=24, wrows=8, wcols=64)
+    forward_case(dev, M, K, N, seed=synth.SEED_BASE + 40 + K + N, rows=24)
