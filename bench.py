@@ -1,0 +1,324 @@
+#!/usr/bin/env python3
+"""bench.py -- fp8 Linear path on one MI355X (BASELINE.json metric).
+
+Workload ("config 4"): the four GPT-2 XL Linears
+(d = 1600: qkv 1600->4800, attn proj 1600->1600, fc 1600->6400, proj
+6400->1600) at M = 16384 tokens, forward and backward, on seeded synthetic
+bf16 tensors already resident in HBM.  One step, per Linear:
+  forward : absmax + quantize X -> e4m3 (row copy and transposed copy),
+            absmax + quantize W -> e4m3 (both copies),
+            Y = Xq . Wq^T * sx * sw + b            (bf16 out, fused bias)
+  backward: absmax + quantize dY -> e5m2 (both copies), db = column sums,
+            dX = dYq . W * sdy * sw                  (bf16 out)
+            dW = dYq^T . X * sdy * sx                (fp32 out, overwrite)
+value = GEMM flops of the step (2*M*N*K per GEMM, 12 GEMMs) / step time.
+
+Also reported on the same JSON line:
+  roofline     -- the dominant kernel (largest summed time) against fp8 MFMA
+                  peak; durations from HIP events around every launch on the
+                  stream the kernels run on.
+  quantize     -- the step's absmax/quantize/colsum kernels against HBM peak.
+  conversion   -- config 2 standalone kernels (n = 2^28, fp32 and bf16 in,
+                  e4m3 and e5m2) against HBM peak.
+  cpu_baseline -- the oracle's restatement of the reference's FC loops
+                  (dnn/layers/fully_connected_layer.cu:29-35,54-59,78-83) on a
+                  token slice of the same workload, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+M_TOKENS = 16384
+XL_LINEARS = [("qkv", 1600, 4800), ("attn_proj", 1600, 1600), ("fc", 1600, 6400), ("proj", 6400, 1600)]
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-conversion", action="store_true")
+    p.add_argument("--cpu-tokens", type=int, default=3072, help="token slice for the CPU baseline")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events around launches on the current stream, grouped by name."""
+
+    def __init__(self, torch, enabled=True):
+        self.torch = torch
+        self.enabled = enabled
+        self.pending = []
+
+    def run(self, name, fn, *a, **k):
+        t = self.torch
+        if not self.enabled:
+            return fn(*a, **k)
+        e0 = t.cuda.Event(enable_timing=True)
+        e1 = t.cuda.Event(enable_timing=True)
+        e0.record()
+        r = fn(*a, **k)
+        e1.record()
+        self.pending.append((name, e0, e1))
+        return r
+
+    def collect(self):
+        self.torch.cuda.synchronize()
+        out = {}
+        for name, e0, e1 in self.pending:
+            ms = e0.elapsed_time(e1)
+            tot, cnt = out.get(name, (0.0, 0))
+            out[name] = (tot + ms, cnt + 1)
+        self.pending = []
+        return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the path's multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import deepfuse_amd as df
+    from deepfuse_amd import DType, Fmt, synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = df.lib()
+    if L.df_device_arch_ok() != 1:
+        raise RuntimeError("device is not gfx950")
+    stream = torch.cuda.current_stream().cuda_stream
+    M = M_TOKENS
+
+    def to_bf16(a):
+        return torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+    ws = torch.empty(L.df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
+    layers = []
+    for i, (name, K, N) in enumerate(XL_LINEARS):
+        seed = synth.SEED_BASE + 4 + 10 * i
+        Kp, Mp, Np = df.round16(K), df.round16(M), df.round16(N)
+        lay = dict(name=name, K=K, N=N,
+                   X=to_bf16(synth.normal((M, K), 1.0, seed=seed)),
+                   W=to_bf16(synth.normal((N, K), 0.02, seed=seed + 1)),
+                   b=to_bf16(synth.normal((N,), 0.02, seed=seed + 2)),
+                   dY=to_bf16(synth.normal((M, N), 1e-3, seed=seed + 3)),
+                   Xq=torch.empty((M, Kp), dtype=torch.uint8, device=dev),
+                   Xt=torch.empty((K, Mp), dtype=torch.uint8, device=dev),
+                   Wq=torch.empty((N, Kp), dtype=torch.uint8, device=dev),
+                   Wt=torch.empty((K, Np), dtype=torch.uint8, device=dev),
+                   dYq=torch.empty((M, Np), dtype=torch.uint8, device=dev),
+                   dYt=torch.empty((N, Mp), dtype=torch.uint8, device=dev),
+                   Y=torch.empty((M, N), dtype=torch.bfloat16, device=dev),
+                   dX=torch.empty((M, K), dtype=torch.bfloat16, device=dev),
+                   dW=torch.empty((N, K), dtype=torch.float32, device=dev),
+                   db=torch.empty((N,), dtype=torch.float32, device=dev),
+                   sc=torch.empty(6, dtype=torch.float32, device=dev))
+        layers.append(lay)
+    torch.cuda.synchronize()
+
+    BF, F32 = int(DType.BFLOAT16), int(DType.FLOAT32)
+    E4, E5 = int(Fmt.E4M3), int(Fmt.E5M2)
+
+    def quant(tm, x, rows, cols, fmt, am, sc, q, qt, tag):
+        tm.run("absmax_" + tag, df.call, "df_absmax_scale_bf16", x.data_ptr(), x.numel(), fmt, am, sc,
+               ws.data_ptr(), ws.numel(), stream)
+        tm.run("quantize2d_" + tag, df.call, "df_quantize_2d", BF, x.data_ptr(), rows, cols, cols, fmt, sc,
+               q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), stream)
+
+    def step(tm):
+        for l in layers:
+            K, N = l["K"], l["N"]
+            s = l["sc"].data_ptr()
+            sx_am, sx, sw_am, sw, sdy_am, sdy = (s + 4 * j for j in range(6))
+            quant(tm, l["X"], M, K, E4, sx_am, sx, l["Xq"], l["Xt"], "act")
+            quant(tm, l["W"], N, K, E4, sw_am, sw, l["Wq"], l["Wt"], "weight")
+            tm.run("gemm_fwd", df.call, "df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["Xq"].stride(0),
+                   l["Wq"].data_ptr(), l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF,
+                   l["Y"].data_ptr(), N, stream)
+            quant(tm, l["dY"], M, N, E5, sdy_am, sdy, l["dYq"], l["dYt"], "grad")
+            tm.run("colsum_db", df.call, "df_colsum", BF, l["dY"].data_ptr(), M, N, N, l["db"].data_ptr(), stream)
+            tm.run("gemm_dx", df.call, "df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0),
+                   l["Wt"].data_ptr(), l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K, stream)
+            tm.run("gemm_dw", df.call, "df_fp8_gemm_bwd_dw", l["dYt"].data_ptr(), l["dYt"].stride(0),
+                   l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K, stream)
+
+    # algorithmic work per step (unpadded shapes; BASELINE.md counting rules)
+    gemm_flops = {"gemm_fwd": 0, "gemm_dx": 0, "gemm_dw": 0}
+    qbytes = {}
+    for (_, K, N) in XL_LINEARS:
+        f = 2 * M * N * K
+        for k in gemm_flops:
+            gemm_flops[k] += f
+        for tag, r, c in (("act", M, K), ("weight", N, K), ("grad", M, N)):
+            qbytes["absmax_" + tag] = qbytes.get("absmax_" + tag, 0) + 2 * r * c
+            qbytes["quantize2d_" + tag] = qbytes.get("quantize2d_" + tag, 0) + 2 * r * c + 2 * r * c
+        qbytes["colsum_db"] = qbytes.get("colsum_db", 0) + 2 * M * N + 4 * N
+    step_flops = sum(gemm_flops.values())
+
+    null = Timer(torch, enabled=False)
+    for _ in range(args.warmup):
+        step(null)
+    torch.cuda.synchronize()
+
+    tm = Timer(torch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(tm)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    per = tm.collect()
+    ms_per_step = 1e3 * elapsed / args.steps
+    value = step_flops / (elapsed / args.steps) / 1e12
+
+    # dominant kernel = largest summed time; GEMM families are one kernel
+    # template each (fwd: e4m3 x e4m3 -> bf16 + bias; dx: e5m2 x e4m3 -> bf16;
+    # dw: e5m2 x e4m3 -> fp32).
+    dom = max(per, key=lambda k: per[k][0])
+    tot_ms, cnt = per[dom]
+    avg_ms = tot_ms / cnt
+    if dom in gemm_flops:
+        work_per_launch = gemm_flops[dom] * args.steps / cnt
+        achieved = work_per_launch / (avg_ms * 1e-3) / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": FP8_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4), "traffic": None,
+                "avg_launch_ms": round(avg_ms, 4), "work_per_launch": work_per_launch}
+    else:
+        work_per_launch = qbytes[dom] * args.steps / cnt
+        achieved = work_per_launch / (avg_ms * 1e-3) / 1e9
+        roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "avg_launch_ms": round(avg_ms, 4), "work_per_launch": work_per_launch}
+    kernels = {}
+    for k, (t, c) in sorted(per.items()):
+        d = {"ms_per_step": round(t / args.steps, 4), "launches_per_step": c // args.steps}
+        if k in gemm_flops:
+            d["tflops"] = round(gemm_flops[k] / (t / args.steps * 1e-3) / 1e12, 1)
+        else:
+            d["gbs"] = round(qbytes[k] / (t / args.steps * 1e-3) / 1e9, 1)
+        kernels[k] = d
+    qt_ms = sum(per[k][0] for k in qbytes) / args.steps
+    q_gbs = sum(qbytes.values()) / (qt_ms * 1e-3) / 1e9
+    gemm_ms = sum(per[k][0] for k in gemm_flops) / args.steps
+    gemm_tflops = step_flops / (gemm_ms * 1e-3) / 1e12
+
+    out = {
+        "metric": "fp8 Linear TFLOP/s + quantize GB/s at GPT-2 XL shapes, % of roofline",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8 e4m3/e5m2 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, N(0,1e-3) grads; bf16)",
+        "config": {"workload": "config 4: GPT-2 XL Linears (d=1600) fwd+bwd, M=16384 tokens",
+                   "linears": [f"{n} {k}->{o}" for n, k, o in XL_LINEARS], "tokens": M,
+                   "step_gemm_flops": step_flops},
+        "frac_of_fp8_peak": round(value / FP8_PEAK_TFLOPS, 4),
+        "gemm_only": {"tflops": round(gemm_tflops, 1), "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
+                      "ms_per_step": round(gemm_ms, 4)},
+        "quantize": {"gbs": round(q_gbs, 1), "frac": round(q_gbs / HBM_PEAK_GBS, 4),
+                     "ms_per_step": round(qt_ms, 4)},
+        "roofline": roof,
+        "kernels": kernels,
+    }
+    if not args.no_conversion:
+        out["conversion"] = conversion_bench(torch, df, synth, dev, stream)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
+    print(json.dumps(out))
+
+
+def conversion_bench(torch, df, synth, dev, stream, reps=10):
+    """Config 2: n = 268,435,456 standalone absmax / quantize / dequantize."""
+    import numpy as np
+    n = 268_435_456
+    x32 = torch.from_numpy(synth.conversion_input(n)).to(dev)
+    x16 = x32.to(torch.bfloat16)
+    q = torch.empty(n, dtype=torch.uint8, device=dev)
+    o32 = torch.empty(n, dtype=torch.float32, device=dev)
+    o16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(df.lib().df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
+    sc = torch.empty(2, dtype=torch.float32, device=dev)
+    res = {"n": n}
+    for src, x, o, esz in (("f32", x32, o32, 4), ("bf16", x16, o16, 2)):
+        for fmt, fname in ((0, "e4m3"), (1, "e5m2")):
+            absfn = "df_absmax_scale_f32" if src == "f32" else "df_absmax_scale_bf16"
+            qfn = f"df_quantize_{src}_{fname}"
+            dfn = f"df_dequantize_{fname}_{src}"
+            calls = {
+                "absmax": (lambda: df.call(absfn, x.data_ptr(), n, fmt, sc.data_ptr(), sc.data_ptr() + 4,
+                                           ws.data_ptr(), ws.numel(), stream), n * esz),
+                "quantize": (lambda: df.call(qfn, x.data_ptr(), n, sc.data_ptr() + 4, q.data_ptr(), stream),
+                             n * esz + n),
+                "dequantize": (lambda: df.call(dfn, q.data_ptr(), n, sc.data_ptr() + 4, o.data_ptr(), stream),
+                               n + n * esz),
+            }
+            for kname, (fn, nbytes) in calls.items():
+                fn()
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / reps
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                res[f"{kname}_{src}_{fname}"] = {"ms": round(ms, 4), "gbs": round(gbs, 1),
+                                                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del x32, x16, q, o32, o16
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(tokens):
+    """Oracle (plain C restatement of the reference's FC kernel loops) on a
+    `tokens`-row slice of the workload: forward, dX and dW of the four XL
+    Linears on dequantized operands, one thread per core."""
+    import numpy as np
+
+    from deepfuse_amd import synth
+    from oracle import pyoracle as orc
+
+    threads = orc.nthreads()
+    flops = 0
+    t_total = 0.0
+    for i, (name, K, N) in enumerate(XL_LINEARS):
+        seed = synth.SEED_BASE + 4 + 10 * i
+        X = synth.normal((tokens, K), 1.0, seed=seed)
+        W = synth.normal((N, K), 0.02, seed=seed + 1)
+        b = synth.normal((N,), 0.02, seed=seed + 2)
+        dY = synth.normal((tokens, N), 1e-3, seed=seed + 3)
+        t0 = time.perf_counter()
+        orc.fc_forward(X, W, b, threads=threads)
+        orc.fc_backward_input(dY, W, threads=threads)
+        orc.fc_backward_weights(dY, X, threads=threads)
+        t_total += time.perf_counter() - t0
+        flops += 3 * 2 * tokens * N * K
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(flops / t_total / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "seconds": round(t_total, 2), "cpu": model,
+            "sample": f"oracle fp32 kernel-order loops, fwd+dX+dW of the 4 GPT-2 XL Linears on a "
+                      f"{tokens}-token slice ({flops} flop), {threads} threads"}
+
+
+if __name__ == "__main__":
+    main()
