@@ -8,7 +8,8 @@ bf16 tensors already resident in HBM.  One step, per Linear:
   forward : absmax + quantize X -> e4m3 (row copy and transposed copy),
             absmax + quantize W -> e4m3 (both copies),
             Y = Xq . Wq^T * sx * sw + b            (bf16 out, fused bias)
-  backward: absmax + quantize dY -> e5m2 (both copies), db = column sums,
+  backward: absmax + quantize dY -> e5m2 (both copies) with db = column
+            sums fused into the same pass,
             dX = dYq . W * sdy * sw                  (bf16 out)
             dW = dYq^T . X * sdy * sx                (fp32 out, overwrite)
 value = GEMM flops of the step (2*M*N*K per GEMM, 12 GEMMs) / step time.
@@ -104,6 +105,11 @@ def main():
         return torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
 
     ws = torch.empty(L.df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
+    gws_bytes = max(L.df_fp8_gemm_workspace_bytes(M, n, k) for _, k, n in XL_LINEARS)
+    gws_bytes = max(gws_bytes, max(L.df_fp8_gemm_workspace_bytes(n, k, M) for _, k, n in XL_LINEARS))
+    gws = torch.empty(gws_bytes, dtype=torch.uint8, device=dev)
+    cws = torch.empty(max(L.df_quantize_2d_workspace_bytes(M, n) for _, _, n in XL_LINEARS), dtype=torch.uint8,
+                      device=dev)
     layers = []
     for i, (name, K, N) in enumerate(XL_LINEARS):
         seed = synth.SEED_BASE + 4 + 10 * i
@@ -130,11 +136,16 @@ def main():
     BF, F32 = int(DType.BFLOAT16), int(DType.FLOAT32)
     E4, E5 = int(Fmt.E4M3), int(Fmt.E5M2)
 
-    def quant(tm, x, rows, cols, fmt, am, sc, q, qt, tag):
+    def quant(tm, x, rows, cols, fmt, am, sc, q, qt, tag, db=None):
         tm.run("absmax_" + tag, df.call, "df_absmax_scale_bf16", x.data_ptr(), x.numel(), fmt, am, sc,
                ws.data_ptr(), ws.numel(), stream)
-        tm.run("quantize2d_" + tag, df.call, "df_quantize_2d", BF, x.data_ptr(), rows, cols, cols, fmt, sc,
-               q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), stream)
+        if db is None:
+            tm.run("quantize2d_" + tag, df.call, "df_quantize_2d", BF, x.data_ptr(), rows, cols, cols, fmt, sc,
+                   q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), stream)
+        else:
+            tm.run("quantize2d_" + tag, df.call, "df_quantize_2d_colsum", BF, x.data_ptr(), rows, cols, cols, fmt,
+                   sc, q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), db.data_ptr(), cws.data_ptr(),
+                   cws.numel(), stream)
 
     def step(tm):
         for l in layers:
@@ -145,13 +156,14 @@ def main():
             quant(tm, l["W"], N, K, E4, sw_am, sw, l["Wq"], l["Wt"], "weight")
             tm.run("gemm_fwd", df.call, "df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["Xq"].stride(0),
                    l["Wq"].data_ptr(), l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF,
-                   l["Y"].data_ptr(), N, stream)
-            quant(tm, l["dY"], M, N, E5, sdy_am, sdy, l["dYq"], l["dYt"], "grad")
-            tm.run("colsum_db", df.call, "df_colsum", BF, l["dY"].data_ptr(), M, N, N, l["db"].data_ptr(), stream)
+                   l["Y"].data_ptr(), N, gws.data_ptr(), gws_bytes, stream)
+            quant(tm, l["dY"], M, N, E5, sdy_am, sdy, l["dYq"], l["dYt"], "grad", db=l["db"])
             tm.run("gemm_dx", df.call, "df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0),
-                   l["Wt"].data_ptr(), l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K, stream)
+                   l["Wt"].data_ptr(), l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K,
+                   gws.data_ptr(), gws_bytes, stream)
             tm.run("gemm_dw", df.call, "df_fp8_gemm_bwd_dw", l["dYt"].data_ptr(), l["dYt"].stride(0),
-                   l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K, stream)
+                   l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K,
+                   gws.data_ptr(), gws_bytes, stream)
 
     # algorithmic work per step (unpadded shapes; BASELINE.md counting rules)
     gemm_flops = {"gemm_fwd": 0, "gemm_dx": 0, "gemm_dw": 0}
@@ -163,7 +175,7 @@ def main():
         for tag, r, c in (("act", M, K), ("weight", N, K), ("grad", M, N)):
             qbytes["absmax_" + tag] = qbytes.get("absmax_" + tag, 0) + 2 * r * c
             qbytes["quantize2d_" + tag] = qbytes.get("quantize2d_" + tag, 0) + 2 * r * c + 2 * r * c
-        qbytes["colsum_db"] = qbytes.get("colsum_db", 0) + 2 * M * N + 4 * N
+
     step_flops = sum(gemm_flops.values())
 
     null = Timer(torch, enabled=False)

@@ -75,15 +75,19 @@ _SIGS = {
     "df_dequantize_e5m2_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
     "df_quantize_2d": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
                                 _vp, _c_int, _vp]),
-    "df_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "df_quantize_2d_workspace_bytes": (_c_sz, [_c_int, _c_int]),
+    "df_quantize_2d_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
+                                       _vp, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_fp8_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
     "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
-                                _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp]),
+                                _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_fwd": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
-                                 _c_int, _vp, _c_int, _vp, _c_int, _vp]),
+                                 _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_bwd_dx": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
-                                    _c_int, _vp, _c_int, _vp]),
+                                    _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_bwd_dw": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
-                                    _c_int, _vp, _c_int, _vp]),
+                                    _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fill": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp]),
     "df_add": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
     "df_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
@@ -198,20 +202,51 @@ def round16(v: int) -> int:
     return (v + 15) // 16 * 16
 
 
-def quantize_2d(x, scale, fmt: Fmt, want_q=True, want_qt=False):
+def _scratch(device, nbytes: int, tag: str):
+    torch = _torch()
+    key = (str(device), tag)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def quantize_2d(x, scale, fmt: Fmt, want_q=True, want_qt=False, colsum=False):
     """2-D quantize into GEMM operand layout: returns (q [R, ceil16(C)],
-    qt [C, ceil16(R)]) with zero padding; either may be None."""
+    qt [C, ceil16(R)]) with zero padding (either may be None), plus the fp32
+    column sums when colsum=True."""
     torch = _torch()
     rows, cols = x.shape
     q = torch.empty((rows, round16(cols)), dtype=torch.uint8, device=x.device) if want_q else None
     qt = torch.empty((cols, round16(rows)), dtype=torch.uint8, device=x.device) if want_qt else None
-    call("df_quantize_2d", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), int(fmt), _ptr(scale),
-         _ptr(q), q.shape[1] if q is not None else 0, _ptr(qt), qt.shape[1] if qt is not None else 0,
-         _stream())
-    return q, qt
+    ldq = q.shape[1] if q is not None else 0
+    ldqt = qt.shape[1] if qt is not None else 0
+    if not colsum:
+        call("df_quantize_2d", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), int(fmt), _ptr(scale),
+             _ptr(q), ldq, _ptr(qt), ldqt, _stream())
+        return q, qt
+    cs = torch.empty(cols, dtype=torch.float32, device=x.device)
+    ws = _scratch(x.device, int(lib().df_quantize_2d_workspace_bytes(rows, cols)), "colsum")
+    call("df_quantize_2d_colsum", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), int(fmt),
+         _ptr(scale), _ptr(q), ldq, _ptr(qt), ldqt, _ptr(cs), _ptr(ws), ws.numel(), _stream())
+    return q, qt, cs
 
 
-def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dtype=None):
+def gemm_workspace(M: int, N: int, K: int, device):
+    """Device workspace sized so split-K is never limited (cached per size)."""
+    torch = _torch()
+    nbytes = int(lib().df_fp8_gemm_workspace_bytes(M, N, K))
+    key = (str(device), "gemm")
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dtype=None,
+            split_k=True):
     """C[M,N] = (A[M,:K] . B[N,:K]^T) * sa * sb + bias on fp8 MFMA."""
     torch = _torch()
     out_dtype = out_dtype or torch.float32
@@ -219,14 +254,18 @@ def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dty
     c = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
     bias_dt = int(DType.FLOAT32) if bias is None or bias.dtype == torch.float32 else int(DType.BFLOAT16)
     c_dt = int(DType.FLOAT32) if out_dtype == torch.float32 else int(DType.BFLOAT16)
+    ws = gemm_workspace(M, N, K, a_q.device) if split_k else None
     call("df_fp8_gemm_nt", int(fmt_a), _ptr(a_q), a_q.stride(0), int(fmt_b), _ptr(b_q), b_q.stride(0),
-         M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _stream())
+         M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _ptr(ws),
+         ws.numel() if ws is not None else 0, _stream())
     return c
 
 
 def colsum(x):
     torch = _torch()
-    out = torch.empty(x.shape[1], dtype=torch.float32, device=x.device)
-    call("df_colsum", int(_in_dtype(x)), _ptr(x), x.shape[0], x.shape[1], x.stride(0), _ptr(out),
+    rows, cols = x.shape
+    out = torch.empty(cols, dtype=torch.float32, device=x.device)
+    ws = _scratch(x.device, int(lib().df_quantize_2d_workspace_bytes(rows, cols)), "colsum")
+    call("df_colsum", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), _ptr(out), _ptr(ws), ws.numel(),
          _stream())
     return out

@@ -134,12 +134,8 @@ __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* _
 }
 
 // ---------------------------------------------------------------- quantize --
-// x / s with IEEE binary32 division (contract D1), then the fp8 encoder.
-template <int FMT>
-__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float s) {
-    return encode_fp8<FMT>(a / s) | (encode_fp8<FMT>(b / s) << 8) |
-           (encode_fp8<FMT>(c / s) << 16) | (encode_fp8<FMT>(d / s) << 24);
-}
+// x / s (correctly rounded: qdiv, contract D1), then the fp8 encoder
+// (encode2_hw: hardware round-to-nearest-even after saturation, NaN kept).
 
 // fp32 -> fp8: one 16-byte load -> one 4-byte store per thread per step.
 template <int FMT>
@@ -147,33 +143,37 @@ __global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __r
                                                                  int64_t n,
                                                                  const float* __restrict__ scale,
                                                                  uint8_t* __restrict__ q) {
-    const float s = scale[0];
+    const QDiv d = make_qdiv(scale[0]);
     const int64_t nvec = n >> 2;
     const f32x4* xv = reinterpret_cast<const f32x4*>(x);
     uint32_t* qv = reinterpret_cast<uint32_t*>(q);
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + stride < nvec; i += 2 * stride) {
-        f32x4 v0 = __builtin_nontemporal_load(xv + i);
-        f32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
-        __builtin_nontemporal_store(quant4<FMT>(v0.x, v0.y, v0.z, v0.w, s), qv + i);
-        __builtin_nontemporal_store(quant4<FMT>(v1.x, v1.y, v1.z, v1.w, s), qv + i + stride);
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+        const f32x4 v0 = __builtin_nontemporal_load(xv + i);
+        const f32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
+        const f32x4 v2 = __builtin_nontemporal_load(xv + i + 2 * stride);
+        const f32x4 v3 = __builtin_nontemporal_load(xv + i + 3 * stride);
+        __builtin_nontemporal_store(quant4_fast<FMT>(v0.x, v0.y, v0.z, v0.w, d), qv + i);
+        __builtin_nontemporal_store(quant4_fast<FMT>(v1.x, v1.y, v1.z, v1.w, d), qv + i + stride);
+        __builtin_nontemporal_store(quant4_fast<FMT>(v2.x, v2.y, v2.z, v2.w, d), qv + i + 2 * stride);
+        __builtin_nontemporal_store(quant4_fast<FMT>(v3.x, v3.y, v3.z, v3.w, d), qv + i + 3 * stride);
     }
     for (; i < nvec; i += stride) {
-        f32x4 v = xv[i];
-        qv[i] = quant4<FMT>(v.x, v.y, v.z, v.w, s);
+        const f32x4 v = xv[i];
+        qv[i] = quant4_fast<FMT>(v.x, v.y, v.z, v.w, d);
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const int64_t j = (nvec << 2) + threadIdx.x;
-        q[j] = (uint8_t)encode_fp8<FMT>(x[j] / s);
+        q[j] = (uint8_t)encode2_hw<FMT>(qdiv(x[j], d), 0.0f);
     }
 }
 
 // bf16 -> fp8: one 16-byte load (8 values) -> one 8-byte store.
 template <int FMT>
-__device__ __forceinline__ uint32_t quant_bf16x4(uint32_t w0, uint32_t w1, float s) {
-    return quant4<FMT>(bf16_to_f32(w0 & 0xFFFFu), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xFFFFu),
-                       bf16_to_f32(w1 >> 16), s);
+__device__ __forceinline__ uint32_t quant_bf16x4(uint32_t w0, uint32_t w1, const QDiv& d) {
+    return quant4_fast<FMT>(bf16_to_f32(w0 & 0xFFFFu), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xFFFFu),
+                            bf16_to_f32(w1 >> 16), d);
 }
 
 template <int FMT>
@@ -181,33 +181,34 @@ __global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t*
                                                                   int64_t n,
                                                                   const float* __restrict__ scale,
                                                                   uint8_t* __restrict__ q) {
-    const float s = scale[0];
+    const QDiv d = make_qdiv(scale[0]);
     const int64_t nvec = n >> 3;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
     u32x2* qv = reinterpret_cast<u32x2*>(q);
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + stride < nvec; i += 2 * stride) {
-        u32x4 v0 = __builtin_nontemporal_load(xv + i);
-        u32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
-        u32x2 o0, o1;
-        o0.x = quant_bf16x4<FMT>(v0.x, v0.y, s);
-        o0.y = quant_bf16x4<FMT>(v0.z, v0.w, s);
-        o1.x = quant_bf16x4<FMT>(v1.x, v1.y, s);
-        o1.y = quant_bf16x4<FMT>(v1.z, v1.w, s);
-        __builtin_nontemporal_store(o0, qv + i);
-        __builtin_nontemporal_store(o1, qv + i + stride);
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(xv + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            u32x2 o;
+            o.x = quant_bf16x4<FMT>(v[u].x, v[u].y, d);
+            o.y = quant_bf16x4<FMT>(v[u].z, v[u].w, d);
+            __builtin_nontemporal_store(o, qv + i + u * stride);
+        }
     }
     for (; i < nvec; i += stride) {
-        u32x4 v = xv[i];
+        const u32x4 v = xv[i];
         u32x2 o;
-        o.x = quant_bf16x4<FMT>(v.x, v.y, s);
-        o.y = quant_bf16x4<FMT>(v.z, v.w, s);
+        o.x = quant_bf16x4<FMT>(v.x, v.y, d);
+        o.y = quant_bf16x4<FMT>(v.z, v.w, d);
         qv[i] = o;
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t j = (nvec << 3) + threadIdx.x;
-        q[j] = (uint8_t)encode_fp8<FMT>(bf16_to_f32(x[j]) / s);
+        q[j] = (uint8_t)encode2_hw<FMT>(qdiv(bf16_to_f32(x[j]), d), 0.0f);
     }
 }
 
@@ -270,76 +271,143 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
 }
 
 // ------------------------------------------------------- 2-D + transposed --
-// One 64x64 tile per block: 256 threads, thread t owns rows t/16 + 16*i
-// (i < 4) and the 4 columns starting at 4*(t%16).  Codes go straight to q
-// (4-byte stores) and through an LDS tile to qt (16-byte stores along the
-// transposed rows).  Out-of-range elements encode as 0 so the padding
-// columns of q and qt are written in the same pass.
-constexpr int kT2 = 64;
+// One 128 x 128 tile per 256-thread block.  Thread t owns the 16-byte
+// column chunk (t % TPR) of RPT consecutive rows: 16-byte loads, row-major
+// codes stored straight to q, and the same codes written transposed into an
+// LDS tile [column][row] that is then stored to qt as 128-byte row segments.
+// Elements outside [rows) x [cols) encode as 0, so the padding of q (columns
+// up to ldq) and of qt (columns up to ldqt) is written in the same pass.
+// With COLSUM the block also folds the fp32 values of its tile into one
+// partial sum per column (rows in fixed order), written to
+// colpart[tile_row][col] for a deterministic second pass.
+constexpr int kT2 = 128;
 
-template <typename InT>
-__device__ __forceinline__ float load_elem(const InT* x, int64_t idx);
-template <>
-__device__ __forceinline__ float load_elem<float>(const float* x, int64_t idx) { return x[idx]; }
-template <>
-__device__ __forceinline__ float load_elem<uint16_t>(const uint16_t* x, int64_t idx) {
-    return bf16_to_f32(x[idx]);
-}
-
-template <typename InT, int FMT>
-__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
-                                                                int cols, int ldx,
-                                                                const float* __restrict__ scale,
-                                                                uint8_t* __restrict__ q, int ldq,
-                                                                uint8_t* __restrict__ qt, int ldqt) {
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2][kT2 + 16];  // [col][row]
-    const float s = scale[0];
-    const int r0 = blockIdx.y * kT2, c0 = blockIdx.x * kT2;
-    const int tc = (threadIdx.x & 15) * 4;
+template <typename InT> struct Ld;
+template <> struct Ld<float> {
+    static constexpr int E = 4;
+    static __device__ __forceinline__ void vec(const float* p, float* v) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+    static __device__ __forceinline__ float one(const float* p) { return *p; }
+};
+template <> struct Ld<uint16_t> {
+    static constexpr int E = 8;
+    static __device__ __forceinline__ void vec(const uint16_t* p, float* v) {
+        const u32x4 t = *reinterpret_cast<const u32x4*>(p);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tr = (threadIdx.x >> 4) + 16 * i;
-        const int r = r0 + tr, c = c0 + tc;
-        uint32_t packed = 0;
-        if (r < rows) {
-            const int64_t base = (int64_t)r * ldx + c;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (c + j < cols) packed |= encode_fp8<FMT>(load_elem<InT>(x, base + j) / s) << (8 * j);
-        }
-        if (q && r < rows && c < ldq) *reinterpret_cast<uint32_t*>(q + (int64_t)r * ldq + c) = packed;
-        if (qt) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) tile[tc + j][tr] = (uint8_t)(packed >> (8 * j));
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = bf16_to_f32(w[i] & 0xFFFFu);
+            v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
         }
     }
-    if (!qt) return;
+    static __device__ __forceinline__ float one(const uint16_t* p) { return bf16_to_f32(*p); }
+};
+
+template <typename InT, int FMT, bool COLSUM, bool CODES>
+__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
+                                                                int cols, int ldx, bool vec_ok,
+                                                                const float* __restrict__ scale,
+                                                                uint8_t* __restrict__ q, int ldq,
+                                                                uint8_t* __restrict__ qt, int ldqt,
+                                                                float* __restrict__ colpart) {
+    constexpr int E = Ld<InT>::E;      // elements per 16-byte load
+    constexpr int TPR = kT2 / E;       // threads per tile row
+    constexpr int RG = kThreads / TPR; // row groups
+    constexpr int RPT = kT2 / RG;      // rows per thread (8 for bf16, 16 for fp32)
+    constexpr int TSTRIDE = kT2 + 16;  // LDS tile row (bytes), [column][row]
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * TSTRIDE];
+    __shared__ float csum[COLSUM ? RG : 1][kT2];
+
+    const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
+    const int r0 = blockIdx.y * kT2, c0 = blockIdx.x * kT2;
+    const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
+    const int c = c0 + tc;
+    const bool full = vec_ok && c + E <= cols;
+    uint32_t codes[RPT][E / 4];
+    float cs[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) cs[e] = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPT; ++rr) {
+        const int r = r0 + rg * RPT + rr;
+        float v[E];
+        if (r < rows && full) {
+            Ld<InT>::vec(x + (int64_t)r * ldx + c, v);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                v[e] = (r < rows && c + e < cols) ? Ld<InT>::one(x + (int64_t)r * ldx + c + e) : 0.0f;
+        }
+        if (COLSUM) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) cs[e] += v[e];
+        }
+        if (!CODES) continue;
+#pragma unroll
+        for (int g = 0; g < E / 4; ++g)
+            codes[rr][g] = quant4_fast<FMT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
+        if (q && r < rows && c < ldq) {
+            if (E == 8)
+                *reinterpret_cast<u32x2*>(q + (int64_t)r * ldq + c) = u32x2{codes[rr][0], codes[rr][E / 4 - 1]};
+            else
+                *reinterpret_cast<uint32_t*>(q + (int64_t)r * ldq + c) = codes[rr][0];
+        }
+    }
+    if (CODES && qt) {
+        // column e of this thread's chunk: RPT codes down rows rg*RPT...
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            uint32_t w[RPT / 4];
+#pragma unroll
+            for (int k = 0; k < RPT / 4; ++k) {
+                uint32_t acc = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc |= ((codes[4 * k + b][e >> 2] >> (8 * (e & 3))) & 0xFFu) << (8 * b);
+                w[k] = acc;
+            }
+            uint8_t* dst = tile + (tc + e) * TSTRIDE + rg * RPT;
+            if (RPT == 16)
+                *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[RPT / 4 > 1 ? 1 : 0], w[RPT / 4 > 2 ? 2 : 0],
+                                                       w[RPT / 4 > 3 ? 3 : 0]};
+            else
+                *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[RPT / 4 > 1 ? 1 : 0]};
+        }
+    }
+    if (COLSUM) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) csum[rg][tc + e] = cs[e];
+    }
     __syncthreads();
-    const int tcol = threadIdx.x >> 2;          // transposed row = column of x
-    const int trow = (threadIdx.x & 3) * 16;    // 16 codes along rows of x
-    const int c = c0 + tcol, r = r0 + trow;
-    if (c < cols && r < ldqt)
-        *reinterpret_cast<uint4*>(qt + (int64_t)c * ldqt + r) =
-            *reinterpret_cast<const uint4*>(&tile[tcol][trow]);
+    if (CODES && qt) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = threadIdx.x + kThreads * k;
+            const int col = idx >> 3, rc = (idx & 7) * 16;
+            if (c0 + col < cols && r0 + rc < ldqt)
+                *reinterpret_cast<u32x4*>(qt + (int64_t)(c0 + col) * ldqt + r0 + rc) =
+                    *reinterpret_cast<const u32x4*>(tile + col * TSTRIDE + rc);
+        }
+    }
+    if (COLSUM && threadIdx.x < kT2 && c0 + threadIdx.x < cols) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int g = 0; g < RG; ++g) sum += csum[g][threadIdx.x];
+        colpart[(int64_t)blockIdx.y * cols + c0 + threadIdx.x] = sum;
+    }
 }
 
-// ------------------------------------------------------------------ colsum --
-// out[c] = sum_r x[r,c]: a block owns 64 columns; its 4 waves take every 4th
-// row (coalesced 64-column rows), then fold through LDS.
-template <typename InT>
-__global__ __launch_bounds__(kThreads) void colsum_kernel(const InT* __restrict__ x, int rows,
-                                                           int cols, int ldx,
-                                                           float* __restrict__ out) {
-    __shared__ float part[4][64];
-    const int c = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int w = threadIdx.x >> 6;
-    float acc = 0.0f;
-    if (c < cols)
-        for (int r = w; r < rows; r += 4) acc += load_elem<InT>(x, (int64_t)r * ldx + c);
-    part[w][threadIdx.x & 63] = acc;
-    __syncthreads();
-    if (w == 0 && c < cols)
-        out[c] = (part[0][threadIdx.x] + part[1][threadIdx.x]) + (part[2][threadIdx.x] + part[3][threadIdx.x]);
+// out[c] = sum over tile rows of colpart[t][c], in tile order.
+__global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __restrict__ colpart,
+                                                                  int tiles, int cols,
+                                                                  float* __restrict__ out) {
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.0f;
+    for (int t = 0; t < tiles; ++t) s += colpart[(int64_t)t * cols + c];
+    out[c] = s;
 }
 
 // --------------------------------------------------------------- launchers --
@@ -491,55 +559,95 @@ extern "C" int df_dequantize_e5m2_bf16(const uint8_t* q, int64_t n, const float*
     return dequantize_bf16_impl<E5M2>(q, n, s, o, st, "df_dequantize_e5m2_bf16");
 }
 
-extern "C" int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
-                              const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
-                              void* stream) {
+extern "C" size_t df_quantize_2d_workspace_bytes(int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    return (size_t)((rows + kT2 - 1) / kT2) * (size_t)cols * sizeof(float);
+}
+
+static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int rows, int cols, int ldx,
+                            int fmt, const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
+                            float* colsum, void* ws, size_t ws_bytes, void* stream) {
     clear_error();
     DF_CHECK(rows >= 0 && cols >= 0 && ldx >= cols, DF_ERR_INVALID,
-             "df_quantize_2d: bad shape rows=%d cols=%d ldx=%d", rows, cols, ldx);
-    DF_CHECK(q || qt, DF_ERR_INVALID, "df_quantize_2d: no output");
-    DF_CHECK(scale_dev && (x || rows * (int64_t)cols == 0), DF_ERR_INVALID, "df_quantize_2d: NULL pointer");
-    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "df_quantize_2d: bad format %d", fmt);
+             "%s: bad shape rows=%d cols=%d ldx=%d", name, rows, cols, ldx);
+    DF_CHECK(q || qt || colsum, DF_ERR_INVALID, "%s: no output", name);
+    DF_CHECK((scale_dev || (!q && !qt)) && (x || rows * (int64_t)cols == 0), DF_ERR_INVALID, "%s: NULL pointer", name);
+    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad format %d", name, fmt);
     DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
-             "df_quantize_2d: dtype %d not supported", in_dtype);
+             "%s: dtype %d not supported", name, in_dtype);
     if (q) {
-        DF_CHECK(ldq >= cols && ldq % 16 == 0, DF_ERR_ALIGN, "df_quantize_2d: ldq=%d must be >= cols and a multiple of 16", ldq);
-        DF_CHECK(aligned16(q), DF_ERR_ALIGN, "df_quantize_2d: q must be 16-byte aligned");
+        DF_CHECK(ldq >= cols && ldq % 16 == 0, DF_ERR_ALIGN, "%s: ldq=%d must be >= cols and a multiple of 16", name, ldq);
+        DF_CHECK(aligned16(q), DF_ERR_ALIGN, "%s: q must be 16-byte aligned", name);
     }
     if (qt) {
-        DF_CHECK(ldqt >= rows && ldqt % 16 == 0, DF_ERR_ALIGN, "df_quantize_2d: ldqt=%d must be >= rows and a multiple of 16", ldqt);
-        DF_CHECK(aligned16(qt), DF_ERR_ALIGN, "df_quantize_2d: qt must be 16-byte aligned");
+        DF_CHECK(ldqt >= rows && ldqt % 16 == 0, DF_ERR_ALIGN, "%s: ldqt=%d must be >= rows and a multiple of 16", name, ldqt);
+        DF_CHECK(aligned16(qt), DF_ERR_ALIGN, "%s: qt must be 16-byte aligned", name);
+    }
+    if (colsum) {
+        DF_CHECK(ws && aligned4(ws), DF_ERR_WORKSPACE, "%s: column sums need a workspace", name);
+        DF_CHECK(ws_bytes >= df_quantize_2d_workspace_bytes(rows, cols), DF_ERR_WORKSPACE,
+                 "%s: workspace %zu bytes < %zu", name, ws_bytes, df_quantize_2d_workspace_bytes(rows, cols));
     }
     const int row_ext = qt ? (rows > ldqt ? rows : ldqt) : rows;
     const int col_ext = q ? (cols > ldq ? cols : ldq) : cols;
-    if (row_ext == 0 || col_ext == 0) return DF_OK;
-    dim3 grid((col_ext + kT2 - 1) / kT2, (row_ext + kT2 - 1) / kT2);
-    hipStream_t st = as_stream(stream);
-    if (in_dtype == DF_DTYPE_FLOAT32) {
-        auto* xp = static_cast<const float*>(x);
-        if (fmt == E4M3) quantize_2d_kernel<float, E4M3><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
-        else quantize_2d_kernel<float, E5M2><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
-    } else {
-        auto* xp = static_cast<const uint16_t*>(x);
-        if (fmt == E4M3) quantize_2d_kernel<uint16_t, E4M3><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
-        else quantize_2d_kernel<uint16_t, E5M2><<<grid, kThreads, 0, st>>>(xp, rows, cols, ldx, scale_dev, q, ldq, qt, ldqt);
+    if (row_ext == 0 || col_ext == 0) {
+        if (colsum && cols > 0) {
+            const float zero = 0.0f;
+            return df_fill(colsum, cols, 4, &zero, stream);
+        }
+        return DF_OK;
     }
-    return launch_status("df_quantize_2d");
+    const int gy = (row_ext + kT2 - 1) / kT2;
+    DF_CHECK(gy <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
+    dim3 grid((col_ext + kT2 - 1) / kT2, gy);
+    hipStream_t st = as_stream(stream);
+    float* part = colsum ? static_cast<float*>(ws) : nullptr;
+    const int esz = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 2;
+    const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
+#define DF_Q2D(T, F, CS) \
+    quantize_2d_kernel<T, F, CS, true><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, ldx, vec_ok, \
+                                                                  scale_dev, q, ldq, qt, ldqt, part)
+    if (!q && !qt) {  // column sums only
+        if (in_dtype == DF_DTYPE_FLOAT32)
+            quantize_2d_kernel<float, E4M3, true, false><<<grid, kThreads, 0, st>>>(
+                static_cast<const float*>(x), rows, cols, ldx, vec_ok, nullptr, nullptr, 0, nullptr, 0, part);
+        else
+            quantize_2d_kernel<uint16_t, E4M3, true, false><<<grid, kThreads, 0, st>>>(
+                static_cast<const uint16_t*>(x), rows, cols, ldx, vec_ok, nullptr, nullptr, 0, nullptr, 0, part);
+    } else if (in_dtype == DF_DTYPE_FLOAT32) {
+        if (fmt == E4M3) { if (colsum) DF_Q2D(float, E4M3, true); else DF_Q2D(float, E4M3, false); }
+        else { if (colsum) DF_Q2D(float, E5M2, true); else DF_Q2D(float, E5M2, false); }
+    } else {
+        if (fmt == E4M3) { if (colsum) DF_Q2D(uint16_t, E4M3, true); else DF_Q2D(uint16_t, E4M3, false); }
+        else { if (colsum) DF_Q2D(uint16_t, E5M2, true); else DF_Q2D(uint16_t, E5M2, false); }
+    }
+#undef DF_Q2D
+    if (colsum)
+        colsum_reduce_kernel<<<(cols + kThreads - 1) / kThreads, kThreads, 0, st>>>(part, rows == 0 ? 0 : (rows + kT2 - 1) / kT2,
+                                                                                    cols, colsum);
+    return launch_status(name);
 }
 
-extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx, float* out,
-                         void* stream) {
-    clear_error();
-    DF_CHECK(rows >= 0 && cols >= 0 && ldx >= cols, DF_ERR_INVALID, "df_colsum: bad shape");
-    if (cols == 0) return DF_OK;
-    DF_CHECK(out && (x || rows == 0), DF_ERR_INVALID, "df_colsum: NULL pointer");
-    hipStream_t st = as_stream(stream);
-    const int blocks = (cols + 63) / 64;
-    if (in_dtype == DF_DTYPE_FLOAT32)
-        colsum_kernel<float><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), rows, cols, ldx, out);
-    else if (in_dtype == DF_DTYPE_BFLOAT16)
-        colsum_kernel<uint16_t><<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), rows, cols, ldx, out);
-    else
-        DF_CHECK(false, DF_ERR_UNSUPPORTED, "df_colsum: dtype %d not supported", in_dtype);
-    return launch_status("df_colsum");
+extern "C" int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                              const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
+                              void* stream) {
+    DF_CHECK(q || qt, DF_ERR_INVALID, "df_quantize_2d: no output");
+    return quantize_2d_impl("df_quantize_2d", in_dtype, x, rows, cols, ldx, fmt, scale_dev, q, ldq, qt, ldqt,
+                            nullptr, nullptr, 0, stream);
+}
+
+extern "C" int df_quantize_2d_colsum(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                                     const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
+                                     float* colsum, void* ws, size_t ws_bytes, void* stream) {
+    DF_CHECK(colsum, DF_ERR_INVALID, "df_quantize_2d_colsum: colsum is NULL");
+    return quantize_2d_impl("df_quantize_2d_colsum", in_dtype, x, rows, cols, ldx, fmt, scale_dev, q, ldq, qt,
+                            ldqt, colsum, ws, ws_bytes, stream);
+}
+
+extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx, float* out, void* ws,
+                         size_t ws_bytes, void* stream) {
+    // column sums alone: the same tile pass with no code outputs
+    DF_CHECK(out, DF_ERR_INVALID, "df_colsum: out is NULL");
+    return quantize_2d_impl("df_colsum", in_dtype, x, rows, cols, ldx, E4M3, nullptr, nullptr, 0, nullptr, 0, out,
+                            ws, ws_bytes, stream);
 }

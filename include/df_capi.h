@@ -117,13 +117,24 @@ int df_dequantize_e5m2_bf16(const uint8_t* q, int64_t n, const float* scale_dev,
 int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx,
                    int fmt, const float* scale_dev, uint8_t* q, int ldq,
                    uint8_t* qt, int ldqt, void* stream);
+/* Workspace for the column-sum passes below: ceil(rows/128) * cols floats. */
+size_t df_quantize_2d_workspace_bytes(int rows, int cols);
+/* df_quantize_2d plus colsum[c] = sum_r x[r,c] in fp32 from the same read of
+ * x (the bias gradient of the upstream gradient dY, replacing
+ * fc_backward_bias, dnn/layers/fully_connected_layer.cu:91-106).  Sums run
+ * over each 128-row tile, then over tiles in order: deterministic, but not
+ * the reference's sequential order.  q and qt may both be NULL. */
+int df_quantize_2d_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
+                          int fmt, const float* scale_dev, uint8_t* q, int ldq,
+                          uint8_t* qt, int ldqt, float* colsum,
+                          void* ws, size_t ws_bytes, void* stream);
 
-/* ---- column sums (replaces fc_backward_bias,
+/* ---- column sums alone (replaces fc_backward_bias,
  * dnn/layers/fully_connected_layer.cu:91-106) ----
- * out[c] = sum_r x[r, c] in fp32 (tree order, not the reference's
- * sequential order); overwrites out. */
+ * out[c] = sum_r x[r, c] in fp32, same order as df_quantize_2d_colsum;
+ * overwrites out.  ws: df_quantize_2d_workspace_bytes(rows, cols) bytes. */
 int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
-              float* out, void* stream);
+              float* out, void* ws, size_t ws_bytes, void* stream);
 
 /* ---- fp8 GEMM, "NT": C[m,n] = (sum_k A[m,k] * B[n,k]) * sa * sb + bias[n]
  *   A [M, lda] fp8 (fmt_a), B [N, ldb] fp8 (fmt_b), both row-major with the
@@ -133,32 +144,41 @@ int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
  *   BFLOAT16), overwritten.  fp32 accumulation on CDNA4 fp8 MFMA.
  *   When K is not a multiple of 16, columns [K, roundup(K,16)) of A and B
  *   must hold zero codes (df_quantize_2d writes its padding that way).
+ *   ws / ws_bytes: optional device workspace (16-byte aligned) for split-K
+ *   partial tiles on outputs too small to fill the GPU; NULL or too small
+ *   only turns split-K off.  df_fp8_gemm_workspace_bytes() is the size that
+ *   never limits it.  Results do not depend on run-to-run timing (split-K
+ *   partials are summed in a fixed order).
  * Replaces fully_connected_forward_kernel (fully_connected_layer.cu:14-41). */
+size_t df_fp8_gemm_workspace_bytes(int M, int N, int K);
 int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda,
                    int fmt_b, const uint8_t* B, int ldb,
                    int M, int N, int K,
                    const float* scale_a_dev, const float* scale_b_dev,
                    int bias_dtype, const void* bias,
-                   int c_dtype, void* C, int ldc, void* stream);
+                   int c_dtype, void* C, int ldc,
+                   void* ws, size_t ws_bytes, void* stream);
 
 /* Forward: Y[M,N] = X_q[M,K] . W_q[N,K]^T * sx * sw + b  (e4m3 x e4m3).
  * Replaces fully_connected_forward_kernel (fully_connected_layer.cu:14-41). */
 int df_fp8_gemm_fwd(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw,
                     int M, int N, int K, const float* sx_dev, const float* sw_dev,
                     int bias_dtype, const void* bias, int y_dtype, void* Y, int ldy,
-                    void* stream);
+                    void* ws, size_t ws_bytes, void* stream);
 /* dX[M,K] = dY_q[M,N] . W[N,K]  (e5m2 x e4m3), given W^T quantized as
  * Wt_q[K, ldwt] (df_quantize_2d's qt).  Replaces fc_backward_input
  * (fully_connected_layer.cu:43-65). */
 int df_fp8_gemm_bwd_dx(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
                        int M, int N, int K, const float* sdy_dev, const float* sw_dev,
-                       int dx_dtype, void* dX, int lddx, void* stream);
+                       int dx_dtype, void* dX, int lddx,
+                       void* ws, size_t ws_bytes, void* stream);
 /* dW[N,K] = dY^T . X, given dY^T quantized as dYt_q[N, ldyt] (e5m2) and X^T
  * as Xt_q[K, ldxt] (e4m3); M tokens is the reduction.  Overwrites dW, like
  * fc_backward_weights (fully_connected_layer.cu:67-89, :85-87). */
 int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ldxt,
                        int M, int N, int K, const float* sdy_dev, const float* sx_dev,
-                       int dw_dtype, void* dW, int lddw, void* stream);
+                       int dw_dtype, void* dW, int lddw,
+                       void* ws, size_t ws_bytes, void* stream);
 
 /* ---- tensor utilities behind dnn::tensor (dnn/core/tensor.cu:18-52) ---- */
 /* fill_kernel (tensor.cu:19): n elements of elem_bytes (1, 2 or 4) = *value */

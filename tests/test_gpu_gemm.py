@@ -140,10 +140,13 @@ def test_backward_entry_points_match_nt(dev):
     dX = torch.empty((M, K), dtype=torch.float32, device=dev)
     dW = torch.empty((N, K), dtype=torch.float32, device=dev)
     st = torch.cuda.current_stream().cuda_stream
+    ws = df.gemm_workspace(M, K, N, dev)
     df.call("df_fp8_gemm_bwd_dx", dyq.data_ptr(), dyq.stride(0), wt.data_ptr(), wt.stride(0), M, N, K,
-            sdy.data_ptr(), sw.data_ptr(), int(df.DType.FLOAT32), dX.data_ptr(), K, st)
+            sdy.data_ptr(), sw.data_ptr(), int(df.DType.FLOAT32), dX.data_ptr(), K, ws.data_ptr(),
+            ws.numel(), st)
     df.call("df_fp8_gemm_bwd_dw", dyt.data_ptr(), dyt.stride(0), xt.data_ptr(), xt.stride(0), M, N, K,
-            sdy.data_ptr(), sx.data_ptr(), int(df.DType.FLOAT32), dW.data_ptr(), K, st)
+            sdy.data_ptr(), sx.data_ptr(), int(df.DType.FLOAT32), dW.data_ptr(), K, ws.data_ptr(),
+            ws.numel(), st)
     assert torch.equal(dX, dX_nt)
     assert torch.equal(dW, dW_nt)
 

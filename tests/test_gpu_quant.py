@@ -76,6 +76,22 @@ def test_exhaustive_f32_patterns_unit_scale(dev, fmt):
         del x, q
 
 
+@pytest.mark.parametrize("fmt,s", [(Fmt.E4M3, 4.0 / 448.0), (Fmt.E5M2, 3.0 / 57344.0)])
+def test_exhaustive_f32_patterns_nonunit_scale(dev, fmt, s):
+    """Every binary32 bit pattern divided by a non-trivial scale: pins the
+    kernel's correctly rounded x / s against the oracle's IEEE division."""
+    s32 = float(np.float32(s))
+    sd = scale_tensor(s32, dev)
+    chunk = 1 << 28
+    for c in range(16):
+        first = c * chunk
+        x = torch.arange(first, first + chunk, dtype=torch.int64, device=dev).to(torch.int32)
+        q = df.quantize(x.view(torch.float32), sd, fmt).cpu().numpy()
+        del x
+        bits = np.arange(first, first + chunk, dtype=np.uint64).astype(np.uint32)
+        assert_bits_equal(q, orc.quantize(bits.view(np.float32), s32, int(fmt)), f"chunk {c} s={s32}")
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_random_patterns_nonunit_scale(dev, fmt):
     """Random binary32 patterns (all classes) under several scales: exercises
@@ -84,7 +100,9 @@ def test_random_patterns_nonunit_scale(dev, fmt):
     bits = rng.integers(0, 1 << 32, size=1 << 24, dtype=np.uint64).astype(np.uint32)
     x = bits.view(np.float32)
     xd = to_dev_f32(x, dev)
-    for s in (448.0 / 3.7, 1.0 / 448.0, 3.0e-5, 2.0 ** -140, 1.7e30, 0.999999940395):
+    for s in (448.0 / 3.7, 1.0 / 448.0, 3.0e-5, 2.0 ** -140, 1.7e30, 0.999999940395,
+              2.0 ** -60, 2.0 ** -61, 2.0 ** 60, 2.0 ** 61, 1.0e-25, 3.0e25,
+              2.0 ** -40, 2.0 ** -41, 2.0 ** 40, 2.0 ** 41, 0.7 * 2.0 ** -40, 1.3 * 2.0 ** 40):
         s32 = float(np.float32(s))
         q = df.quantize(xd, scale_tensor(s32, dev), fmt)
         assert_bits_equal(q.cpu().numpy(), orc.quantize(x, s32, int(fmt)), f"s={s32}")
@@ -186,6 +204,24 @@ def test_config2_full_size(dev, src, fmt):
     for lo in range(0, n, step):
         exp[lo:lo + step] = orc.dequantize(qe[lo:lo + step], s_exp, int(fmt), deq_kind)
     assert_bits_equal(got, exp, "round trip")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_quantize_2d_colsum(dev, fmt):
+    """Fused column sums of the 2-D pass (the dY pass of the backward, db)."""
+    for rows, cols in [(1, 3), (100, 50), (129, 257), (1000, 1600)]:
+        x = synth.normal((rows, cols), 1e-3, seed=rows + cols)
+        xd = to_dev_f32(x, dev)
+        s = float(np.float32(orc.scale(orc.absmax(x), int(fmt))))
+        q, qt, cs = df.quantize_2d(xd, scale_tensor(s, dev), fmt, want_q=True, want_qt=True, colsum=True)
+        flat = orc.quantize(x, s, int(fmt))
+        assert_bits_equal(q.cpu().numpy()[:, :cols], flat, "q")
+        assert_bits_equal(qt.cpu().numpy()[:, :rows], np.ascontiguousarray(flat.T), "qt")
+        assert orc.rel_err(cs.cpu().numpy(), orc.fc_backward_bias(x)) <= 1e-4
+        xb = synth.f32_to_bf16_bits(x)
+        _, _, csb = df.quantize_2d(to_dev_bf16(xb, dev).view(rows, cols), scale_tensor(s, dev), fmt,
+                                   want_q=False, want_qt=False, colsum=True)
+        assert orc.rel_err(csb.cpu().numpy(), orc.fc_backward_bias(orc.bf16_to_f32(xb).reshape(rows, cols))) <= 1e-4
 
 
 @pytest.mark.parametrize("fmt", FMTS)
