@@ -419,16 +419,29 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_nt_dma128_kernel(
                                            vec_out, sa[0] * sb[0], bias);
 }
 
-// out[m,n] = (sum_s P[s][m][n]) * sa * sb + bias[n], slices in order.
+// out[m,n] = (sum_s P[s][m][n]) * sa * sb + bias[n], slices in order; four
+// consecutive columns per thread (16-byte partial loads) when N % 4 == 0.
 template <typename OutT, typename BiasT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int S, int M,
                                                             int N, const float* __restrict__ sa,
                                                             const float* __restrict__ sb,
                                                             const BiasT* __restrict__ bias,
-                                                            OutT* __restrict__ C, int ldc) {
+                                                            OutT* __restrict__ C, int ldc, bool vec) {
     const float sab = sa[0] * sb[0];
     const int64_t total = (int64_t)M * N;
     const int64_t stride = (int64_t)gridDim.x * 256;
+    if (vec) {
+        for (int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; e < total; e += stride * 4) {
+            f32x4 acc = *reinterpret_cast<const f32x4*>(P + e);
+            for (int s = 1; s < S; ++s) acc += *reinterpret_cast<const f32x4*>(P + (int64_t)s * total + e);
+            const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
+            float v[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = v[r] * sab + (bias ? bias_ld(bias, n + r) : 0.0f);
+            store4(C + (int64_t)m * ldc + n, v);
+        }
+        return;
+    }
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += stride) {
         float acc = P[e];
         for (int s = 1; s < S; ++s) acc += P[(int64_t)s * total + e];
@@ -448,41 +461,54 @@ struct GemmArgs {
     hipStream_t st;
 };
 
-// Split-K choice: only when the output has too few tiles to occupy the 256
-// CUs and the reduction is long; S balances tiles*S against whole rounds.
-static int choose_split(int tiles, int nk, size_t ws_bytes, int64_t MN) {
-    constexpr int kCUs = 256;
-    if (tiles >= kCUs || nk < 16) return 1;
-    int best = 1;
-    double best_eff = (double)tiles / kCUs;
-    for (int s = 2; s <= 8 && nk / s >= 4; ++s) {
-        if ((size_t)s * MN * sizeof(float) > ws_bytes) break;
-        const int blocks = tiles * s;
-        const int rounds = (blocks + kCUs - 1) / kCUs;
-        // partial-tile traffic costs roughly one extra round fraction per split
-        const double eff = (double)blocks / (rounds * kCUs) * (1.0 - 0.03 * s);
-        if (eff > best_eff + 0.02) { best = s; best_eff = eff; }
+// Launch plan: tile configuration and split-K factor from a rounds cost
+// model.  A 256x256 block (8 waves) occupies a CU alone: 256 tiles per
+// round.  128x128 blocks (4 waves) run two per CU: 512 per round, each
+// round doing half the work of a 256x256 round at about 85% of its
+// per-CU rate (measured on the GPT-2 XL/small Linear shapes).  Cost is in
+// units of one 256x256 K-step (128 bytes): rounds x (K-steps per slice +
+// a fixed per-tile overhead), plus, for split-K, the partial-tile traffic
+// ((S + 1) * M * N fp32 at roughly two K-steps per 10 MB).
+struct GemmPlan {
+    bool big;  // 256x256 (true) or 128x128
+    int split;
+};
+
+static GemmPlan plan_gemm(int M, int N, int K, size_t ws_bytes) {
+    constexpr double kOverheadSteps = 3.0;
+    constexpr double kSmallRate = 0.59;  // (1/2) / 0.85
+    const int nk = (K + kBK - 1) / kBK;
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    const double red_steps_per_byte = 2.0 / 10e6;
+    GemmPlan best{true, 1};
+    double best_cost = 1e300;
+    for (int big = 1; big >= 0; --big) {
+        if (big && (M < 256 || N < 256)) continue;
+        const int64_t tiles = big ? t256 : t128;
+        const int64_t slots = big ? 256 : 512;
+        for (int s = 1; s <= 8; ++s) {
+            if (s > 1 && (nk / s < 4 || (size_t)s * M * N * sizeof(float) > ws_bytes)) break;
+            const double rounds = (double)((tiles * s + slots - 1) / slots);
+            double cost = rounds * ((nk + s - 1) / s + kOverheadSteps) * (big ? 1.0 : kSmallRate);
+            if (s > 1) cost += (double)(s + 1) * M * N * sizeof(float) * red_steps_per_byte;
+            if (cost < best_cost * 0.97) {
+                best_cost = cost;
+                best = GemmPlan{big != 0, s};
+            }
+        }
     }
     return best;
 }
 
-// Tile configuration by output shape: 256x256 blocks (8 waves of 128x64,
-// two per SIMD) when both sides are large, 128x128 (4 waves of 64x64)
-// otherwise.
-static bool use_big_tiles(int M, int N) { return M >= 256 && N >= 256; }
-
-static int plan_split(int M, int N, int K, size_t ws_bytes) {
-    const int bm = use_big_tiles(M, N) ? 256 : 128;
-    const int tiles = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
-    return choose_split(tiles, (K + kBK - 1) / kBK, ws_bytes, (int64_t)M * N);
-}
+static int plan_split(int M, int N, int K, size_t ws_bytes) { return plan_gemm(M, N, K, ws_bytes).split; }
 
 template <int BM, int BN, int WM, int WN, int FA, int FB, typename OutT, typename BiasT>
 static void launch_cfg(const GemmArgs& g) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
     const int nk = (g.K + kBK - 1) / kBK;
-    const int S = plan_split(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0);
+    const int S = plan_gemm(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0).split;
     // vector epilogue stores need 4-element groups to stay aligned
     const bool vec_out = ((int64_t)g.ldc * (int64_t)sizeof(OutT)) % 16 == 0 && aligned16(g.C);
     // buffer-resource ranges are 32-bit byte counts
@@ -511,14 +537,15 @@ static void launch_cfg(const GemmArgs& g) {
             static_cast<OutT*>(g.C), g.ldc, false, g.ws);
     const int64_t total = (int64_t)g.M * g.N;
     int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+    const bool vec_red = (g.N % 4 == 0) && vec_out;
     splitk_reduce_kernel<OutT, BiasT><<<blocks, 256, 0, g.st>>>(g.ws, S_eff, g.M, g.N, g.sa, g.sb,
                                                                 static_cast<const BiasT*>(g.bias),
-                                                                static_cast<OutT*>(g.C), g.ldc);
+                                                                static_cast<OutT*>(g.C), g.ldc, vec_red);
 }
 
 template <int FA, int FB, typename OutT, typename BiasT>
 static void launch_shape(const GemmArgs& g) {
-    if (use_big_tiles(g.M, g.N))
+    if (plan_gemm(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0).big)
         launch_cfg<256, 256, 2, 4, FA, FB, OutT, BiasT>(g);
     else
         launch_cfg<128, 128, 2, 2, FA, FB, OutT, BiasT>(g);

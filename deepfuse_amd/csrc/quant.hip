@@ -399,15 +399,32 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
     }
 }
 
-// out[c] = sum over tile rows of colpart[t][c], in tile order.
+// out[c] = sum over tile rows of colpart[t][c].  A block owns 64 columns;
+// its 4 waves each take every 4th tile row (8 independent loads in flight
+// per thread), then the 4 partial sums are added in wave order -- the same
+// order on every run.
 __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __restrict__ colpart,
                                                                   int tiles, int cols,
                                                                   float* __restrict__ out) {
-    const int c = blockIdx.x * kThreads + threadIdx.x;
-    if (c >= cols) return;
+    __shared__ float part[4][64];
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int w = threadIdx.x >> 6;
     float s = 0.0f;
-    for (int t = 0; t < tiles; ++t) s += colpart[(int64_t)t * cols + c];
-    out[c] = s;
+    if (c < cols) {
+        int t = w;
+        for (; t + 28 < tiles; t += 32) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = colpart[(int64_t)(t + 4 * u) * cols + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; t < tiles; t += 4) s += colpart[(int64_t)t * cols + c];
+    }
+    part[w][threadIdx.x & 63] = s;
+    __syncthreads();
+    if (w == 0 && c < cols)
+        out[c] = ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) + part[3][threadIdx.x];
 }
 
 // --------------------------------------------------------------- launchers --
@@ -623,8 +640,8 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
     }
 #undef DF_Q2D
     if (colsum)
-        colsum_reduce_kernel<<<(cols + kThreads - 1) / kThreads, kThreads, 0, st>>>(part, rows == 0 ? 0 : (rows + kT2 - 1) / kT2,
-                                                                                    cols, colsum);
+        colsum_reduce_kernel<<<(cols + 63) / 64, kThreads, 0, st>>>(part, rows == 0 ? 0 : (rows + kT2 - 1) / kT2,
+                                                                    cols, colsum);
     return launch_status(name);
 }
 

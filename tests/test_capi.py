@@ -1,0 +1,88 @@
+"""The C-ABI library loads, exports every symbol include/df_capi.h declares,
+and rejects bad arguments with status codes before touching a GPU
+(CPU only: none of these calls launches a kernel)."""
+import ctypes
+
+import pytest
+
+import deepfuse_amd as df
+from deepfuse_amd import DType, Fmt
+
+
+def test_exports_every_header_symbol():
+    L = df.lib()
+    names = df.header_functions()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) == set(df._SIGS), "ctypes signature table and header disagree"
+
+
+def test_version_and_sizes():
+    L = df.lib()
+    assert L.df_version() == 100
+    assert L.df_absmax_workspace_bytes() >= 1024
+    assert L.df_quantize_2d_workspace_bytes(16384, 6400) == 128 * 6400 * 4
+    assert L.df_quantize_2d_workspace_bytes(0, 10) == 0
+    # split-K workspace only for outputs too small to fill the GPU
+    assert L.df_fp8_gemm_workspace_bytes(16384, 4800, 1600) == 0
+    assert L.df_fp8_gemm_workspace_bytes(1600, 1600, 16384) > 0
+
+
+def status(fn, *args):
+    return getattr(df.lib(), fn)(*args)
+
+
+def err():
+    return df.lib().df_last_error_string().decode()
+
+
+FAKE = 0x1000  # never dereferenced: each call fails its checks first
+
+
+def test_argument_errors():
+    ws_ok = df.lib().df_absmax_workspace_bytes()
+    assert status("df_quantize_f32_e4m3", None, -1, None, None, None) == -1
+    assert "n < 0" in err()
+    assert status("df_quantize_f32_e4m3", None, 5, None, None, None) == -1
+    assert status("df_quantize_f32_e4m3", FAKE + 4, 5, FAKE, FAKE, None) == -4  # misaligned x
+    assert status("df_quantize_f32_e4m3", None, 0, None, None, None) == 0  # empty is fine
+    assert status("df_dequantize_e4m3_f32", FAKE, 8, FAKE, FAKE + 8, None) == -4
+    assert status("df_absmax_f32", FAKE, 8, FAKE, None, ws_ok, None) == -5  # no workspace
+    assert status("df_absmax_f32", FAKE, 8, FAKE, FAKE, 16, None) == -5      # too small
+    assert status("df_absmax_scale_f32", FAKE, 8, 7, FAKE, FAKE, FAKE, ws_ok, None) == -2  # bad format
+    assert status("df_compute_scale", FAKE, 3, FAKE, None) == -2
+    # 2-D quantize: ld rules
+    assert status("df_quantize_2d", int(DType.FLOAT32), FAKE, 4, 20, 20, 0, FAKE, FAKE, 20, None, 0, None) == -4
+    assert status("df_quantize_2d", int(DType.HALF), FAKE, 4, 4, 4, 0, FAKE, FAKE, 16, None, 0, None) == -2
+    assert status("df_quantize_2d", int(DType.FLOAT32), FAKE, 4, 4, 3, 0, FAKE, FAKE, 16, None, 0, None) == -1
+    assert status("df_quantize_2d_colsum", int(DType.FLOAT32), FAKE, 4, 4, 4, 0, FAKE, None, 0, None, 0,
+                  FAKE, None, 0, None) == -5
+    # GEMM
+    g = df.lib().df_fp8_gemm_nt
+    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 4, 32, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -4  # ld < K
+    assert g(0, FAKE, 24, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -4  # ld % 16
+    assert g(0, FAKE + 8, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -4
+    assert g(0, FAKE, 16, 3, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -2
+    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, int(DType.HALF), FAKE, 4, None, 0, None) == -2
+    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 5, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1  # ldc < N
+    assert g(0, FAKE, 16, 0, FAKE, 16, -1, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1
+    assert g(0, FAKE, 16, 0, FAKE, 16, 0, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == 0  # M = 0
+    # tensor utilities
+    assert status("df_fill", FAKE, 4, 3, ctypes.byref(ctypes.c_int(0)), None) == -2
+    assert status("df_add", 99, FAKE, FAKE, FAKE, 4, None) == -2
+    assert status("df_approx_equal_mask", int(DType.FP8E4M3), FAKE, FAKE, FAKE, 4, 0.1, None) == -2
+
+
+def test_error_raises_in_python_binding():
+    with pytest.raises(df.DFError) as ei:
+        df.call("df_quantize_bf16_e5m2", None, -3, None, None, None)
+    assert ei.value.status == -1
+    assert "n < 0" in str(ei.value)
+
+
+def test_enums_mirror_reference():
+    """OnnxLoader::DType (dnn/utils/onnx_loader.cuh:16-22) values 0-4 kept."""
+    assert [DType.FLOAT32, DType.HALF, DType.INT8, DType.UINT8, DType.BFLOAT16] == [0, 1, 2, 3, 4]
+    assert (DType.FP8E4M3, DType.FP8E5M2) == (5, 6)
+    assert (Fmt.E4M3, Fmt.E5M2) == (0, 1)
