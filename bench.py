@@ -16,8 +16,12 @@ value = GEMM flops of the step (2*M*N*K per GEMM, 12 GEMMs) / step time.
 
 Also reported on the same JSON line:
   roofline     -- the dominant kernel (largest summed time) against fp8 MFMA
-                  peak; durations from HIP events around every launch on the
+                  peak; its average duration comes from a second pass of the
+                  same steps with HIP events around every C-ABI call, on the
                   stream the kernels run on.
+The timed region (value, ms_per_step) is K steps replayed from a HIP graph
+captured once from the same launches (--no-graph: eager launches), with one
+HIP-event pair around the K steps.
   quantize     -- the step's absmax/quantize/colsum kernels against HBM peak.
   conversion   -- config 2 standalone kernels (n = 2^28, fp32 and bf16 in,
                   e4m3 and e5m2) against HBM peak.
@@ -47,6 +51,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-conversion", action="store_true")
     p.add_argument("--cpu-tokens", type=int, default=3072, help="token slice for the CPU baseline")
+    p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="first run one plain 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
     return p.parse_args()
 
 
@@ -98,8 +105,17 @@ def main():
     L = df.lib()
     if L.df_device_arch_ok() != 1:
         raise RuntimeError("device is not gfx950")
-    stream = torch.cuda.current_stream().cuda_stream
     M = M_TOKENS
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # reads and writes 1 GiB
+        torch.cuda.synchronize()
+        del src, dst
+
+    def cur():  # the stream kernels go to (the capture stream while capturing)
+        return torch.cuda.current_stream().cuda_stream
 
     def to_bf16(a):
         return torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
@@ -138,14 +154,14 @@ def main():
 
     def quant(tm, x, rows, cols, fmt, am, sc, q, qt, tag, db=None):
         tm.run("absmax_" + tag, df.call, "df_absmax_scale_bf16", x.data_ptr(), x.numel(), fmt, am, sc,
-               ws.data_ptr(), ws.numel(), stream)
+               ws.data_ptr(), ws.numel(), cur())
         if db is None:
             tm.run("quantize2d_" + tag, df.call, "df_quantize_2d", BF, x.data_ptr(), rows, cols, cols, fmt, sc,
-                   q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), stream)
+                   q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), cur())
         else:
             tm.run("quantize2d_" + tag, df.call, "df_quantize_2d_colsum", BF, x.data_ptr(), rows, cols, cols, fmt,
                    sc, q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), db.data_ptr(), cws.data_ptr(),
-                   cws.numel(), stream)
+                   cws.numel(), cur())
 
     def step(tm):
         for l in layers:
@@ -156,14 +172,14 @@ def main():
             quant(tm, l["W"], N, K, E4, sw_am, sw, l["Wq"], l["Wt"], "weight")
             tm.run("gemm_fwd", df.call, "df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["Xq"].stride(0),
                    l["Wq"].data_ptr(), l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF,
-                   l["Y"].data_ptr(), N, gws.data_ptr(), gws_bytes, stream)
+                   l["Y"].data_ptr(), N, gws.data_ptr(), gws_bytes, cur())
             quant(tm, l["dY"], M, N, E5, sdy_am, sdy, l["dYq"], l["dYt"], "grad", db=l["db"])
             tm.run("gemm_dx", df.call, "df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0),
                    l["Wt"].data_ptr(), l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K,
-                   gws.data_ptr(), gws_bytes, stream)
+                   gws.data_ptr(), gws_bytes, cur())
             tm.run("gemm_dw", df.call, "df_fp8_gemm_bwd_dw", l["dYt"].data_ptr(), l["dYt"].stride(0),
                    l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K,
-                   gws.data_ptr(), gws_bytes, stream)
+                   gws.data_ptr(), gws_bytes, cur())
 
     # algorithmic work per step (unpadded shapes; BASELINE.md counting rules)
     gemm_flops = {"gemm_fwd": 0, "gemm_dx": 0, "gemm_dw": 0}
@@ -183,16 +199,39 @@ def main():
         step(null)
     torch.cuda.synchronize()
 
-    tm = Timer(torch)
+    # Timed region: K steps, one HIP-event pair around all of them.  By
+    # default the step is captured once as a HIP graph (the same kernel
+    # launches, replayed without host launch gaps).
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(null)
+        graph.replay()
+        torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record()
     for _ in range(args.steps):
-        step(tm)
+        if graph is not None:
+            graph.replay()
+        else:
+            step(null)
+    e1.record()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    per = tm.collect()
+    wall = time.perf_counter() - t0
+    elapsed = max(e0.elapsed_time(e1) / 1e3, 1e-9)
     ms_per_step = 1e3 * elapsed / args.steps
     value = step_flops / (elapsed / args.steps) / 1e12
+
+    # Per-kernel durations: the same step launched eagerly with a HIP-event
+    # pair around every C-ABI call, over as many steps as the timed region.
+    tm = Timer(torch)
+    for _ in range(args.steps):
+        step(tm)
+    per = tm.collect()
 
     # dominant kernel = largest summed time; GEMM families are one kernel
     # template each (fwd: e4m3 x e4m3 -> bf16 + bias; dx: e5m2 x e4m3 -> bf16;
@@ -212,6 +251,7 @@ def main():
         roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                 "avg_launch_ms": round(avg_ms, 4), "work_per_launch": work_per_launch}
+    roof["traffic"] = measured_traffic(roof["kernel"])
     kernels = {}
     for k, (t, c) in sorted(per.items()):
         d = {"ms_per_step": round(t / args.steps, 4), "launches_per_step": c // args.steps}
@@ -231,6 +271,7 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8 e4m3/e5m2 (fp32 accumulate)",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, N(0,1e-3) grads; bf16)",
+        "timing": {"region": "hip_graph" if graph is not None else "eager", "wall_s": round(wall, 4)},
         "config": {"workload": "config 4: GPT-2 XL Linears (d=1600) fwd+bwd, M=16384 tokens",
                    "linears": [f"{n} {k}->{o}" for n, k, o in XL_LINEARS], "tokens": M,
                    "step_gemm_flops": step_flops},
@@ -243,10 +284,23 @@ def main():
         "kernels": kernels,
     }
     if not args.no_conversion:
-        out["conversion"] = conversion_bench(torch, df, synth, dev, stream)
+        out["conversion"] = conversion_bench(torch, df, synth, dev, cur())
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
     print(json.dumps(out))
+
+
+def measured_traffic(kernel_family):
+    """HBM bytes per launch of a kernel family from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (profiles/hbm_traffic.json, written from
+    those runs with the copy-kernel scale factor applied), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as fh:
+            data = json.load(fh)
+        return data["families"][kernel_family]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def conversion_bench(torch, df, synth, dev, stream, reps=10):
