@@ -90,6 +90,7 @@ _SIGS = {
                                     _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fill": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp]),
     "df_add": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
+    "df_convert": (_c_int, [_c_int, _vp, _c_int, _vp, _c_i64, _vp]),
     "df_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
     "df_approx_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_f, _vp]),
 }

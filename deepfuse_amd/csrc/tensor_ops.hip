@@ -26,7 +26,14 @@ void set_error(const char* fmt, ...) {
     g_last_error = buf;
 }
 
-void clear_error() { g_last_error.clear(); }
+// Every entry point starts here: besides the message, this resets the HIP
+// runtime's per-thread last error, so that launch_status() reports only
+// what this call's launches raised, not a failed runtime call the caller
+// made earlier (a sticky device fault is still reported, by every call).
+void clear_error() {
+    g_last_error.clear();
+    (void)hipGetLastError();
+}
 
 int launch_status(const char* what) {
     const hipError_t e = hipGetLastError();
@@ -105,6 +112,14 @@ __global__ __launch_bounds__(kThreads) void approx_int_kernel(const T* a, const 
         m[i] = fabsf((float)a[i] - (float)b[i]) <= atol ? 1 : 0;
 }
 
+template <int DI, int DO>
+__global__ __launch_bounds__(kThreads) void convert_kernel(const typename Elem<DI>::T* __restrict__ in,
+                                                            typename Elem<DO>::T* __restrict__ out, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+        out[i] = Elem<DO>::st(Elem<DI>::ld(in[i]));
+}
+
 static int blocks_for(int64_t n) {
     int64_t b = (n + kThreads - 1) / kThreads;
     if (b > 4096) b = 4096;
@@ -140,6 +155,27 @@ extern "C" int df_fill(void* dst, int64_t n, int elem_bytes, const void* value_h
         default: DF_CHECK(false, DF_ERR_UNSUPPORTED, "df_fill: elem_bytes %d", elem_bytes);
     }
     return launch_status("df_fill");
+}
+
+extern "C" int df_convert(int in_dtype, const void* in, int out_dtype, void* out, int64_t n, void* stream) {
+    clear_error();
+    DF_CHECK(n >= 0, DF_ERR_INVALID, "df_convert: n < 0");
+    if (n == 0) return DF_OK;
+    DF_CHECK(in && out, DF_ERR_INVALID, "df_convert: NULL pointer");
+    hipStream_t st = as_stream(stream);
+    const int g = blocks_for(n);
+#define DF_CVT(I, O)                                                                                  \
+    if (in_dtype == I && out_dtype == O) {                                                            \
+        convert_kernel<I, O><<<g, kThreads, 0, st>>>((const typename Elem<I>::T*)in, (typename Elem<O>::T*)out, n); \
+        return launch_status("df_convert");                                                           \
+    }
+    DF_CVT(DF_DTYPE_FLOAT32, DF_DTYPE_FLOAT32)
+    DF_CVT(DF_DTYPE_FLOAT32, DF_DTYPE_BFLOAT16)
+    DF_CVT(DF_DTYPE_FLOAT32, DF_DTYPE_HALF)
+    DF_CVT(DF_DTYPE_BFLOAT16, DF_DTYPE_FLOAT32)
+    DF_CVT(DF_DTYPE_HALF, DF_DTYPE_FLOAT32)
+#undef DF_CVT
+    DF_CHECK(false, DF_ERR_UNSUPPORTED, "df_convert: %d -> %d not supported", in_dtype, out_dtype);
 }
 
 extern "C" int df_add(int dtype, const void* a, const void* b, void* out, int64_t n, void* stream) {

@@ -1,0 +1,61 @@
+// dnn/layers/fully_connected_layer.hpp -- the fp8 Linear layer (drop-in).
+//
+// Public contract of the reference's FullyConnectedLayer<TT>
+// (dnn/layers/fully_connected_layer.cuh:21-52, .cu:111-402): W is
+// [out, in], bias [1, out, 1, 1], input [N, in] -> output [N, out];
+// forward caches what backward needs when training is enabled; backward
+// returns dX [N, in] and overwrites grad_weights [out, in] and grad_bias;
+// backward without training (or before a forward) throws; save/load write
+// in, out, weights, bias.
+//
+// Compute is fp8 on CDNA4 MFMA through the C ABI: forward quantizes X and
+// W to e4m3 (per-tensor absmax scales) and runs Y = Xq . Wq^T * sx * sw + b;
+// backward quantizes dY to e5m2 (its column sums give grad_bias in the same
+// pass), dX = dYq . W * sdy * sw, dW = dYq^T . X * sdy * sx, all with fp32
+// accumulation.  Instead of a full clone of the input, training caches the
+// transposed e4m3 codes of X (one byte per element) and their scale.
+// TT: float or bfloat16.
+#pragma once
+
+#include <iostream>
+#include <optional>
+#include <string>
+
+#include "dnn/core/layer.hpp"
+#include "dnn/core/tensor.hpp"
+
+namespace dnn {
+
+template <typename TT>
+class FullyConnectedLayer : public LayerWeightBias<TT> {
+public:
+    FullyConnectedLayer(int in_features, int out_features, bool training_enabled = false);
+    ~FullyConnectedLayer() override = default;
+
+    tensor<TT> forward(const tensor<TT>& input) override;
+    tensor<TT> backward(const tensor<TT>& grad_output) override;
+
+    std::string name() const override { return "FullyConnected"; }
+    void initialize_weights() override;
+    void save(std::ostream& out) const override;
+    void load(std::istream& in) override;
+
+private:
+    // device scratch reused across calls, grown on demand
+    struct Scratch {
+        uint8_t* p = nullptr;
+        size_t bytes = 0;
+        ~Scratch();
+        uint8_t* get(size_t n, bool zeroed = false);
+    };
+    void quantize_operand(const TT* x, int rows, int cols, int fmt, float* scale_dev, uint8_t* q, int ldq,
+                          uint8_t* qt, int ldqt, float* colsum);
+
+    int in_features_;
+    int out_features_;
+    int cached_n_ = -1;                        // tokens of the cached forward
+    std::optional<tensor<fp8_e4m3>> xt_cache_;  // X^T codes [in, round16(N)] + scale
+    Scratch absmax_ws_, colsum_ws_, gemm_ws_, codes_a_, codes_b_, codes_c_, scales_, colsum_;
+};
+
+}  // namespace dnn

@@ -1,0 +1,186 @@
+// FullyConnectedLayer<TT> in fp8 compute (the reference's
+// dnn/layers/fully_connected_layer.cu:110-406), all device work through the
+// C ABI on Hip::stream().
+#include "dnn/layers/fully_connected_layer.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <random>
+#include <stdexcept>
+#include <type_traits>
+#include <vector>
+
+#include "dnn/core/hip.hpp"
+#include "dnn/utils/common.hpp"
+
+namespace dnn {
+
+namespace {
+inline int round16(int v) { return (v + 15) & ~15; }
+inline void* st() { return reinterpret_cast<void*>(Hip::stream()); }
+}  // namespace
+
+template <typename TT>
+FullyConnectedLayer<TT>::Scratch::~Scratch() {
+    if (p) (void)hipFree(p);
+}
+
+template <typename TT>
+uint8_t* FullyConnectedLayer<TT>::Scratch::get(size_t n, bool zeroed) {
+    if (n == 0) n = 16;
+    if (n > bytes) {
+        if (p) {
+            CHECK_HIP_EX(hipStreamSynchronize(Hip::stream()));  // previous users are done
+            CHECK_HIP_EX(hipFree(p));
+            p = nullptr;
+        }
+        const size_t alloc = (n + 255) & ~size_t(255);
+        CHECK_HIP_EX(hipMalloc(&p, alloc));
+        if (zeroed) CHECK_HIP_EX(hipMemset(p, 0, alloc));
+        bytes = alloc;
+    }
+    return p;
+}
+
+template <typename TT>
+FullyConnectedLayer<TT>::FullyConnectedLayer(int in_features, int out_features, bool training_enabled)
+    : LayerWeightBias<TT>(tensor<TT>({out_features, in_features}), tensor<TT>({1, out_features, 1, 1}),
+                          tensor<TT>({out_features, in_features}), tensor<TT>({1, out_features, 1, 1}),
+                          training_enabled),
+      in_features_(in_features),
+      out_features_(out_features) {
+    if (in_features <= 0 || out_features <= 0) throw std::invalid_argument("FullyConnectedLayer: bad sizes");
+    initialize_weights();
+}
+
+// Xavier/Glorot uniform weights, zero bias (reference :359-385).
+template <typename TT>
+void FullyConnectedLayer<TT>::initialize_weights() {
+    std::random_device rd;
+    std::mt19937 gen(rd());
+    const float limit = std::sqrt(6.0f / (in_features_ + out_features_));
+    std::uniform_real_distribution<float> dist(-limit, limit);
+    std::vector<TT> w(this->weights_.size());
+    std::vector<TT> b(this->bias_.size());
+    for (auto& v : w) v = static_cast<TT>(dist(gen));
+    for (auto& v : b) v = static_cast<TT>(0.0f);
+    this->weights_.upload(w.data());
+    this->bias_.upload(b.data());
+}
+
+// absmax -> scale (written to scale_dev) -> 2-D codes (row copy q, transposed
+// copy qt, optional fp32 column sums), all stream ordered.
+template <typename TT>
+void FullyConnectedLayer<TT>::quantize_operand(const TT* x, int rows, int cols, int fmt, float* scale_dev, uint8_t* q,
+                                               int ldq, uint8_t* qt, int ldqt, float* colsum) {
+    constexpr int dt = dtype_traits<TT>::value;
+    const size_t ab = df_absmax_workspace_bytes();
+    uint8_t* aws = absmax_ws_.get(ab);
+    const int64_t n = (int64_t)rows * cols;
+    if constexpr (std::is_same_v<TT, float>)
+        CHECK_DF_EX(df_absmax_scale_f32(x, n, fmt, nullptr, scale_dev, aws, ab, st()));
+    else
+        CHECK_DF_EX(df_absmax_scale_bf16(reinterpret_cast<const uint16_t*>(x), n, fmt, nullptr, scale_dev, aws, ab,
+                                         st()));
+    if (colsum) {
+        const size_t cb = df_quantize_2d_workspace_bytes(rows, cols);
+        CHECK_DF_EX(df_quantize_2d_colsum(dt, x, rows, cols, cols, fmt, scale_dev, q, ldq, qt, ldqt, colsum,
+                                          colsum_ws_.get(cb), cb, st()));
+    } else {
+        CHECK_DF_EX(df_quantize_2d(dt, x, rows, cols, cols, fmt, scale_dev, q, ldq, qt, ldqt, st()));
+    }
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input) {
+    const auto& sh = input.shape();
+    if (sh.size() != 2 || sh[1] != in_features_)
+        throw std::invalid_argument("FullyConnectedLayer::forward: input must be [N, " +
+                                    std::to_string(in_features_) + "], got " + input.to_string());
+    const int N = sh[0];
+    tensor<TT> output({N, out_features_});
+    if (N == 0) return output;
+    constexpr int dt = dtype_traits<TT>::value;
+    const int Kp = round16(in_features_), Np = round16(N);
+    float* sc = reinterpret_cast<float*>(scales_.get(4 * sizeof(float)));
+    uint8_t* xq = codes_a_.get((size_t)N * Kp);
+    uint8_t* xt = nullptr;
+    float* sx = sc;
+    if (this->training_enabled_) {
+        const std::vector<int> xt_shape{in_features_, Np};
+        if (!xt_cache_ || xt_cache_->shape() != xt_shape) xt_cache_.emplace(xt_shape);
+        xt = reinterpret_cast<uint8_t*>(xt_cache_->data());
+        sx = xt_cache_->scale_data();
+    }
+    quantize_operand(input.data(), N, in_features_, DF_FMT_E4M3, sx, xq, Kp, xt, Np, nullptr);
+    uint8_t* wq = codes_b_.get((size_t)out_features_ * Kp);
+    quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, wq, Kp, nullptr, 0,
+                     nullptr);
+    const size_t gb = df_fp8_gemm_workspace_bytes(N, out_features_, in_features_);
+    CHECK_DF_EX(df_fp8_gemm_fwd(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sc + 1, dt, this->bias_.data(), dt,
+                                output.data(), out_features_, gemm_ws_.get(gb), gb, st()));
+    cached_n_ = this->training_enabled_ ? N : -1;
+    return output;
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
+    if (!this->training_enabled_)
+        throw std::runtime_error("FullyConnectedLayer: backward called without input argument in stateless mode");
+    if (!xt_cache_ || cached_n_ < 0)
+        throw std::runtime_error("FullyConnectedLayer: input_cache_ not set for backward");
+    const int N = cached_n_;
+    const auto& sh = grad_output.shape();
+    if (sh.size() != 2 || sh[0] != N || sh[1] != out_features_)
+        throw std::invalid_argument("FullyConnectedLayer::backward: grad_output must be [" + std::to_string(N) + ", " +
+                                    std::to_string(out_features_) + "], got " + grad_output.to_string());
+    constexpr int dt = dtype_traits<TT>::value;
+    const int Np = round16(N), Op = round16(out_features_);
+    float* sc = reinterpret_cast<float*>(scales_.get(4 * sizeof(float)));
+    // dY -> e5m2 row copy (for dX), transposed copy (for dW), and db
+    uint8_t* dyq = codes_a_.get((size_t)N * Op);
+    uint8_t* dyt = codes_c_.get((size_t)out_features_ * Np);
+    float* db = reinterpret_cast<float*>(colsum_.get((size_t)out_features_ * sizeof(float)));
+    quantize_operand(grad_output.data(), N, out_features_, DF_FMT_E5M2, sc + 2, dyq, Op, dyt, Np, db);
+    // the current weights (reference: backward reads weights_), transposed
+    uint8_t* wt = codes_b_.get((size_t)in_features_ * Op);
+    quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, nullptr, 0, wt, Op,
+                     nullptr);
+    tensor<TT> grad_input({N, in_features_});
+    const size_t gb = std::max(df_fp8_gemm_workspace_bytes(N, in_features_, out_features_),
+                               df_fp8_gemm_workspace_bytes(out_features_, in_features_, N));
+    uint8_t* gws = gemm_ws_.get(gb);
+    CHECK_DF_EX(df_fp8_gemm_bwd_dx(dyq, Op, wt, Op, N, out_features_, in_features_, sc + 2, sc + 1, dt,
+                                   grad_input.data(), in_features_, gws, gb, st()));
+    CHECK_DF_EX(df_fp8_gemm_bwd_dw(dyt, Np, reinterpret_cast<const uint8_t*>(xt_cache_->data()), Np, N,
+                                   out_features_, in_features_, sc + 2, xt_cache_->scale_data(), dt,
+                                   this->grad_weights_.data(), in_features_, gws, gb, st()));
+    CHECK_DF_EX(df_convert(DF_DTYPE_FLOAT32, db, dt, this->grad_bias_.data(), out_features_, st()));
+    return grad_input;
+}
+
+template <typename TT>
+void FullyConnectedLayer<TT>::save(std::ostream& out) const {
+    out.write(reinterpret_cast<const char*>(&in_features_), sizeof(in_features_));
+    out.write(reinterpret_cast<const char*>(&out_features_), sizeof(out_features_));
+    this->weights_.save(out);
+    this->bias_.save(out);
+}
+
+template <typename TT>
+void FullyConnectedLayer<TT>::load(std::istream& in) {
+    in.read(reinterpret_cast<char*>(&in_features_), sizeof(in_features_));
+    in.read(reinterpret_cast<char*>(&out_features_), sizeof(out_features_));
+    this->weights_.load(in);
+    this->bias_.load(in);
+    if (this->grad_weights_.shape() != this->weights_.shape())
+        this->grad_weights_ = tensor<TT>(this->weights_.shape());
+    if (this->grad_bias_.shape() != this->bias_.shape()) this->grad_bias_ = tensor<TT>(this->bias_.shape());
+    xt_cache_.reset();
+    cached_n_ = -1;
+}
+
+template class FullyConnectedLayer<float>;
+template class FullyConnectedLayer<bfloat16>;
+
+}  // namespace dnn

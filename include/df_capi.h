@@ -188,6 +188,9 @@ int df_add(int dtype, const void* a, const void* b, void* out, int64_t n, void* 
 /* equal_kernel (tensor.cu:39): mask[i] = bitwise a[i] == b[i] (per element) */
 int df_equal_mask(int dtype, const void* a, const void* b, uint8_t* mask, int64_t n,
                   void* stream);
+/* elementwise cast (RNE), fp32 <-> bf16 and fp32 <-> f16; the reference's
+ * utils::to_float / to_half (dnn/utils/convert.cu:6-27) as a tensor op */
+int df_convert(int in_dtype, const void* in, int out_dtype, void* out, int64_t n, void* stream);
 /* approx_equal_kernel (tensor.cu:46): mask[i] = |a[i]-b[i]| <= atol, in fp32 */
 int df_approx_equal_mask(int dtype, const void* a, const void* b, uint8_t* mask,
                          int64_t n, float atol, void* stream);

@@ -1,0 +1,679 @@
+// C++ drop-in tests (namespace dnn), shaped like the reference's GTest
+// suites: tests/core/cuda_test.cu (-> HipTest), tests/core/tensor_test.cu
+// (-> TensorTest), tests/layers/fully_connected_layer_test.cu
+// (-> FullyConnectedLayerTest), plus the fp8 tensor conversions.
+//
+// Expected values of the fp8 path come from the CPU oracle
+// (oracle/libdf_oracle.so): the operands are quantized and dequantized by
+// the oracle and the reference's fp32 loops run on them.  Where the
+// reference's test checks the fp32 product to 1e-5, these tests check the
+// fp8 product to the same 1e-5 and the fp32 product to the fp8 error bound.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <random>
+#include <sstream>
+#include <thread>
+#include <vector>
+
+#include "df_oracle.h"
+#include "dnn/core/hip.hpp"
+#include "dnn/core/tensor.hpp"
+#include "dnn/layers/fully_connected_layer.hpp"
+#include "mini_test.hpp"
+
+using namespace dnn;
+
+namespace {
+
+std::vector<float> uniform(size_t n, float lo, float hi, unsigned seed) {
+    std::mt19937 g(seed);
+    std::uniform_real_distribution<float> d(lo, hi);
+    std::vector<float> v(n);
+    for (auto& x : v) x = d(g);
+    return v;
+}
+
+// oracle: per-tensor absmax quantize then dequantize (the values the GEMM sees)
+std::vector<float> fp8_values(const std::vector<float>& x, int fmt) {
+    const int64_t n = (int64_t)x.size();
+    const float s = dfo_scale(dfo_absmax_f32(x.data(), n), fmt);
+    std::vector<uint8_t> q(n);
+    std::vector<float> d(n);
+    dfo_quantize_f32(x.data(), n, s, fmt, q.data());
+    dfo_dequantize_f32(q.data(), n, s, fmt, d.data());
+    return d;
+}
+
+std::vector<float> bf16_to_float(const std::vector<uint16_t>& h) {
+    std::vector<float> f(h.size());
+    for (size_t i = 0; i < h.size(); ++i) f[i] = dfo_bf16_to_f32(h[i]);
+    return f;
+}
+
+std::vector<uint16_t> float_to_bf16(const std::vector<float>& f) {
+    std::vector<uint16_t> h(f.size());
+    for (size_t i = 0; i < f.size(); ++i) h[i] = dfo_f32_to_bf16(f[i]);
+    return h;
+}
+
+// max|y - r| / max|r|: the normwise relative error of the fp8 GEMM contract
+double rel_err(const std::vector<float>& y, const std::vector<float>& r) {
+    double num = 0, den = 0;
+    for (size_t i = 0; i < r.size(); ++i) {
+        num = std::max(num, (double)std::fabs(y[i] - r[i]));
+        den = std::max(den, (double)std::fabs(r[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+template <typename TT>
+std::vector<TT> download(const tensor<TT>& t) {
+    std::vector<TT> h(t.size());
+    t.download(h.data());
+    return h;
+}
+
+std::vector<float> download_f(const tensor<bfloat16>& t) {
+    std::vector<uint16_t> h(t.size());
+    t.download(reinterpret_cast<bfloat16*>(h.data()));
+    return bf16_to_float(h);
+}
+
+void upload_bf16(tensor<bfloat16>& t, const std::vector<float>& v) {
+    const auto h = float_to_bf16(v);
+    t.upload(reinterpret_cast<const bfloat16*>(h.data()));
+}
+
+class HipFixture : public mini_test::Test {
+protected:
+    std::unique_ptr<Hip> hip_;
+    void SetUp() override {
+        hip_ = std::make_unique<Hip>(0);
+        (void)hipDeviceSynchronize();
+    }
+    void TearDown() override {
+        (void)hipDeviceSynchronize();
+        hip_.reset();
+        Hip::set_stream(nullptr);
+    }
+};
+
+using HipTest = HipFixture;
+using TensorTest = HipFixture;
+using Fp8TensorTest = HipFixture;
+using FullyConnectedLayerTest = HipFixture;
+
+}  // namespace
+
+// ============================================================== HipTest ==
+TEST_F(HipTest, Constructor) {
+    EXPECT_NO_THROW({
+        Hip hip;
+        EXPECT_EQ(hip.id(), 0);
+    });
+    int device_count = 0;
+    (void)hipGetDeviceCount(&device_count);
+    EXPECT_THROW(Hip hip(device_count), std::runtime_error);
+    (void)hipSetDevice(0);
+}
+
+TEST_F(HipTest, CurrentInstance) {
+    hip_.reset();
+    {
+        Hip h1(0);
+        EXPECT_EQ(&Hip::current(), &h1);
+        {
+            Hip h2(0);
+            EXPECT_EQ(&Hip::current(), &h2);
+        }
+    }
+    EXPECT_THROW(Hip::current(), std::runtime_error);
+}
+
+TEST_F(HipTest, GetDevices) {
+    const auto& devices = Hip::get_devices();
+    int device_count = 0;
+    (void)hipGetDeviceCount(&device_count);
+    EXPECT_EQ((int)devices.size(), device_count);
+    for (size_t i = 0; i < devices.size(); ++i) {
+        EXPECT_EQ(devices[i].id(), (int)i);
+        EXPECT_FALSE(devices[i].name().empty());
+        EXPECT_EQ(devices[i].architecture_name().rfind("gfx950", 0), 0u);
+        EXPECT_GT(devices[i].num_sm(), 0);
+        EXPECT_GT(devices[i].available_memory_bytes(), 0u);
+    }
+}
+
+TEST_F(HipTest, DumpInfo) {
+    Hip hip;
+    std::stringstream ss;
+    hip.dump_info(ss);
+    const std::string info = ss.str();
+    EXPECT_TRUE(info.find("[HIP System Summary]") != std::string::npos);
+    EXPECT_TRUE(info.find("HIP Device") != std::string::npos);
+}
+
+TEST_F(HipTest, ThreadSafety) {
+    Hip* seen[2] = {nullptr, nullptr};
+    std::thread t1([&] {
+        Hip h(0);
+        seen[0] = &Hip::current();
+    });
+    std::thread t2([&] {
+        Hip h(0);
+        seen[1] = &Hip::current();
+    });
+    t1.join();
+    t2.join();
+    EXPECT_NE(seen[0], nullptr);
+    EXPECT_NE(seen[1], nullptr);
+    EXPECT_EQ(&Hip::current(), hip_.get());  // other threads leave ours alone
+}
+
+TEST_F(HipTest, DefaultStreamIsLegacy) { EXPECT_EQ(Hip::stream(), hipStreamLegacy); }
+
+TEST_F(HipTest, SetAndGetStream) {
+    hipStream_t s;
+    ASSERT_EQ(hipStreamCreate(&s), hipSuccess);
+    Hip::set_stream(s);
+    EXPECT_EQ(Hip::stream(), s);
+    Hip::set_stream(nullptr);
+    EXPECT_EQ(Hip::stream(), hipStreamLegacy);
+    (void)hipStreamDestroy(s);
+}
+
+TEST_F(HipTest, StreamGuardRestoresPreviousStream) {
+    hipStream_t s1, s2;
+    ASSERT_EQ(hipStreamCreate(&s1), hipSuccess);
+    ASSERT_EQ(hipStreamCreate(&s2), hipSuccess);
+    Hip::set_stream(s1);
+    EXPECT_EQ(Hip::stream(), s1);
+    {
+        StreamGuard guard(s2);
+        EXPECT_EQ(Hip::stream(), s2);
+    }
+    EXPECT_EQ(Hip::stream(), s1);
+    Hip::set_stream(nullptr);
+    (void)hipStreamDestroy(s1);
+    (void)hipStreamDestroy(s2);
+}
+
+// =========================================================== TensorTest ==
+TEST_F(TensorTest, ConstructorAndShape) {
+    std::vector<int> shape = {2, 3, 4};
+    tensor<float> t(shape);
+    EXPECT_TRUE(t.shape() == shape);
+    EXPECT_EQ(t.size(), 24);
+    EXPECT_EQ(t.size(0), 2);
+    EXPECT_EQ(t.size(1), 3);
+    EXPECT_EQ(t.size(2), 4);
+    EXPECT_THROW(t.size(3), std::out_of_range);
+}
+
+TEST_F(TensorTest, UploadDownload) {
+    tensor<float> t({2, 2});
+    std::vector<float> host = {1.0f, 2.0f, 3.0f, 4.0f};
+    t.upload(host.data());
+    const auto back = download(t);
+    for (size_t i = 0; i < host.size(); ++i) EXPECT_FLOAT_EQ(host[i], back[i]);
+}
+
+TEST_F(TensorTest, FillAndZero) {
+    tensor<float> t({2, 2});
+    t.fill(1.0f);
+    for (float v : download(t)) EXPECT_FLOAT_EQ(v, 1.0f);
+    t.zero();
+    for (float v : download(t)) EXPECT_FLOAT_EQ(v, 0.0f);
+    tensor<bfloat16> b({3, 5});
+    b.fill(__float2bfloat16(-2.5f));
+    for (float v : download_f(b)) EXPECT_FLOAT_EQ(v, -2.5f);
+    tensor<fp8_e4m3> q({7});
+    q.fill(fp8_e4m3(0x3C));
+    for (auto v : download(q)) EXPECT_EQ((int)v.bits, 0x3C);
+}
+
+// a failed runtime call the caller made earlier is not reported by the
+// next C-ABI launch (the library resets the per-thread last error)
+TEST_F(TensorTest, FillAfterFailedRuntimeCall) {
+    int device_count = 0;
+    (void)hipGetDeviceCount(&device_count);
+    EXPECT_NE(hipSetDevice(device_count), hipSuccess);
+    tensor<float> t({5});
+    EXPECT_NO_THROW(t.fill(3.0f));
+    for (float v : download(t)) EXPECT_FLOAT_EQ(v, 3.0f);
+}
+
+TEST_F(TensorTest, Reshape) {
+    tensor<float> t({2, 2});
+    std::vector<int> new_shape = {4, 1};
+    t.reshape(new_shape);
+    EXPECT_TRUE(t.shape() == new_shape);
+    EXPECT_EQ(t.size(), 4);
+    EXPECT_THROW(t.reshape({3, 2}), std::runtime_error);
+}
+
+TEST_F(TensorTest, MoveSemantics) {
+    tensor<float> t1({2, 2});
+    std::vector<float> host = {1.0f, 2.0f, 3.0f, 4.0f};
+    t1.upload(host.data());
+    tensor<float> t2(std::move(t1));
+    EXPECT_EQ(t1.data(), nullptr);
+    EXPECT_NE(t2.data(), nullptr);
+    const auto back = download(t2);
+    for (size_t i = 0; i < host.size(); ++i) EXPECT_FLOAT_EQ(host[i], back[i]);
+    tensor<float> t3({2, 2});
+    t3 = std::move(t2);
+    EXPECT_EQ(t2.data(), nullptr);
+    EXPECT_NE(t3.data(), nullptr);
+}
+
+TEST_F(TensorTest, Addition) {
+    tensor<float> t1({2, 2}), t2({2, 2});
+    std::vector<float> a = {1.0f, 2.0f, 3.0f, 4.0f}, b = {5.0f, 6.0f, 7.0f, 8.0f};
+    t1.upload(a.data());
+    t2.upload(b.data());
+    tensor<float> t3 = t1 + t2;
+    const auto r = download(t3);
+    EXPECT_FLOAT_EQ(r[0], 6.0f);
+    EXPECT_FLOAT_EQ(r[1], 8.0f);
+    EXPECT_FLOAT_EQ(r[2], 10.0f);
+    EXPECT_FLOAT_EQ(r[3], 12.0f);
+}
+
+TEST_F(TensorTest, InPlaceAddition) {
+    tensor<float> t1({2, 2}), t2({2, 2});
+    std::vector<float> a = {1.0f, 2.0f, 3.0f, 4.0f}, b = {5.0f, 6.0f, 7.0f, 8.0f};
+    t1.upload(a.data());
+    t2.upload(b.data());
+    t1 += t2;
+    const auto r = download(t1);
+    EXPECT_FLOAT_EQ(r[0], 6.0f);
+    EXPECT_FLOAT_EQ(r[1], 8.0f);
+    EXPECT_FLOAT_EQ(r[2], 10.0f);
+    EXPECT_FLOAT_EQ(r[3], 12.0f);
+}
+
+TEST_F(TensorTest, ShapeMismatchAddition) {
+    tensor<float> t1({2, 2}), t2({2, 3});
+    EXPECT_THROW(t1 + t2, std::runtime_error);
+    EXPECT_THROW(t1 += t2, std::runtime_error);
+}
+
+TEST_F(TensorTest, Clone) {
+    tensor<float> t1({2, 2});
+    std::vector<float> host = {1.0f, 2.0f, 3.0f, 4.0f};
+    t1.upload(host.data());
+    tensor<float> t2 = t1.clone();
+    EXPECT_TRUE(t2.shape() == t1.shape());
+    EXPECT_NE(t2.data(), t1.data());
+    const auto back = download(t2);
+    for (size_t i = 0; i < host.size(); ++i) EXPECT_FLOAT_EQ(host[i], back[i]);
+}
+
+TEST_F(TensorTest, Equals) {
+    tensor<float> t1({2, 2}), t2({2, 2}), t3({2, 2});
+    std::vector<float> a = {1.0f, 2.0f, 3.0f, 4.0f}, b = {1.0f, 2.0f, 3.0f, 5.0f};
+    t1.upload(a.data());
+    t2.upload(a.data());
+    t3.upload(b.data());
+    EXPECT_TRUE(t1.equals(t2));
+    EXPECT_FALSE(t1.equals(t3));
+    const auto mask = download(t1 == t3);
+    EXPECT_EQ((int)mask[0], 1);
+    EXPECT_EQ((int)mask[3], 0);
+}
+
+TEST_F(TensorTest, ApproxEqual) {
+    tensor<float> t1({2, 2}), t2({2, 2});
+    std::vector<float> a = {1.0f, 2.0f, 3.0f, 4.0f}, b = {1.001f, 2.001f, 3.001f, 4.001f};
+    t1.upload(a.data());
+    t2.upload(b.data());
+    EXPECT_TRUE(t1.approx_equal(t2, 0.01f));
+    EXPECT_FALSE(t1.approx_equal(t2, 0.0001f));
+}
+
+TEST_F(TensorTest, SaveLoad) {
+    tensor<float> t({3, 2});
+    std::vector<float> host = {1, -2, 3.5f, 0, 7, -0.25f};
+    t.upload(host.data());
+    std::stringstream ss;
+    t.save(ss);
+    tensor<float> u({1});
+    u.load(ss);
+    EXPECT_TRUE(u.shape() == t.shape());
+    EXPECT_TRUE(u.equals(t));
+}
+
+// ======================================================== Fp8TensorTest ==
+// quantize / dequantize through the drop-in vs the oracle, bit for bit
+TEST_F(Fp8TensorTest, QuantizeFloatMatchesOracle) {
+    const int n = 4099;
+    auto x = uniform(n, -3.0f, 3.0f, 11);
+    x[0] = NAN;
+    x[1] = INFINITY;
+    x[2] = -INFINITY;
+    x[3] = -0.0f;
+    x[4] = 1e-30f;
+    x[5] = 2.9999f * 1e6f;  // absmax well above the rest
+    tensor<float> t({n});
+    t.upload(x.data());
+    for (int fmt : {DFO_E4M3, DFO_E5M2}) {
+        const float s = dfo_scale(dfo_absmax_f32(x.data(), n), fmt);
+        std::vector<uint8_t> expect(n);
+        dfo_quantize_f32(x.data(), n, s, fmt, expect.data());
+        std::vector<uint8_t> got(n);
+        float got_s;
+        if (fmt == DFO_E4M3) {
+            auto q = quantize<fp8_e4m3>(t);
+            q.download(reinterpret_cast<fp8_e4m3*>(got.data()));
+            got_s = q.scale();
+        } else {
+            auto q = quantize<fp8_e5m2>(t);
+            q.download(reinterpret_cast<fp8_e5m2*>(got.data()));
+            got_s = q.scale();
+        }
+        EXPECT_EQ(got_s, s);
+        int mismatches = 0;
+        for (int i = 0; i < n; ++i) mismatches += got[i] != expect[i];
+        EXPECT_EQ(mismatches, 0);
+    }
+}
+
+TEST_F(Fp8TensorTest, QuantizeBFloat16MatchesOracle) {
+    const int n = 1000;
+    const auto xf = uniform(n, -50.0f, 50.0f, 12);
+    const auto xh = float_to_bf16(xf);
+    tensor<bfloat16> t({10, 100});
+    t.upload(reinterpret_cast<const bfloat16*>(xh.data()));
+    auto q = quantize<fp8_e5m2>(t);
+    EXPECT_TRUE(q.shape() == t.shape());
+    const float s = dfo_scale(dfo_absmax_bf16(xh.data(), n), DFO_E5M2);
+    std::vector<uint8_t> expect(n), got(n);
+    dfo_quantize_bf16(xh.data(), n, s, DFO_E5M2, expect.data());
+    q.download(reinterpret_cast<fp8_e5m2*>(got.data()));
+    EXPECT_EQ(q.scale(), s);
+    EXPECT_TRUE(got == expect);
+}
+
+TEST_F(Fp8TensorTest, DequantizeMatchesOracle) {
+    // every code, at a non-unit scale
+    tensor<fp8_e4m3> q({256});
+    std::vector<uint8_t> codes(256);
+    for (int i = 0; i < 256; ++i) codes[i] = (uint8_t)i;
+    q.upload(reinterpret_cast<const fp8_e4m3*>(codes.data()));
+    q.set_scale(0.0371f);
+    const auto f = download(dequantize<float>(q));
+    const auto b = download_f(dequantize<bfloat16>(q));
+    std::vector<float> ef(256);
+    std::vector<uint16_t> eb(256);
+    dfo_dequantize_f32(codes.data(), 256, 0.0371f, DFO_E4M3, ef.data());
+    dfo_dequantize_bf16(codes.data(), 256, 0.0371f, DFO_E4M3, eb.data());
+    int bad = 0;
+    for (int i = 0; i < 256; ++i) {
+        uint32_t a, e;
+        std::memcpy(&a, &f[i], 4);
+        std::memcpy(&e, &ef[i], 4);
+        bad += a != e;
+        const uint16_t bb = dfo_f32_to_bf16(b[i]);
+        bad += bb != eb[i];
+    }
+    EXPECT_EQ(bad, 0);
+}
+
+TEST_F(Fp8TensorTest, RoundTripWithinHalfUlp) {
+    const int n = 2048;
+    const auto x = uniform(n, -1.0f, 1.0f, 13);
+    tensor<float> t({n});
+    t.upload(x.data());
+    const auto back = download(dequantize<float>(quantize<fp8_e4m3>(t)));
+    const float s = dfo_scale(dfo_absmax_f32(x.data(), n), DFO_E4M3);
+    for (int i = 0; i < n; ++i) {
+        // e4m3 has 3 fraction bits: |x - q| <= 2^-4 |x| in the normal
+        // range, and <= 2^-10 * s (half the subnormal step) below it
+        EXPECT_LE(std::fabs(back[i] - x[i]), std::max(std::fabs(x[i]) * 0.0625f, s * 0.0009766f) * 1.0001f);
+    }
+}
+
+TEST_F(Fp8TensorTest, SaveLoadKeepsScale) {
+    tensor<float> t({4, 4});
+    const auto x = uniform(16, -9.0f, 9.0f, 14);
+    t.upload(x.data());
+    auto q = quantize<fp8_e4m3>(t);
+    std::stringstream ss;
+    q.save(ss);
+    tensor<fp8_e4m3> r({1});
+    r.load(ss);
+    EXPECT_TRUE(r.equals(q));
+    EXPECT_EQ(r.scale(), q.scale());
+    EXPECT_THROW(q += r, std::runtime_error);
+}
+
+// ============================================== FullyConnectedLayerTest ==
+TEST_F(FullyConnectedLayerTest, ConstructorAndInitialization) {
+    const int in_features = 4, out_features = 3;
+    FullyConnectedLayer<float> layer(in_features, out_features, true);
+    auto params = layer.parameters();
+    EXPECT_EQ(params.size(), 2u);
+    EXPECT_EQ(params[0]->shape()[0], out_features);
+    EXPECT_EQ(params[0]->shape()[1], in_features);
+    EXPECT_EQ(params[1]->shape()[1], out_features);
+    EXPECT_EQ(layer.name(), std::string("FullyConnected"));
+    // Xavier uniform weights, zero bias
+    const float limit = std::sqrt(6.0f / (in_features + out_features));
+    for (float w : download(*params[0])) EXPECT_LE(std::fabs(w), limit);
+    for (float b : download(*params[1])) EXPECT_EQ(b, 0.0f);
+}
+
+TEST_F(FullyConnectedLayerTest, ForwardPass) {
+    const int in_features = 4, out_features = 3;
+    FullyConnectedLayer<float> layer(in_features, out_features, true);
+    tensor<float> input({1, in_features});
+    std::vector<float> x(in_features);
+    for (int i = 0; i < in_features; ++i) x[i] = static_cast<float>(i) / in_features;
+    input.upload(x.data());
+    auto params = layer.parameters();
+    const auto w = download(*params[0]);
+    const auto b = download(*params[1]);
+    tensor<float> output = layer.forward(input);
+    const auto y = download(output);
+
+    std::vector<float> expect(out_features), exact(out_features);
+    dfo_fc_forward(fp8_values(x, DFO_E4M3).data(), fp8_values(w, DFO_E4M3).data(), b.data(), expect.data(), 1,
+                   in_features, out_features, 1);
+    dfo_fc_forward(x.data(), w.data(), b.data(), exact.data(), 1, in_features, out_features, 1);
+    for (int i = 0; i < out_features; ++i) {
+        EXPECT_NEAR(y[i], expect[i], 1e-5);
+        double bound = 0;  // two e4m3 roundings per product term
+        for (int j = 0; j < in_features; ++j) bound += std::fabs(x[j] * w[i * in_features + j]);
+        EXPECT_NEAR(y[i], exact[i], bound * (2 * 0.0625 + 0.0625 * 0.0625) + 1e-6);
+    }
+}
+
+TEST_F(FullyConnectedLayerTest, BackwardPass) {
+    const int in_features = 4, out_features = 3;
+    FullyConnectedLayer<float> layer(in_features, out_features, true);
+    tensor<float> input({1, in_features});
+    std::vector<float> x(in_features);
+    for (int i = 0; i < in_features; ++i) x[i] = static_cast<float>(i) / in_features;
+    input.upload(x.data());
+    tensor<float> output = layer.forward(input);
+    tensor<float> grad_output(output.shape());
+    std::vector<float> dy(out_features);
+    for (int i = 0; i < out_features; ++i) dy[i] = static_cast<float>(i) / out_features;
+    grad_output.upload(dy.data());
+    auto params = layer.parameters();
+    const auto w = download(*params[0]);
+    tensor<float> grad_input = layer.backward(grad_output);
+    const auto dx = download(grad_input);
+
+    const auto dyd = fp8_values(dy, DFO_E5M2);
+    std::vector<float> edx(in_features), edw(w.size()), edb(out_features);
+    dfo_fc_backward_input(dyd.data(), fp8_values(w, DFO_E4M3).data(), edx.data(), 1, in_features, out_features, 1);
+    dfo_fc_backward_weights(dyd.data(), fp8_values(x, DFO_E4M3).data(), edw.data(), 1, in_features, out_features, 1);
+    dfo_fc_backward_bias(dy.data(), edb.data(), 1, out_features);
+    for (int i = 0; i < in_features; ++i) EXPECT_NEAR(dx[i], edx[i], 1e-5);
+
+    auto grads = layer.gradients();
+    EXPECT_EQ(grads.size(), 2u);
+    EXPECT_EQ(grads[0]->shape()[0], out_features);
+    EXPECT_EQ(grads[0]->shape()[1], in_features);
+    EXPECT_EQ(grads[1]->shape()[1], out_features);
+    const auto dw = download(*grads[0]);
+    const auto db = download(*grads[1]);
+    for (size_t i = 0; i < dw.size(); ++i) EXPECT_NEAR(dw[i], edw[i], 1e-5);
+    for (int i = 0; i < out_features; ++i) EXPECT_NEAR(db[i], edb[i], 1e-6);
+}
+
+TEST_F(FullyConnectedLayerTest, DifferentDimensions) {
+    const int in_features = 5, out_features = 2;
+    FullyConnectedLayer<float> layer(in_features, out_features, true);
+    tensor<float> input({1, in_features});
+    std::vector<float> x(in_features);
+    for (int i = 0; i < in_features; ++i) x[i] = static_cast<float>(i) / in_features;
+    input.upload(x.data());
+    tensor<float> output = layer.forward(input);
+    EXPECT_EQ(output.shape()[0], 1);
+    EXPECT_EQ(output.shape()[1], out_features);
+    tensor<float> grad_output(output.shape());
+    std::vector<float> dy(out_features);
+    for (int i = 0; i < out_features; ++i) dy[i] = static_cast<float>(i) / out_features;
+    grad_output.upload(dy.data());
+    tensor<float> grad_input = layer.backward(grad_output);
+    EXPECT_EQ(grad_input.shape()[0], 1);
+    EXPECT_EQ(grad_input.shape()[1], in_features);
+}
+
+TEST_F(FullyConnectedLayerTest, NonzeroInputGivesNonzeroOutput) {
+    const int in_features = 2, out_features = 2;
+    FullyConnectedLayer<float> layer(in_features, out_features, true);
+    auto params = layer.parameters();
+    std::vector<float> w = {1.0f, 2.0f, 3.0f, 4.0f};
+    std::vector<float> b = {0.5f, -0.5f};
+    params[0]->upload(w.data());
+    params[1]->upload(b.data());
+    tensor<float> input({1, in_features});
+    std::vector<float> x = {1.0f, 2.0f};
+    input.upload(x.data());
+    const auto y = download(layer.forward(input));
+    for (float v : y) EXPECT_NE(v, 0.0f);
+    // fp8 values of W: 3 -> 336 * s ties to 320 * s (RNE), so y differs
+    // from the fp32 {5.5, 10.5}; the oracle fixes what it must be
+    std::vector<float> expect(2);
+    dfo_fc_forward(fp8_values(x, DFO_E4M3).data(), fp8_values(w, DFO_E4M3).data(), b.data(), expect.data(), 1, 2, 2,
+                   1);
+    EXPECT_NEAR(y[0], expect[0], 1e-5);
+    EXPECT_NEAR(y[1], expect[1], 1e-5);
+}
+
+TEST_F(FullyConnectedLayerTest, BackwardRequiresTrainingAndForward) {
+    FullyConnectedLayer<float> inference(4, 3, false);
+    tensor<float> g({1, 3});
+    g.zero();
+    EXPECT_THROW(inference.backward(g), std::runtime_error);
+    FullyConnectedLayer<float> training(4, 3, true);
+    EXPECT_THROW(training.backward(g), std::runtime_error);
+    tensor<float> bad({1, 5});
+    EXPECT_THROW(training.forward(bad), std::invalid_argument);
+}
+
+// ragged shapes (not multiples of 16) through forward and backward, fp32
+TEST_F(FullyConnectedLayerTest, RaggedShapesMatchOracle) {
+    const int N = 37, in_f = 100, out_f = 52;
+    FullyConnectedLayer<float> layer(in_f, out_f, true);
+    const auto w = uniform((size_t)out_f * in_f, -0.2f, 0.2f, 21);
+    const auto b = uniform(out_f, -1.0f, 1.0f, 22);
+    layer.parameters()[0]->upload(w.data());
+    layer.parameters()[1]->upload(b.data());
+    const auto x = uniform((size_t)N * in_f, -2.0f, 2.0f, 23);
+    const auto dy = uniform((size_t)N * out_f, -0.01f, 0.01f, 24);
+    tensor<float> input({N, in_f}), grad_out({N, out_f});
+    input.upload(x.data());
+    grad_out.upload(dy.data());
+    const auto y = download(layer.forward(input));
+    const auto dx = download(layer.backward(grad_out));
+    const auto dw = download(*layer.grad_weights());
+    const auto db = download(*layer.grad_bias());
+
+    const auto xd = fp8_values(x, DFO_E4M3), wd = fp8_values(w, DFO_E4M3), dyd = fp8_values(dy, DFO_E5M2);
+    std::vector<float> ey((size_t)N * out_f), edx((size_t)N * in_f), edw(w.size()), edb(out_f);
+    dfo_fc_forward(xd.data(), wd.data(), b.data(), ey.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_input(dyd.data(), wd.data(), edx.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_weights(dyd.data(), xd.data(), edw.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_bias(dy.data(), edb.data(), N, out_f);
+    EXPECT_LE(rel_err(y, ey), 1e-4);
+    EXPECT_LE(rel_err(dx, edx), 1e-4);
+    EXPECT_LE(rel_err(dw, edw), 1e-4);
+    EXPECT_LE(rel_err(db, edb), 1e-5);
+}
+
+// bfloat16 layer: operands quantized from bf16, outputs rounded to bf16
+TEST_F(FullyConnectedLayerTest, BFloat16LayerMatchesOracle) {
+    const int N = 64, in_f = 96, out_f = 80;
+    FullyConnectedLayer<bfloat16> layer(in_f, out_f, true);
+    const auto w = bf16_to_float(float_to_bf16(uniform((size_t)out_f * in_f, -0.3f, 0.3f, 31)));
+    const auto b = bf16_to_float(float_to_bf16(uniform(out_f, -1.0f, 1.0f, 32)));
+    const auto x = bf16_to_float(float_to_bf16(uniform((size_t)N * in_f, -3.0f, 3.0f, 33)));
+    const auto dy = bf16_to_float(float_to_bf16(uniform((size_t)N * out_f, -0.5f, 0.5f, 34)));
+    upload_bf16(*layer.weights(), w);
+    upload_bf16(*layer.bias(), b);
+    tensor<bfloat16> input({N, in_f}), grad_out({N, out_f});
+    upload_bf16(input, x);
+    upload_bf16(grad_out, dy);
+    const auto y = download_f(layer.forward(input));
+    const auto dx = download_f(layer.backward(grad_out));
+    const auto dw = download_f(*layer.grad_weights());
+    const auto db = download_f(*layer.grad_bias());
+
+    const auto xd = fp8_values(x, DFO_E4M3), wd = fp8_values(w, DFO_E4M3), dyd = fp8_values(dy, DFO_E5M2);
+    std::vector<float> ey((size_t)N * out_f), edx((size_t)N * in_f), edw(w.size()), edb(out_f);
+    dfo_fc_forward(xd.data(), wd.data(), b.data(), ey.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_input(dyd.data(), wd.data(), edx.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_weights(dyd.data(), xd.data(), edw.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_bias(dy.data(), edb.data(), N, out_f);
+    // bf16 outputs: unit roundoff 2^-8 (relative) on top of the fp32 bound
+    const double tol = 1e-4 + 1.0 / 256;
+    EXPECT_LE(rel_err(y, ey), tol);
+    EXPECT_LE(rel_err(dx, edx), tol);
+    EXPECT_LE(rel_err(dw, edw), tol);
+    EXPECT_LE(rel_err(db, edb), tol);
+}
+
+// all launches follow Hip::stream(): results on a created stream equal
+// those on the legacy stream, bit for bit
+TEST_F(FullyConnectedLayerTest, RunsOnTheCurrentStream) {
+    const int N = 48, in_f = 64, out_f = 32;
+    FullyConnectedLayer<float> layer(in_f, out_f, true);
+    const auto x = uniform((size_t)N * in_f, -1.0f, 1.0f, 41);
+    tensor<float> input({N, in_f});
+    input.upload(x.data());
+    const auto y0 = download(layer.forward(input));
+    hipStream_t s;
+    ASSERT_EQ(hipStreamCreate(&s), hipSuccess);
+    std::vector<float> y1;
+    {
+        StreamGuard guard(s);
+        EXPECT_EQ(Hip::stream(), s);
+        y1 = download(layer.forward(input));
+    }
+    (void)hipStreamDestroy(s);
+    EXPECT_TRUE(y0 == y1);
+}
+
+TEST_F(FullyConnectedLayerTest, SaveLoadRoundTrip) {
+    FullyConnectedLayer<float> a(12, 7, false);
+    std::stringstream ss;
+    a.save(ss);
+    FullyConnectedLayer<float> b(3, 3, false);
+    b.load(ss);
+    EXPECT_TRUE(b.weights()->equals(*a.weights()));
+    EXPECT_TRUE(b.bias()->equals(*a.bias()));
+    tensor<float> input({2, 12});
+    input.fill(0.5f);
+    EXPECT_TRUE(a.forward(input).equals(b.forward(input)));
+}
+
+int main(int argc, char** argv) { return mini_test::run_all(argc, argv); }
