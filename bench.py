@@ -54,6 +54,9 @@ def parse():
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run one plain 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
+    p.add_argument("--summarize-profiles", action="store_true",
+                   help="no GPU work: turn the rocprofv3 output of PROFILE_COMMANDS (under gpurun_out/) into "
+                        "the summaries under profiles/")
     return p.parse_args()
 
 
@@ -90,6 +93,9 @@ class Timer:
 
 def main():
     args = parse()
+    if args.summarize_profiles:
+        summarize_profiles()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
               "(the path's multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
@@ -301,6 +307,113 @@ def measured_traffic(kernel_family):
         return data["families"][kernel_family]["bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+# The profiling runs behind profiles/ (from the repository root on one
+# MI355X, with TMPDIR=/tmp), and the directories they write.
+PROFILE_COMMANDS = {
+    "stats": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_bench -o bench -- "
+              "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion"),
+    "fetch": ("timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv "
+              "-d gpurun_out/pmc_fetch -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
+              "--no-conversion --no-graph --copy-calibration"),
+    "write": ("timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --kernel-trace --output-format csv "
+              "-d gpurun_out/pmc_write -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
+              "--no-conversion --no-graph --copy-calibration"),
+}
+# GEMM families whose C-ABI call is exactly one kernel, by template
+# arguments: <BM, BN, WM, WN, A format, B format, output, bias, split>.
+TRAFFIC_FAMILIES = {
+    "gemm_fwd": ("0, 0, unsigned short, unsigned short, false>",),
+    "gemm_dx": ("1, 0, unsigned short, float, false>",),
+}
+
+
+def _short_kernel(name):
+    """Kernel name without its parameter list."""
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def summarize_profiles():
+    """Write profiles/bench_config4_kernel_stats.md, hbm_traffic_config4.md
+    and hbm_traffic.json from the output of PROFILE_COMMANDS."""
+    import csv
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    prof = os.path.join(root, "profiles")
+    out_dir = os.path.join(root, "gpurun_out")
+    os.makedirs(prof, exist_ok=True)
+
+    stats_csv = os.path.join(out_dir, "prof_bench", "bench_kernel_stats.csv")
+    with open(stats_csv) as fh:
+        rows = list(csv.DictReader(fh))
+    lines = ["# rocprofv3 kernel statistics -- bench.py, config 4 (GPT-2 XL Linears fwd+bwd, M=16384)", "",
+             "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["stats"], "",
+             "23 steps: 3 warm-up + 20 HIP-graph replays (the timed region) + 20 eager steps with HIP events "
+             "(the per-kernel pass).  Durations in microseconds.", "",
+             "| kernel | calls | avg us | min us | max us | % time |", "|---|---|---|---|---|---|"]
+    for r in rows:
+        lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    with open(os.path.join(prof, "bench_config4_kernel_stats.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+    def counters(which, counter):
+        path = os.path.join(out_dir, "pmc_" + which, "bench_counter_collection.csv")
+        vals = {}
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] == counter:
+                    vals.setdefault(_short_kernel(r["Kernel_Name"]), []).append(float(r["Counter_Value"]))
+        return vals
+
+    fetch_all = counters("fetch", "FETCH_SIZE")
+    write_all = counters("write", "WRITE_SIZE")
+    copy = "__amd_rocclr_copyBuffer"
+    # calibration: the largest copy dispatch is the 1 GiB device-to-device
+    # copy (--copy-calibration); it reads and writes exactly 2^30 bytes
+    copy_f, copy_w = max(fetch_all.pop(copy)), max(write_all.pop(copy))
+    fscale = (1 << 30) / (copy_f * 1024)
+    wscale = (1 << 30) / (copy_w * 1024)
+    fetch = {k: (sum(v) / len(v), len(v)) for k, v in fetch_all.items()}
+    write = {k: (sum(v) / len(v), len(v)) for k, v in write_all.items()}
+    fams = {}
+    for fam, pats in TRAFFIC_FAMILIES.items():
+        names = [k for k in fetch if k.startswith("void dfk::gemm") and any(k.endswith(p) for p in pats)]
+        if len(names) != 1 or names[0] not in write:
+            continue
+        k = names[0]
+        fams[fam] = {"kernel": k, "bytes_per_launch": int(round(fetch[k][0] * 1024 * fscale + write[k][0] * 1024 * wscale)),
+                     "fetch_KiB": fetch[k][0], "write_KiB": write[k][0]}
+    data = {"command_fetch": PROFILE_COMMANDS["fetch"], "command_write": PROFILE_COMMANDS["write"],
+            "calibration": {"kernel": copy, "bytes": 1 << 30, "fetch_KiB": copy_f, "write_KiB": copy_w,
+                            "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
+            "families": fams}
+    with open(os.path.join(prof, "hbm_traffic.json"), "w") as fh:
+        json.dump(data, fh, indent=1)
+        fh.write("\n")
+    lines = ["# HBM-side traffic per launch -- rocprofv3 FETCH_SIZE / WRITE_SIZE, config 4", "",
+             "Commands (two separate counter runs, eager launches, from the repository root):", "",
+             "    " + PROFILE_COMMANDS["fetch"], "    " + PROFILE_COMMANDS["write"], "",
+             f"Calibration: the 1 GiB device-to-device copy (`{copy}`, one dispatch) reads FETCH_SIZE = "
+             f"{copy_f:.1f} KiB and WRITE_SIZE = {copy_w:.1f} KiB, so bytes = FETCH_SIZE x 1024 x {fscale:.4f} "
+             f"and WRITE_SIZE x 1024 x {wscale:.4f}.  FETCH_SIZE counts L2 misses served by the fabric "
+             "(Infinity Cache or HBM).", "",
+             "| kernel | launches | FETCH KiB | WRITE KiB | calibrated MB/launch |", "|---|---|---|---|---|"]
+    for k in sorted(set(fetch) & set(write)):
+        mb = (fetch[k][0] * 1024 * fscale + write[k][0] * 1024 * wscale) / 1e6
+        lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:.1f} | {write[k][0]:.1f} | {mb:.1f} |")
+    with open(os.path.join(prof, "hbm_traffic_config4.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)})")
 
 
 def conversion_bench(torch, df, synth, dev, stream, reps=10):

@@ -34,6 +34,22 @@ static_assert(sizeof(fp8_e4m3) == 1 && sizeof(fp8_e5m2) == 1, "fp8 elements are 
 
 using bfloat16 = __hip_bfloat16;
 
+// The project's element-type enum: values 0-4 as the reference's
+// DType (dnn/utils/onnx_loader.cuh:16-22), extended with the
+// two fp8 formats; the same values as df_dtype in the C ABI.
+enum class DType : uint8_t {
+    Float32 = DF_DTYPE_FLOAT32,
+    Half = DF_DTYPE_HALF,
+    Int8 = DF_DTYPE_INT8,
+    UInt8 = DF_DTYPE_UINT8,
+    BFloat16 = DF_DTYPE_BFLOAT16,
+    FP8E4M3 = DF_DTYPE_FP8E4M3,
+    FP8E5M2 = DF_DTYPE_FP8E5M2,
+};
+static_assert((int)DType::Float32 == 0 && (int)DType::BFloat16 == 4 && (int)DType::FP8E4M3 == 5 &&
+                  (int)DType::FP8E5M2 == 6,
+              "enum values are part of the on-disk and C-ABI contract");
+
 template <typename T> struct dtype_traits;
 template <> struct dtype_traits<float> { static constexpr int value = DF_DTYPE_FLOAT32; static constexpr bool is_fp8 = false; };
 template <> struct dtype_traits<__half> { static constexpr int value = DF_DTYPE_HALF; static constexpr bool is_fp8 = false; };
