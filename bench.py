@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
-"""bench.py -- fp8 Linear path on one MI355X (BASELINE.json metric).
+"""bench.py -- fp8 Linear path on one MI355X: fp8 Linear TFLOP/s and quantize GB/s
+at GPT-2 XL shapes, as fractions of the fp8 MFMA and HBM rooflines.
 
-Workload (BASELINE.json configs[3], "config 4"): the four GPT-2 XL Linears
+Workload ("config 4"): the four GPT-2 XL Linears
 (d = 1600: qkv 1600->4800, attn proj 1600->1600, fc 1600->6400, proj
 6400->1600) at M = 16384 tokens, forward and backward, on seeded synthetic
 bf16 tensors already resident in HBM.  One step, per Linear:
@@ -55,8 +56,8 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run one plain 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
     p.add_argument("--summarize-profiles", action="store_true",
-                   help="no GPU work: turn the rocprofv3 output of PROFILE_COMMANDS (under gpurun_out/) into "
-                        "the summaries under profiles/")
+                   help="no GPU work: turn the rocprofv3 output of PROFILE_COMMANDS into the summaries under "
+                        "profiles/")
     return p.parse_args()
 
 
@@ -98,7 +99,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the path's multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(multi-GPU sharding of this path is designed, not built)", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -187,7 +188,7 @@ def main():
                    l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K,
                    gws.data_ptr(), gws_bytes, cur())
 
-    # algorithmic work per step (unpadded shapes; BASELINE.md counting rules)
+    # algorithmic work per step: 2*M*N*K per GEMM on unpadded shapes
     gemm_flops = {"gemm_fwd": 0, "gemm_dx": 0, "gemm_dw": 0}
     qbytes = {}
     for (_, K, N) in XL_LINEARS:

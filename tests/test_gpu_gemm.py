@@ -1,6 +1,6 @@
 """GPU parity of the fp8 Linear GEMMs (forward, dX, dW) and db.
 
-Bar (contract D6): the GPU output is within
+Bar (the path's GEMM contract D6): the GPU output is within
 normwise relative error 1e-4 (max|y - r| / max|r|) of the reference's
 fp32-accumulated product of the same dequantized operands, computed by the
 oracle's restatement of dnn/layers/fully_connected_layer.cu:14-106.  Codes

@@ -88,7 +88,7 @@ def test_random_patterns_with_scale_against_torch(name):
 
 
 def test_reference_kat_codes():
-    """SURVEY-derived KAT from fully_connected_layer_test.cu:266-284: W
+    """Known-answer codes derived from fully_connected_layer_test.cu:266-284: W
     absmax 4 -> s = 4/448, codes {0x6E,0x76,0x7A,0x7E} (336 ties to 320);
     x absmax 2 -> {0x76, 0x7E}."""
     kat = GOLDEN["fc_kat"]
