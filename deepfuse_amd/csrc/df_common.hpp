@@ -170,6 +170,7 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_floa
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 int launch_status(const char* what);  // DF_OK or DF_ERR_HIP (checks hipGetLastError)
+int device_cu_count();                 // compute units of the current device (cached; 0 on error)
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }

@@ -33,6 +33,9 @@
 // and fc_backward_weights (dnn/layers/fully_connected_layer.cu:14-89).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "df_common.hpp"
 
 namespace dfk {
@@ -419,6 +422,360 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_nt_dma128_kernel(
                                            vec_out, sa[0] * sb[0], bias);
 }
 
+// ---------------------------------------------------------------------------
+// Persistent kernel for outputs with at least one 256x256 tile per CU.
+//
+// One block per CU (grid = min(tiles, CUs)) walks tiles bl, bl+P, bl+2P, ...
+// of the grouped tile order; bl remaps the block id so that each XCD owns a
+// contiguous range of P/8 concurrent tiles (sharing A rows and B columns in
+// its L2).  8 waves, two per SIMD, each owning a 128x64 quarter-row of the
+// 256x256 tile as 4x2 v_mfma_f32_32x32x64_f8f6f4 tiles.
+//
+// Pipeline: K advances in half-steps of 64 bytes (one MFMA depth).  A DMA
+// step moves 128 bytes of K (whole cache lines) for the tile's 256 A rows
+// and 256 B rows into one of two 64 KiB LDS stages.  Half-step h issues the
+// MFMAs on fragments h and reads fragments h+1 from LDS.  At the start of
+// each odd half-step 2g+1 a wave waits for its part of DMA step g+1, the
+// block synchronises, and DMA step g+2 goes into stage g%2, whose last reads
+// were in half-step 2g.  The DMA cursor runs across tile boundaries, so the
+// next tile's first steps load while this tile finishes and stores.
+//
+// LDS rows are 128 bytes; 16-byte chunk c of row r sits in slot
+// c ^ ((r >> 1) & 7), which spreads the 16 rows read by each group of 16
+// lanes over all 64 banks (no bank conflicts for the fragment reads).
+//
+// Bias: every DMA step also moves the tile's bias slice (4 bytes per lane)
+// into one of three 2 KiB LDS slots (tile index mod 3), so the epilogue reads
+// it from LDS.  Epilogue: scale, bias and the bf16 conversion
+// (v_cvt_pk_bf16_f32, round to nearest even) in registers, then each 32-row
+// block passes through the wave's LDS slab and leaves as 16-byte stores, 8
+// lanes per 128-byte row segment.
+constexpr int kPBM = 256, kPBN = 256;  // persistent block tile
+constexpr int kPKB = 128;              // K bytes per DMA step
+constexpr int kPStage = (kPBM + kPBN) * kPKB;
+constexpr int kPBiasSlots = 3;
+constexpr int kPBiasSlot = 2048;
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16_rne(float a, float b) {
+    const v2f f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n), lgkmcnt(0), no expcnt wait
+__device__ __forceinline__ constexpr int waitcnt_vm_lgkm0(int n) {
+    return (n & 15) | ((n >> 4) << 14) | 0x70;
+}
+
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
+    const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
+    const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
+    OutT* __restrict__ C, int ldc, int vec_out) {
+    constexpr int FM = 4, FN = 2;                 // 32x32 MFMA tiles per wave
+    constexpr int ES = (int)sizeof(OutT);
+    constexpr int SR = ES == 2 ? 16 : 8;          // epilogue slab rows
+    constexpr int SROW = 64 * ES + 16;            // padded slab row (bytes)
+    constexpr int SLAB = SR * SROW;
+    constexpr int NPASS = 32 / SR;                // slab passes per 32-row block
+    constexpr int SPP = SR * 64 * ES / 1024;      // 16-byte stores per lane per pass
+    constexpr int NST = FM * NPASS * SPP;         // epilogue stores per wave
+    constexpr int W_AFTER = NST > 63 ? 63 : NST;
+    constexpr uint32_t kOOB = 0x80000000u;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kPStage + kPBiasSlots * kPBiasSlot + 8 * SLAB];
+    uint8_t* const lbias = lds + 2 * kPStage;
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = w >> 2, wn = w & 3;
+    uint8_t* const slab = lds + 2 * kPStage + kPBiasSlots * kPBiasSlot + w * SLAB;
+    const int tiles_m = (M + kPBM - 1) / kPBM, tiles_n = (N + kPBN - 1) / kPBN;
+    const int ntiles = tiles_m * tiles_n;
+    const int nk = (K + kPKB - 1) / kPKB;
+    const int P = gridDim.x;
+    const int q = P >> 3, rr = P & 7;
+    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int bl = xcd < rr ? xcd * (q + 1) + idx : rr * (q + 1) + (xcd - rr) * q + idx;
+    const int my_tiles = bl < ntiles ? (ntiles - bl + P - 1) / P : 0;
+    const int S = my_tiles * nk;  // DMA steps of this block
+    auto tile_mn = [&](int r, int& m0, int& n0) {
+        const int lt = bl + r * P;
+        const int per_group = kGroupM * tiles_n;
+        const int group = lt / per_group;
+        const int first_m = group * kGroupM;
+        const int gsize = min(tiles_m - first_m, kGroupM);
+        const int in_group = lt - group * per_group;
+        m0 = (first_m + in_group % gsize) * kPBM;
+        n0 = (in_group / gsize) * kPBN;
+    };
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * lda, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, N * ldb, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rBias =
+        __builtin_amdgcn_make_buffer_rsrc((void*)bias, (short)0, HAS_BIAS ? N * (int)sizeof(BiasT) : 0, 0x00020000);
+
+    // ---- DMA.  Instruction d (0..3) of wave w fills rows (w*4+d)*8 + lane/8
+    // of the stage's A and B parts; the lane's slot lane&7 takes global chunk
+    // (lane&7) ^ swz(row), and swz(row) = 4*(d&1) + (lane>>4).  Each lane
+    // keeps the byte offsets of its even- and odd-instruction rows; the
+    // whole offset is the buffer's per-lane offset, so rows past M (N) are
+    // outside the buffer's range and read as zero, and a chunk past K (or a
+    // step past the block's last) gets an offset beyond any range.
+    const int drow = lane >> 3;
+    const int dch0 = ((lane & 7) ^ (lane >> 4)) << 4;
+    const int dch1 = dch0 ^ 64;
+    const uint32_t a16 = 16u * (uint32_t)lda, b16 = 16u * (uint32_t)ldb;
+    int d_tile = 0, d_k = 0, d_m0 = 0, d_n0 = 0, d_g = 0;
+    uint32_t oa0 = kOOB, oa1 = kOOB, ob0 = kOOB, ob1 = kOOB, obias = kOOB;
+    auto dprep = [&]() {
+        const bool live = d_g < S;
+        const int k0 = d_k * kPKB + dch0, k1 = d_k * kPKB + dch1;
+        const uint32_t ra = (uint32_t)(d_m0 + w * 32 + drow), rb = (uint32_t)(d_n0 + w * 32 + drow);
+        oa0 = (live && k0 < K) ? ra * (uint32_t)lda + (uint32_t)k0 : kOOB;
+        oa1 = (live && k1 < K) ? (ra + 8u) * (uint32_t)lda + (uint32_t)k1 : kOOB;
+        ob0 = (live && k0 < K) ? rb * (uint32_t)ldb + (uint32_t)k0 : kOOB;
+        ob1 = (live && k1 < K) ? (rb + 8u) * (uint32_t)ldb + (uint32_t)k1 : kOOB;
+        if (HAS_BIAS) obias = live ? (uint32_t)(d_n0 * (int)sizeof(BiasT) + w * 256 + lane * 4) : kOOB;
+    };
+    auto dissue = [&]() {
+        uint8_t* base = lds + ((uint32_t)d_g & 1u) * kPStage;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rA, (__attribute__((address_space(3))) void*)(base + (w * 4 + d) * 1024), 16,
+                ((d & 1) ? oa1 : oa0) + (uint32_t)(d >> 1) * a16, 0, 0, 0);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rB, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
+                ((d & 1) ? ob1 : ob0) + (uint32_t)(d >> 1) * b16, 0, 0, 0);
+        if (HAS_BIAS)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rBias,
+                (__attribute__((address_space(3))) void*)(lbias + ((uint32_t)d_tile % kPBiasSlots) * kPBiasSlot +
+                                                          w * 256),
+                4, obias, 0, 0, 0);
+    };
+    auto dadvance = [&]() {
+        if (d_g < S && ++d_k == nk) {
+            d_k = 0;
+            if (++d_tile < my_tiles) tile_mn(d_tile, d_m0, d_n0);
+        }
+        ++d_g;
+        dprep();
+    };
+    if (my_tiles > 0) tile_mn(0, d_m0, d_n0);
+    dprep();
+
+    // ---- fragments (v_mfma_f32_32x32x64_f8f6f4 operand layout: lane l
+    // supplies row l%32, K bytes 32*(l/32) .. +32 of the 64-byte depth):
+    // chunks 4e + 2*(l/32) and +1 of K-half e, from slots chunk ^ swz(row)
+    const int fr = lane & 31;
+    const int fsw = (fr >> 1) & 7;
+    const int c0 = (lane >> 5) * 2;
+    int foff[2][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        foff[e][0] = fr * kPKB + (((4 * e + c0) ^ fsw) << 4);
+        foff[e][1] = fr * kPKB + (((4 * e + c0 + 1) ^ fsw) << 4);
+    }
+    auto rd = [&](const uint8_t* p, int e) -> v8i {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + foff[e][0]);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + foff[e][1]);
+        v8i r;
+        r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+        r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+        return r;
+    };
+
+    v16f acc[FM][FN];
+    v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    int after_epi = 0, c_h = 0;
+    const float sab = sa[0] * sb[0];
+
+    // One half-step: MFMAs on (fa, fb); fragments of half-step c_h+1 into
+    // (na, nb).  Odd half-steps first wait for the DMA step that half-step
+    // c_h+1 reads (after an epilogue its stores are still counted), then
+    // synchronise the block and issue the DMA two steps ahead.
+    auto half = [&](auto zero, auto odd, v8i* fa, v8i* fb, v8i* na, v8i* nb) {
+        if (decltype(odd)::value) {
+            if (after_epi)
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(W_AFTER));
+            else
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+            after_epi = 0;
+            __builtin_amdgcn_s_barrier();
+        }
+        const int nxt = c_h + 1;
+        const uint8_t* sA = lds + (((uint32_t)nxt >> 1) & 1u) * kPStage;
+        const uint8_t* sB = sA + kPBM * kPKB;
+        const int e = nxt & 1;
+        if (decltype(odd)::value) dissue();
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if (decltype(zero)::value) {
+                    const v16f z = {};
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], z, FB, FA, 0, 0, 0, 0);
+                } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], FB, FA, 0,
+                                                                                0, 0, 0);
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) na[i] = rd(sA + (wm * 128 + i * 32) * kPKB, e);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) nb[j] = rd(sB + (wn * 64 + j * 32) * kPKB, e);
+        // interleave: one MFMA, then its share of the LDS reads and DMAs
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (x < 4)
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            else
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (decltype(odd)::value) {
+                if (x == 0)
+                    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+                else
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+        }
+        ++c_h;
+        if (decltype(odd)::value) dadvance();
+    };
+
+    auto epilogue = [&](int tile) {
+        int tm0, tn0;
+        tile_mn(tile, tm0, tn0);
+        const int rowb = tm0 + wm * 128;
+        const int colw = tn0 + wn * 64;
+        const int h4 = (lane >> 5) * 4;
+        const uint8_t* bsl = lbias + ((uint32_t)tile % kPBiasSlots) * kPBiasSlot;
+        // bias of the lane's columns colw + 32j + 8g + h4 + (0..3).  A bf16
+        // bias of odd length: its last element shares a dword with the end
+        // of the buffer, which the dword DMA returned as zero.
+        float bv[FN][4][4];
+        float btail = 0.f;
+        if (HAS_BIAS && sizeof(BiasT) == 2 && (N & 1) && colw + 64 >= N) btail = bias_ld(bias, N - 1);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int lc = wn * 64 + j * 32 + 8 * g + h4;
+                const int col = tn0 + lc;
+                float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+                if (HAS_BIAS) {
+                    if (sizeof(BiasT) == 4) {
+                        const f32x4 v = *reinterpret_cast<const f32x4*>(bsl + lc * 4);
+                        b0 = v.x; b1 = v.y; b2 = v.z; b3 = v.w;
+                    } else {
+                        const u32x2 v = *reinterpret_cast<const u32x2*>(bsl + lc * 2);
+                        b0 = bf16_to_f32(v.x & 0xFFFFu); b1 = bf16_to_f32(v.x >> 16);
+                        b2 = bf16_to_f32(v.y & 0xFFFFu); b3 = bf16_to_f32(v.y >> 16);
+                        if (N & 1) {
+                            b0 = col == N - 1 ? btail : b0;
+                            b1 = col + 1 == N - 1 ? btail : b1;
+                            b2 = col + 2 == N - 1 ? btail : b2;
+                            b3 = col + 3 == N - 1 ? btail : b3;
+                        }
+                    }
+                }
+                bv[j][g][0] = b0; bv[j][g][1] = b1; bv[j][g][2] = b2; bv[j][g][3] = b3;
+            }
+        // slab read-back geometry: lane -> (row, 16-byte chunk)
+        constexpr int CPR = 64 * ES / 16;
+        constexpr int RPS = 64 / CPR;
+        const int srow = lane / CPR, rc = lane % CPR;
+        const int scol = colw + rc * (16 / ES);
+        const bool col_full = vec_out && scol + 16 / ES <= N;
+        const int my_sr = fr % SR, my_pass = fr / SR;
+        typedef typename std::conditional<ES == 2, u32x2, f32x4>::type Pk;
+        Pk pk[FM][FN][4];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const v16f& a = acc[i][j];
+                    const float v0 = a[4 * g] * sab + bv[j][g][0], v1 = a[4 * g + 1] * sab + bv[j][g][1];
+                    const float v2 = a[4 * g + 2] * sab + bv[j][g][2], v3 = a[4 * g + 3] * sab + bv[j][g][3];
+                    if constexpr (ES == 2)
+                        pk[i][j][g] = u32x2{pack_bf16_rne(v0, v1), pack_bf16_rne(v2, v3)};
+                    else
+                        pk[i][j][g] = f32x4{v0, v1, v2, v3};
+                }
+        // LDS operations of one wave execute in order, so a pass's reads see
+        // its writes and precede the next pass's writes; the empty asm
+        // statements keep the compiler from reordering them.
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int p = 0; p < NPASS; ++p) {
+                if (my_pass == p) {
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g)
+                            *reinterpret_cast<Pk*>(slab + my_sr * SROW + (j * 32 + 8 * g + h4) * ES) = pk[i][j][g];
+                }
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int s = 0; s < SPP; ++s) {
+                    const int sr = s * RPS + srow;
+                    const u32x4 val = *reinterpret_cast<const u32x4*>(slab + sr * SROW + rc * 16);
+                    const int row = rowb + i * 32 + p * SR + sr;
+                    if (row < M) {
+                        OutT* dst = C + (int64_t)row * ldc + scol;
+                        if (col_full) {
+                            *reinterpret_cast<u32x4*>(dst) = val;
+                        } else {
+                            const OutT* ev = reinterpret_cast<const OutT*>(&val);
+#pragma unroll
+                            for (int x = 0; x < 16 / ES; ++x)
+                                if (scol + x < N) dst[x] = ev[x];
+                        }
+                    }
+                }
+                asm volatile("" ::: "memory");
+            }
+        after_epi = 1;
+    };
+
+    // prologue: DMA steps 0 and 1, fragments of half-step 0
+    for (int g = 0; g < 2; ++g) {
+        dissue();
+        dadvance();
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(HAS_BIAS ? 9 : 8));
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa0[i] = rd(lds + (wm * 128 + i * 32) * kPKB, 0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb0[j] = rd(lds + kPBM * kPKB + (wn * 64 + j * 32) * kPKB, 0);
+
+    using Z = std::true_type;
+    using NZ = std::false_type;
+    using ODD = std::true_type;
+    using EVEN = std::false_type;
+    // a tile is 2*max(nk,1) half-steps; the fragments of its first half-step
+    // are in (fa0, fb0) when it starts
+    for (int tile = 0; tile < my_tiles; ++tile) {
+        half(Z{}, EVEN{}, fa0, fb0, fa1, fb1);
+        half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
+        for (int k = 1; k < nk; ++k) {
+            half(NZ{}, EVEN{}, fa0, fb0, fa1, fb1);
+            half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
+        }
+        epilogue(tile);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every DMA has landed before the block's LDS is released
+}
+
 // out[m,n] = (sum_s P[s][m][n]) * sa * sb + bias[n], slices in order; four
 // consecutive columns per thread (16-byte partial loads) when N % 4 == 0.
 template <typename OutT, typename BiasT>
@@ -543,8 +900,40 @@ static void launch_cfg(const GemmArgs& g) {
                                                                 static_cast<OutT*>(g.C), g.ldc, vec_red);
 }
 
+// The persistent kernel takes outputs with at least one 256x256 tile per CU
+// (smaller ones keep the split-K plan below).  Its per-lane buffer offsets
+// reach a tile past the last row, so M*lda and N*ldb stay below 2^31 (and
+// lda, ldb below 2^23); its bias DMA reads whole dwords.
+template <typename BiasT>
+static int persistent_grid(const GemmArgs& g) {
+    const int cus = device_cu_count();
+    if (cus <= 0) return 0;
+    const int64_t tiles = (int64_t)((g.M + kPBM - 1) / kPBM) * ((g.N + kPBN - 1) / kPBN);
+    if (tiles < cus) return 0;
+    if ((int64_t)g.M * g.lda >= (1ll << 31) || (int64_t)g.N * g.ldb >= (1ll << 31)) return 0;
+    if (g.lda >= (1 << 23) || g.ldb >= (1 << 23)) return 0;
+    if (g.bias && !aligned4(g.bias)) return 0;
+    return cus;
+}
+
+template <int FA, int FB, typename OutT, typename BiasT>
+static void launch_persistent(const GemmArgs& g, int grid) {
+    const int vec_out = ((int64_t)g.ldc * (int64_t)sizeof(OutT)) % 16 == 0 && aligned16(g.C);
+    if (g.bias)
+        gemm_nt_persistent_kernel<FA, FB, OutT, BiasT, true><<<grid, 512, 0, g.st>>>(
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, static_cast<const BiasT*>(g.bias),
+            static_cast<OutT*>(g.C), g.ldc, vec_out);
+    else
+        gemm_nt_persistent_kernel<FA, FB, OutT, BiasT, false><<<grid, 512, 0, g.st>>>(
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, static_cast<OutT*>(g.C), g.ldc, vec_out);
+}
+
 template <int FA, int FB, typename OutT, typename BiasT>
 static void launch_shape(const GemmArgs& g) {
+    if (const int grid = persistent_grid<BiasT>(g)) {
+        launch_persistent<FA, FB, OutT, BiasT>(g, grid);
+        return;
+    }
     if (plan_gemm(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0).big)
         launch_cfg<256, 256, 2, 4, FA, FB, OutT, BiasT>(g);
     else
