@@ -93,6 +93,15 @@ _SIGS = {
     "df_convert": (_c_int, [_c_int, _vp, _c_int, _vp, _c_i64, _vp]),
     "df_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
     "df_approx_equal_mask": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_f, _vp]),
+    "df_host_alloc": (_c_int, [_c_sz, ctypes.POINTER(_vp)]),
+    "df_host_free": (_c_int, [_vp]),
+    "df_streamer_create": (_c_int, [_c_int, _c_sz, ctypes.POINTER(_vp)]),
+    "df_streamer_destroy": (_c_int, [_vp]),
+    "df_streamer_load": (_c_int, [_vp, _vp, _c_sz, ctypes.POINTER(_c_int), ctypes.POINTER(_vp)]),
+    "df_streamer_wait": (_c_int, [_vp, _c_int, _vp]),
+    "df_streamer_release": (_c_int, [_vp, _c_int, _vp]),
+    "df_streamer_slot": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
+    "df_streamer_copy_stream": (_c_int, [_vp, ctypes.POINTER(_vp)]),
 }
 
 _lib = None
@@ -270,3 +279,44 @@ def colsum(x):
     call("df_colsum", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), _ptr(out), _ptr(ws), ws.numel(),
          _stream())
     return out
+
+
+class WeightStreamer:
+    """Ring of device weight slots filled from pinned host memory on a copy
+    stream (``df_streamer_*`` in include/df_capi.h).  ``load`` returns
+    (slot, device pointer); ``wait`` / ``release`` order the slot against the
+    current torch stream."""
+
+    def __init__(self, slots: int, slot_bytes: int):
+        h = _vp()
+        call("df_streamer_create", slots, slot_bytes, ctypes.byref(h))
+        self.handle = h
+        self.slots = slots
+
+    def load(self, host_ptr: int, nbytes: int):
+        slot = _c_int()
+        dev = _vp()
+        call("df_streamer_load", self.handle, host_ptr, nbytes, ctypes.byref(slot), ctypes.byref(dev))
+        return slot.value, dev.value
+
+    def wait(self, slot: int, stream: int | None = None):
+        call("df_streamer_wait", self.handle, slot, _stream() if stream is None else stream)
+
+    def release(self, slot: int, stream: int | None = None):
+        call("df_streamer_release", self.handle, slot, _stream() if stream is None else stream)
+
+    def copy_stream(self) -> int:
+        st = _vp()
+        call("df_streamer_copy_stream", self.handle, ctypes.byref(st))
+        return st.value or 0
+
+    def close(self):
+        if self.handle is not None:
+            call("df_streamer_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,169 @@
+// stream.hip -- layer weight streaming: a ring of device slots filled from
+// pinned host memory by hipMemcpyAsync on the streamer's own copy stream,
+// ordered against the compute stream with events in both directions:
+//   load(l)    : the copy into slot s waits for the event recorded when the
+//                slot's previous contents were released, then records
+//                loaded[s] on the copy stream;
+//   wait(s)    : the compute stream waits for loaded[s];
+//   release(s) : records released[s] on the compute stream after the last
+//                launch that reads the slot.
+// With S slots and loads issued S-1 layers ahead, the copy of layer l+S-1
+// runs while layer l computes (it only waits for layer l-1's kernels).
+//
+// The reference describes this as layer-serialized execution
+// (README.md:212-226) but implements only the host side of it: pinned
+// cudaHostAlloc buffers, per-slot streams and cudaMemcpyAsync in its NVMe
+// loader (apps/host-multi/NVMeLoader_Linux.hpp:20-26,64-71,123-125).  Here
+// the same pieces feed the fp8 GEMMs: each slot holds one layer's e4m3
+// weight codes.
+#include <hip/hip_runtime.h>
+
+#include <new>
+
+#include "df_common.hpp"
+
+namespace dfk {
+
+constexpr int kMaxSlots = 16;
+constexpr size_t kSlotAlign = 4096;
+
+enum SlotState : int { kEmpty = 0, kLoaded = 1, kReleased = 2 };
+
+}  // namespace dfk
+
+struct df_streamer_s {
+    int device = -1;
+    int slots = 0;
+    size_t slot_bytes = 0;
+    uint8_t* dev = nullptr;
+    hipStream_t copy = nullptr;
+    hipEvent_t loaded[dfk::kMaxSlots] = {};
+    hipEvent_t released[dfk::kMaxSlots] = {};
+    int state[dfk::kMaxSlots] = {};
+    int next = 0;
+};
+
+using namespace dfk;
+
+#define DF_HIP(call, what)                                                                      \
+    do {                                                                                        \
+        const hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess) {                                                                 \
+            set_error("%s: HIP error %d (%s)", what, (int)e_, hipGetErrorString(e_));           \
+            return DF_ERR_HIP;                                                                  \
+        }                                                                                       \
+    } while (0)
+
+extern "C" int df_host_alloc(size_t bytes, void** host_ptr) {
+    clear_error();
+    DF_CHECK(host_ptr, DF_ERR_INVALID, "df_host_alloc: host_ptr is NULL");
+    *host_ptr = nullptr;
+    if (bytes == 0) return DF_OK;
+    DF_HIP(hipHostMalloc(host_ptr, bytes, hipHostMallocDefault), "df_host_alloc");
+    return DF_OK;
+}
+
+extern "C" int df_host_free(void* host_ptr) {
+    clear_error();
+    if (host_ptr) DF_HIP(hipHostFree(host_ptr), "df_host_free");
+    return DF_OK;
+}
+
+static void destroy_streamer(df_streamer_s* s) {
+    if (!s) return;
+    if (s->copy) (void)hipStreamSynchronize(s->copy);
+    for (int i = 0; i < kMaxSlots; ++i) {
+        if (s->loaded[i]) (void)hipEventDestroy(s->loaded[i]);
+        if (s->released[i]) (void)hipEventDestroy(s->released[i]);
+    }
+    if (s->copy) (void)hipStreamDestroy(s->copy);
+    if (s->dev) (void)hipFree(s->dev);
+    delete s;
+}
+
+extern "C" int df_streamer_create(int slots, size_t slot_bytes, df_streamer_s** out) {
+    clear_error();
+    DF_CHECK(out, DF_ERR_INVALID, "df_streamer_create: out is NULL");
+    *out = nullptr;
+    DF_CHECK(slots >= 2 && slots <= kMaxSlots, DF_ERR_INVALID, "df_streamer_create: slots=%d not in [2, %d]",
+             slots, kMaxSlots);
+    DF_CHECK(slot_bytes > 0, DF_ERR_INVALID, "df_streamer_create: slot_bytes is 0");
+    df_streamer_s* s = new (std::nothrow) df_streamer_s();
+    DF_CHECK(s, DF_ERR_INVALID, "df_streamer_create: out of host memory");
+    s->slots = slots;
+    s->slot_bytes = (slot_bytes + kSlotAlign - 1) / kSlotAlign * kSlotAlign;
+    hipError_t e = hipGetDevice(&s->device);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->dev), s->slot_bytes * (size_t)slots);
+    // default priority, non-blocking with respect to the null stream
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->copy, hipStreamNonBlocking);
+    for (int i = 0; i < slots && e == hipSuccess; ++i) {
+        e = hipEventCreateWithFlags(&s->loaded[i], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&s->released[i], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        set_error("df_streamer_create: HIP error %d (%s)", (int)e, hipGetErrorString(e));
+        destroy_streamer(s);
+        return DF_ERR_HIP;
+    }
+    *out = s;
+    return DF_OK;
+}
+
+extern "C" int df_streamer_destroy(df_streamer_s* s) {
+    clear_error();
+    destroy_streamer(s);
+    return DF_OK;
+}
+
+extern "C" int df_streamer_copy_stream(df_streamer_s* s, void** stream) {
+    clear_error();
+    DF_CHECK(s && stream, DF_ERR_INVALID, "df_streamer_copy_stream: NULL argument");
+    *stream = s->copy;
+    return DF_OK;
+}
+
+extern "C" int df_streamer_slot(df_streamer_s* s, int slot, void** dev_ptr) {
+    clear_error();
+    DF_CHECK(s && dev_ptr, DF_ERR_INVALID, "df_streamer_slot: NULL argument");
+    DF_CHECK(slot >= 0 && slot < s->slots, DF_ERR_INVALID, "df_streamer_slot: slot %d out of range", slot);
+    *dev_ptr = s->dev + (size_t)slot * s->slot_bytes;
+    return DF_OK;
+}
+
+extern "C" int df_streamer_load(df_streamer_s* s, const void* host_src, size_t bytes, int* slot, void** dev_ptr) {
+    clear_error();
+    DF_CHECK(s && host_src && slot, DF_ERR_INVALID, "df_streamer_load: NULL argument");
+    DF_CHECK(bytes <= s->slot_bytes, DF_ERR_INVALID, "df_streamer_load: %zu bytes exceed the slot size %zu", bytes,
+             s->slot_bytes);
+    const int k = s->next;
+    DF_CHECK(s->state[k] != kLoaded, DF_ERR_INVALID,
+             "df_streamer_load: slot %d is still in use (df_streamer_release was not called for it)", k);
+    if (s->state[k] == kReleased) DF_HIP(hipStreamWaitEvent(s->copy, s->released[k], 0), "df_streamer_load");
+    uint8_t* dst = s->dev + (size_t)k * s->slot_bytes;
+    if (bytes) DF_HIP(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, s->copy), "df_streamer_load");
+    DF_HIP(hipEventRecord(s->loaded[k], s->copy), "df_streamer_load");
+    s->state[k] = kLoaded;
+    s->next = (k + 1) % s->slots;
+    *slot = k;
+    if (dev_ptr) *dev_ptr = dst;
+    return DF_OK;
+}
+
+extern "C" int df_streamer_wait(df_streamer_s* s, int slot, void* stream) {
+    clear_error();
+    DF_CHECK(s, DF_ERR_INVALID, "df_streamer_wait: streamer is NULL");
+    DF_CHECK(slot >= 0 && slot < s->slots, DF_ERR_INVALID, "df_streamer_wait: slot %d out of range", slot);
+    DF_CHECK(s->state[slot] == kLoaded, DF_ERR_INVALID, "df_streamer_wait: slot %d holds no load", slot);
+    DF_HIP(hipStreamWaitEvent(as_stream(stream), s->loaded[slot], 0), "df_streamer_wait");
+    return DF_OK;
+}
+
+extern "C" int df_streamer_release(df_streamer_s* s, int slot, void* stream) {
+    clear_error();
+    DF_CHECK(s, DF_ERR_INVALID, "df_streamer_release: streamer is NULL");
+    DF_CHECK(slot >= 0 && slot < s->slots, DF_ERR_INVALID, "df_streamer_release: slot %d out of range", slot);
+    DF_CHECK(s->state[slot] == kLoaded, DF_ERR_INVALID, "df_streamer_release: slot %d holds no load", slot);
+    DF_HIP(hipEventRecord(s->released[slot], as_stream(stream)), "df_streamer_release");
+    s->state[slot] = kReleased;
+    return DF_OK;
+}

@@ -180,6 +180,33 @@ int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ld
                        int dw_dtype, void* dW, int lddw,
                        void* ws, size_t ws_bytes, void* stream);
 
+/* ---- layer weight streaming (new: the reference describes layer-serialized
+ * execution, README.md:212-226, and has its host-side pieces in the NVMe
+ * loader -- pinned cudaHostAlloc buffers, per-slot streams, cudaMemcpyAsync,
+ * apps/host-multi/NVMeLoader_Linux.hpp:20-26,64-71,123-125) ----
+ * A streamer owns `slots` device buffers of slot_bytes (rounded up to 4 KiB)
+ * and a copy stream of default priority.  Per layer:
+ *   df_streamer_load    : copies `bytes` from host memory (pinned, for the
+ *                         copy to be asynchronous) into the next slot in ring
+ *                         order on the copy stream, after the work recorded
+ *                         by that slot's last df_streamer_release;
+ *   df_streamer_wait    : makes `stream` wait until the slot's copy landed;
+ *   df_streamer_release : records, on `stream`, the point after which the
+ *                         slot may be overwritten (call it after enqueuing
+ *                         every launch that reads the slot).
+ * Loading into a slot that was loaded but not released is DF_ERR_INVALID.
+ * One streamer is used by one host thread at a time. */
+typedef struct df_streamer_s df_streamer;
+int df_host_alloc(size_t bytes, void** host_ptr);  /* pinned host memory (hipHostMalloc) */
+int df_host_free(void* host_ptr);
+int df_streamer_create(int slots, size_t slot_bytes, df_streamer** out);
+int df_streamer_destroy(df_streamer* s);             /* waits for its copies first */
+int df_streamer_load(df_streamer* s, const void* host_src, size_t bytes, int* slot, void** dev_ptr);
+int df_streamer_wait(df_streamer* s, int slot, void* stream);
+int df_streamer_release(df_streamer* s, int slot, void* stream);
+int df_streamer_slot(df_streamer* s, int slot, void** dev_ptr);
+int df_streamer_copy_stream(df_streamer* s, void** stream);  /* the hipStream_t of the copies */
+
 /* ---- tensor utilities behind dnn::tensor (dnn/core/tensor.cu:18-52) ---- */
 /* fill_kernel (tensor.cu:19): n elements of elem_bytes (1, 2 or 4) = *value */
 int df_fill(void* dst, int64_t n, int elem_bytes, const void* value_host, void* stream);
