@@ -44,6 +44,7 @@ import time
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 M_TOKENS = 16384
+SINGLE_KERNEL_FAMILIES = ("gemm_fwd", "gemm_dx")
 XL_LINEARS = [("qkv", 1600, 4800), ("attn_proj", 1600, 1600), ("fc", 1600, 6400), ("proj", 6400, 1600)]
 
 
@@ -246,10 +247,14 @@ def main():
         step(tm)
     per = tm.collect()
 
-    # dominant kernel = largest summed time; GEMM families are one kernel
-    # template each (fwd: e4m3 x e4m3 -> bf16 + bias; dx: e5m2 x e4m3 -> bf16;
-    # dw: e5m2 x e4m3 -> fp32).
-    dom = max(per, key=lambda k: per[k][0])
+    # dominant kernel = the largest summed time among the families whose
+    # C-ABI call is exactly one kernel launch: gemm_fwd (the persistent
+    # kernel, e4m3 x e4m3 -> bf16 + bias) and gemm_dx (persistent, e5m2 x e4m3
+    # -> bf16).  gemm_dw is several kernels (split-K partial tiles + their
+    # reduction on the small outputs) and each quantize family two or three
+    # (absmax passes, 2-D quantize, column-sum fold); they are reported in
+    # `kernels` but a per-launch roofline needs one kernel.
+    dom = max(SINGLE_KERNEL_FAMILIES, key=lambda k: per[k][0])
     tot_ms, cnt = per[dom]
     avg_ms = tot_ms / cnt
     if dom in gemm_flops:
@@ -323,19 +328,19 @@ def measured_traffic(kernel_family):
 # MI355X, with TMPDIR=/tmp), and the directories they write.
 PROFILE_COMMANDS = {
     "stats": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_bench -o bench -- "
-              "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion"),
+              "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion --no-streaming"),
     "fetch": ("timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_fetch -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
-              "--no-conversion --no-graph --copy-calibration"),
+              "--no-conversion --no-streaming --no-graph --copy-calibration"),
     "write": ("timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_write -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
-              "--no-conversion --no-graph --copy-calibration"),
+              "--no-conversion --no-streaming --no-graph --copy-calibration"),
 }
-# GEMM families whose C-ABI call is exactly one kernel, by template
-# arguments: <BM, BN, WM, WN, A format, B format, output, bias, split>.
+# GEMM families whose C-ABI call is exactly one kernel, by the persistent
+# kernel's template arguments: <A format, B format, output, bias type, bias>.
 TRAFFIC_FAMILIES = {
-    "gemm_fwd": ("0, 0, unsigned short, unsigned short, false>",),
-    "gemm_dx": ("1, 0, unsigned short, float, false>",),
+    "gemm_fwd": ("gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true>",),
+    "gemm_dx": ("gemm_nt_persistent_kernel<1, 0, unsigned short, float, false>",),
 }
 
 
@@ -397,7 +402,7 @@ def summarize_profiles():
     write = {k: (sum(v) / len(v), len(v)) for k, v in write_all.items()}
     fams = {}
     for fam, pats in TRAFFIC_FAMILIES.items():
-        names = [k for k in fetch if k.startswith("void dfk::gemm") and any(k.endswith(p) for p in pats)]
+        names = [k for k in fetch if k.startswith("void dfk::") and any(k.endswith(p) for p in pats)]
         if len(names) != 1 or names[0] not in write:
             continue
         k = names[0]
