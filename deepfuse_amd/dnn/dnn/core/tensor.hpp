@@ -67,8 +67,10 @@ public:
     float scale() const;
     void set_scale(float s);
 
-    // Serialisation: int ndim, int dims[ndim], raw elements (as the
-    // reference, tensor.cuh:104-125); fp8 tensors append their float scale.
+    // Serialisation: int ndim, int dims[ndim], raw elements (the reference's
+    // layout, tensor.cuh:104-125).  fp8 tensors write a tagged record (a
+    // negative tag, the DType value, then that layout and the float scale);
+    // float and bfloat16 tensors also load such a record, dequantized.
     void save(std::ostream& out) const;
     void load(std::istream& in);
 };

@@ -39,6 +39,11 @@ public:
     void initialize_weights() override;
     void save(std::ostream& out) const override;
     void load(std::istream& in) override;
+    // The reference's layout (in, out, weights, bias; fully_connected_layer.cu:
+    // 388-402) with the weights as an fp8 e4m3 record (codes + scale, a
+    // quarter of the fp32 bytes).  load() reads both forms; the fp8 form
+    // comes back as the dequantized weights.
+    void save_fp8(std::ostream& out) const;
 
 private:
     // device scratch reused across calls, grown on demand

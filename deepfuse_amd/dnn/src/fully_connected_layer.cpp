@@ -168,6 +168,14 @@ void FullyConnectedLayer<TT>::save(std::ostream& out) const {
 }
 
 template <typename TT>
+void FullyConnectedLayer<TT>::save_fp8(std::ostream& out) const {
+    out.write(reinterpret_cast<const char*>(&in_features_), sizeof(in_features_));
+    out.write(reinterpret_cast<const char*>(&out_features_), sizeof(out_features_));
+    quantize<fp8_e4m3>(this->weights_).save(out);
+    this->bias_.save(out);
+}
+
+template <typename TT>
 void FullyConnectedLayer<TT>::load(std::istream& in) {
     in.read(reinterpret_cast<char*>(&in_features_), sizeof(in_features_));
     in.read(reinterpret_cast<char*>(&out_features_), sizeof(out_features_));

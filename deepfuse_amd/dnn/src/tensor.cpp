@@ -220,8 +220,38 @@ void tensor<TT>::set_scale(float s) {
     CHECK_HIP_EX(hipMemcpy(scale_, &s, sizeof(float), hipMemcpyHostToDevice));
 }
 
+// On-disk layout.  Element types the reference has keep its layout
+// unchanged -- int ndim, int dims[ndim], raw elements (tensor.cuh:104-125) --
+// so files move both ways.  fp8 tensors, which have no counterpart there,
+// write a tagged record: int kFp8Tag (negative, so never a valid ndim), int
+// dtype (DType::FP8E4M3 = 5 / FP8E5M2 = 6), int ndim, int dims[ndim], one code
+// per element, float scale.  An fp8 tensor also loads the untagged form (ndim,
+// dims, codes, scale) that earlier builds wrote; a float or bfloat16 tensor
+// loads a tagged fp8 record as its dequantized values (decode(code) * scale).
+namespace {
+constexpr int32_t kFp8Tag = -0x38465044;
+
+template <typename Q>
+tensor<Q> read_fp8_body(std::istream& in, const std::vector<int>& shape) {
+    tensor<Q> q(shape);
+    std::vector<Q> host(q.size());
+    in.read(reinterpret_cast<char*>(host.data()), (std::streamsize)host.size());
+    float s = 1.0f;
+    in.read(reinterpret_cast<char*>(&s), sizeof(s));
+    if (!in) throw std::runtime_error("tensor::load: truncated fp8 record");
+    q.upload(host.data());
+    q.set_scale(s);
+    return q;
+}
+}  // namespace
+
 template <typename TT>
 void tensor<TT>::save(std::ostream& out) const {
+    if constexpr (is_fp8<TT>()) {
+        const int32_t tag = kFp8Tag, dt = dtype_traits<TT>::value;
+        out.write(reinterpret_cast<const char*>(&tag), sizeof(tag));
+        out.write(reinterpret_cast<const char*>(&dt), sizeof(dt));
+    }
     const int ndim = static_cast<int>(shape_.size());
     out.write(reinterpret_cast<const char*>(&ndim), sizeof(ndim));
     out.write(reinterpret_cast<const char*>(shape_.data()), ndim * sizeof(int));
@@ -236,11 +266,36 @@ void tensor<TT>::save(std::ostream& out) const {
 
 template <typename TT>
 void tensor<TT>::load(std::istream& in) {
-    int ndim = 0;
-    in.read(reinterpret_cast<char*>(&ndim), sizeof(ndim));
-    if (!in || ndim < 0 || ndim > 16) throw std::runtime_error("tensor::load: bad header");
+    int first = 0;
+    in.read(reinterpret_cast<char*>(&first), sizeof(first));
+    if (!in) throw std::runtime_error("tensor::load: bad header");
+    int fp8_dtype = -1;
+    if (first == kFp8Tag) {
+        in.read(reinterpret_cast<char*>(&fp8_dtype), sizeof(fp8_dtype));
+        in.read(reinterpret_cast<char*>(&first), sizeof(first));
+        if (!in || (fp8_dtype != DF_DTYPE_FP8E4M3 && fp8_dtype != DF_DTYPE_FP8E5M2))
+            throw std::runtime_error("tensor::load: bad fp8 record header");
+    }
+    const int ndim = first;
+    if (ndim < 0 || ndim > 16) throw std::runtime_error("tensor::load: bad header");
     std::vector<int> shape(ndim);
     in.read(reinterpret_cast<char*>(shape.data()), ndim * sizeof(int));
+    if (!in) throw std::runtime_error("tensor::load: truncated header");
+    if (fp8_dtype >= 0) {
+        if constexpr (is_fp8<TT>()) {
+            if (fp8_dtype != dtype_traits<TT>::value)
+                throw std::runtime_error("tensor::load: the file holds the other fp8 format");
+            *this = read_fp8_body<TT>(in, shape);
+        } else if constexpr (std::is_same_v<TT, float> || std::is_same_v<TT, bfloat16>) {
+            if (fp8_dtype == DF_DTYPE_FP8E4M3)
+                *this = dequantize<TT>(read_fp8_body<fp8_e4m3>(in, shape));
+            else
+                *this = dequantize<TT>(read_fp8_body<fp8_e5m2>(in, shape));
+        } else {
+            throw std::runtime_error("tensor::load: an fp8 record loads into fp8, float or bfloat16 tensors only");
+        }
+        return;
+    }
     *this = tensor<TT>(shape);
     std::vector<TT> host(total_size_);
     in.read(reinterpret_cast<char*>(host.data()), (std::streamsize)total_size_ * sizeof(TT));

@@ -452,6 +452,91 @@ TEST_F(Fp8TensorTest, SaveLoadKeepsScale) {
     EXPECT_THROW(q += r, std::runtime_error);
 }
 
+TEST_F(TensorTest, SaveKeepsTheReferenceLayout) {
+    // int ndim, int dims[ndim], raw elements (dnn/core/tensor.cuh:104-125)
+    tensor<float> t({2, 3});
+    std::vector<float> host = {1, 2, 3, 4, 5, 6};
+    t.upload(host.data());
+    std::stringstream ss;
+    t.save(ss);
+    const std::string b = ss.str();
+    ASSERT_EQ(b.size(), 4u + 8u + 24u);
+    int hdr[3];
+    std::memcpy(hdr, b.data(), sizeof(hdr));
+    EXPECT_EQ(hdr[0], 2);
+    EXPECT_EQ(hdr[1], 2);
+    EXPECT_EQ(hdr[2], 3);
+    EXPECT_EQ(std::memcmp(b.data() + 12, host.data(), 24), 0);
+}
+
+TEST_F(Fp8TensorTest, SaveWritesTaggedRecord) {
+    tensor<float> t({5, 3});
+    const auto x = uniform(15, -4.0f, 4.0f, 21);
+    t.upload(x.data());
+    auto q = quantize<fp8_e5m2>(t);
+    std::stringstream ss;
+    q.save(ss);
+    const std::string b = ss.str();
+    ASSERT_EQ(b.size(), 4u + 4u + 4u + 8u + 15u + 4u);
+    int hdr[5];
+    std::memcpy(hdr, b.data(), sizeof(hdr));
+    EXPECT_LT(hdr[0], 0);                       // tag: never a valid ndim
+    EXPECT_EQ(hdr[1], (int)DType::FP8E5M2);     // 6
+    EXPECT_EQ(hdr[2], 2);
+    EXPECT_EQ(hdr[3], 5);
+    EXPECT_EQ(hdr[4], 3);
+    float s;
+    std::memcpy(&s, b.data() + b.size() - 4, 4);
+    EXPECT_EQ(s, q.scale());
+    // the other fp8 format refuses the record
+    std::stringstream s2(b);
+    tensor<fp8_e4m3> wrong({1});
+    EXPECT_THROW(wrong.load(s2), std::runtime_error);
+    // an integer tensor refuses it too
+    std::stringstream s3(b);
+    tensor<int> wrong_i({1});
+    EXPECT_THROW(wrong_i.load(s3), std::runtime_error);
+}
+
+TEST_F(Fp8TensorTest, FloatTensorsLoadFp8RecordsDequantized) {
+    tensor<float> t({7, 9});
+    const auto x = uniform(63, -30.0f, 30.0f, 22);
+    t.upload(x.data());
+    auto q = quantize<fp8_e4m3>(t);
+    std::stringstream ss;
+    q.save(ss);
+    const std::string b = ss.str();
+    std::stringstream s1(b), s2(b);
+    tensor<float> f({1});
+    f.load(s1);
+    EXPECT_TRUE(f.shape() == t.shape());
+    EXPECT_TRUE(f.equals(dequantize<float>(q)));
+    tensor<bfloat16> h({1});
+    h.load(s2);
+    EXPECT_TRUE(h.equals(dequantize<bfloat16>(q)));
+}
+
+TEST_F(Fp8TensorTest, LoadsUntaggedFp8Record) {
+    // ndim, dims, codes, scale: the form written before the tag existed
+    std::stringstream ss;
+    const int ndim = 1, dim = 4;
+    const uint8_t codes[4] = {0x38, 0xB8, 0x7E, 0x00};  // e4m3: 1, -1, 448, 0
+    const float s = 0.5f;
+    ss.write(reinterpret_cast<const char*>(&ndim), 4);
+    ss.write(reinterpret_cast<const char*>(&dim), 4);
+    ss.write(reinterpret_cast<const char*>(codes), 4);
+    ss.write(reinterpret_cast<const char*>(&s), 4);
+    tensor<fp8_e4m3> q({1});
+    q.load(ss);
+    EXPECT_EQ(q.scale(), 0.5f);
+    const auto back = download(dequantize<float>(q));
+    ASSERT_EQ(back.size(), 4u);
+    EXPECT_EQ(back[0], 0.5f);
+    EXPECT_EQ(back[1], -0.5f);
+    EXPECT_EQ(back[2], 224.0f);
+    EXPECT_EQ(back[3], 0.0f);
+}
+
 // ============================================== FullyConnectedLayerTest ==
 TEST_F(FullyConnectedLayerTest, ConstructorAndInitialization) {
     const int in_features = 4, out_features = 3;
@@ -674,6 +759,33 @@ TEST_F(FullyConnectedLayerTest, SaveLoadRoundTrip) {
     tensor<float> input({2, 12});
     input.fill(0.5f);
     EXPECT_TRUE(a.forward(input).equals(b.forward(input)));
+}
+
+TEST_F(FullyConnectedLayerTest, SaveFp8LoadsDequantizedWeights) {
+    FullyConnectedLayer<float> a(40, 24, false);
+    std::stringstream full, small;
+    a.save(full);
+    a.save_fp8(small);
+    // in, out, fp8 record of W (tag, dtype, ndim, dims, codes, scale), fp32 bias
+    EXPECT_EQ(small.str().size(), 8u + (12u + 8u + 40u * 24u + 4u) + (4u + 16u + 24u * 4u));
+    EXPECT_LT(small.str().size(), full.str().size() / 2);
+    FullyConnectedLayer<float> b(3, 3, false);
+    b.load(small);
+    EXPECT_TRUE(b.weights()->shape() == a.weights()->shape());
+    EXPECT_TRUE(b.weights()->equals(dequantize<float>(quantize<fp8_e4m3>(*a.weights()))));
+    EXPECT_TRUE(b.bias()->equals(*a.bias()));
+    // the reloaded layer quantizes its (dequantized) weights back to codes
+    // within a step of the originals: the forward agrees to the fp8 bound
+    tensor<float> input({4, 40});
+    const auto xi = uniform(160, -1.0f, 1.0f, 31);
+    input.upload(xi.data());
+    const auto ya = download(a.forward(input)), yb = download(b.forward(input));
+    float m = 0.0f, d = 0.0f;
+    for (size_t i = 0; i < ya.size(); ++i) {
+        m = std::max(m, std::fabs(ya[i]));
+        d = std::max(d, std::fabs(ya[i] - yb[i]));
+    }
+    EXPECT_LE(d, 0.07f * m);
 }
 
 int main(int argc, char** argv) { return mini_test::run_all(argc, argv); }
