@@ -102,6 +102,11 @@ _SIGS = {
     "df_streamer_release": (_c_int, [_vp, _c_int, _vp]),
     "df_streamer_slot": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
     "df_streamer_copy_stream": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "df_grad_norm_workspace_bytes": (_c_sz, [_c_int, _vp]),
+    "df_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_clip_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _c_f, _vp, _vp, _c_sz, _vp]),
+    "df_adam_update_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_f, _c_f, _c_f, _c_f, _c_f,
+                                    _c_int, _vp, _c_f, _vp]),
 }
 
 _lib = None
@@ -320,3 +325,45 @@ class WeightStreamer:
             self.close()
         except Exception:
             pass
+
+
+# ----------------------------------------------------------------------------
+# consumer side: global-norm clipping and Adam over lists of fp32 tensors
+# (dnn/utils/clip_grad_norm.cu:31-67, dnn/optimizers/adam_optimizer.cu:11-109)
+# ----------------------------------------------------------------------------
+def _ptrs(tensors):
+    return (_vp * max(len(tensors), 1))(*[t.data_ptr() for t in tensors])
+
+
+def _sizes(tensors):
+    return (_c_i64 * max(len(tensors), 1))(*[t.numel() for t in tensors])
+
+
+def grad_norm(grads, clip: float | None = None):
+    """Global L2 norm of fp32 device tensors as a 1-element device tensor;
+    with ``clip`` the tensors are scaled in place by clip / norm when
+    norm > clip (utils::clip_grad_norm)."""
+    torch = _torch()
+    dev = grads[0].device
+    sizes = _sizes(grads)
+    nbytes = lib().df_grad_norm_workspace_bytes(len(grads), sizes)
+    ws = _scratch(dev, nbytes, "grad_norm")
+    norm = torch.empty(1, dtype=torch.float32, device=dev)
+    if clip is None:
+        call("df_grad_norm_f32", _ptrs(grads), sizes, len(grads), _ptr(norm), _ptr(ws), ws.numel(), _stream())
+    else:
+        call("df_clip_grad_norm_f32", _ptrs(grads), sizes, len(grads), float(clip), _ptr(norm), _ptr(ws),
+             ws.numel(), _stream())
+    return norm
+
+
+def adam_update(params, grads, ms, vs, timestep: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
+                weight_decay=0.0, clip_norm=None, max_norm=0.0):
+    """One Adam step (AdamOptimizer<float>::step) over fp32 device tensors,
+    in place on params, ms and vs; ``clip_norm`` (a device norm from
+    :func:`grad_norm`) applies max_norm / norm to the gradients on the fly."""
+    n = len(params)
+    assert len(grads) == n and len(ms) == n and len(vs) == n
+    call("df_adam_update_f32", _ptrs(params), _ptrs(grads), _ptrs(ms), _ptrs(vs), _sizes(params), n,
+         float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(timestep),
+         _ptr(clip_norm), float(max_norm), _stream())

@@ -9,10 +9,25 @@
 
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "df_capi.h"
 
+namespace dnn {
+template <typename TT>
+struct tensor;
+}
+
 namespace dnn::utils {
+
+// Gradient clipping by global L2 norm, as declared at dnn/utils/common.cuh:
+// 116-119 (defined clip_grad_norm.cu:31-62): when the norm over every
+// element of every tensor exceeds max_norm, each element is multiplied by
+// max_norm / norm.  Provided for T = float.  The norm is computed and
+// compared on the device (the reference downloads each gradient and sums on
+// the host), so the call only enqueues work on Hip::stream().
+template <typename T>
+void clip_grad_norm(std::vector<tensor<T>*>& gradients, T max_norm);
 
 inline void check_hip_error(hipError_t error, const char* file, int line) {
     if (error != hipSuccess) {

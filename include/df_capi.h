@@ -207,6 +207,45 @@ int df_streamer_release(df_streamer* s, int slot, void* stream);
 int df_streamer_slot(df_streamer* s, int slot, void** dev_ptr);
 int df_streamer_copy_stream(df_streamer* s, void** stream);  /* the hipStream_t of the copies */
 
+/* ---- consumer side of the fp32 gradients: global-norm clipping and Adam ----
+ * Lists of fp32 tensors: the pointer arrays and `sizes` are HOST arrays of
+ * `count` entries holding DEVICE pointers (16-byte aligned) and element
+ * counts; zero-size entries are skipped.
+ *
+ * df_grad_norm_f32 writes norm_dev[0] = sqrt(sum over every element of
+ * RN32(g*g)), the squares accumulated in binary64 in a fixed order, the root
+ * rounded once to binary32.  It replaces the host-side norm of
+ * utils::clip_grad_norm (dnn/utils/clip_grad_norm.cu:31-50), which downloads
+ * every gradient and sums in binary32.  `ws` holds
+ * df_grad_norm_workspace_bytes(count, sizes) bytes (8-byte aligned).
+ *
+ * df_clip_grad_norm_f32 is utils::clip_grad_norm (clip_grad_norm.cu:31-67):
+ * the norm as above, then every element g = g * (max_norm / norm) when
+ * norm > max_norm, decided on the device (no host synchronisation).
+ *
+ * df_adam_update_f32 is one AdamOptimizer<float>::step over the list
+ * (dnn/optimizers/adam_optimizer.cu:83-109 with adam_update_kernel's float
+ * path, :24-30), `timestep` the already-incremented step count (>= 1):
+ *   g = grad + wd*p;  m = b1*m + (1-b1)*g;  v = b2*v + (1-b2)*g*g;
+ *   p = p - lr * (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps)
+ * every operation rounded to binary32 (no fused multiply-add), IEEE division
+ * and square root; b^t is rounded to binary32 on the host.  With
+ * clip_norm_dev non-NULL, grad is first multiplied by max_norm / norm when
+ * norm = clip_norm_dev[0] > max_norm: the same values as
+ * df_clip_grad_norm_f32 followed by this call, without rewriting the
+ * gradients. */
+size_t df_grad_norm_workspace_bytes(int count, const int64_t* sizes);
+int df_grad_norm_f32(const float* const* grads, const int64_t* sizes, int count,
+                     float* norm_dev, void* ws, size_t ws_bytes, void* stream);
+int df_clip_grad_norm_f32(float* const* grads, const int64_t* sizes, int count,
+                          float max_norm, float* norm_dev, void* ws, size_t ws_bytes,
+                          void* stream);
+int df_adam_update_f32(float* const* params, const float* const* grads, float* const* m,
+                       float* const* v, const int64_t* sizes, int count, float lr,
+                       float beta1, float beta2, float eps, float weight_decay,
+                       int timestep, const float* clip_norm_dev, float max_norm,
+                       void* stream);
+
 /* ---- tensor utilities behind dnn::tensor (dnn/core/tensor.cu:18-52) ---- */
 /* fill_kernel (tensor.cu:19): n elements of elem_bytes (1, 2 or 4) = *value */
 int df_fill(void* dst, int64_t n, int elem_bytes, const void* value_host, void* stream);

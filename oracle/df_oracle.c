@@ -364,3 +364,72 @@ void dfo_fc_backward_bias(const float* dY, float* db, int N, int out_f) {
         db[o] = sum;
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* Consumer side: global-norm clipping and Adam                             */
+/* ------------------------------------------------------------------------ */
+
+/* Sum of RN32(x*x) in binary64, sequential. */
+double dfo_sumsq(const float* x, int64_t n) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        const float q = x[i] * x[i];
+        s += (double)q;
+    }
+    return s;
+}
+
+/* Product contract: squares in binary32 (clip_grad_norm.cu:41-43 forms them
+ * that way), accumulated in binary64, root rounded once to binary32. */
+float dfo_grad_norm(const float* const* g, const int64_t* n, int count) {
+    double s = 0.0;
+    for (int t = 0; t < count; ++t) s += dfo_sumsq(g[t], n[t]);
+    return (float)sqrt(s);
+}
+
+/* The reference's own host norm, clip_grad_norm.cu:36-50: a binary32
+ * running sum per tensor, binary32 total, sqrt in binary32. */
+float dfo_grad_norm_ref_f32(const float* const* g, const int64_t* n, int count) {
+    float total = 0.0f;
+    for (int t = 0; t < count; ++t) {
+        float sum_sq = 0.0f;
+        for (int64_t i = 0; i < n[t]; ++i) sum_sq += g[t][i] * g[t][i];
+        total += sum_sq;
+    }
+    return sqrtf(total);
+}
+
+/* clip_grad_norm.cu:18 (kernel) and :55 (condition): grad * (max_norm / norm)
+ * when norm > max_norm.  Returns 1 when it scaled. */
+int dfo_clip_scale(float* g, int64_t n, float norm, float max_norm) {
+    if (!(norm > max_norm)) return 0;
+    const float f = max_norm / norm;
+    for (int64_t i = 0; i < n; ++i) g[i] = g[i] * f;
+    return 1;
+}
+
+/* 1 - beta^t: beta^t rounded once to binary32, then the binary32
+ * subtraction (adam_optimizer.cu:28-29 writes T(1.0) - pow(beta, t)). */
+float dfo_bias_correction(float beta, int t) {
+    return 1.0f - (float)pow((double)beta, (double)t);
+}
+
+/* adam_optimizer.cu:24-30 (float path), element by element, each binary32
+ * operation rounded in the order written; `clip_factor` multiplies the
+ * gradient first (1.0f leaves it unchanged). */
+void dfo_adam_step(float* p, const float* grad, float* m, float* v, int64_t n,
+                   float lr, float beta1, float beta2, float eps, float wd, int t,
+                   float clip_factor) {
+    const float bc1 = dfo_bias_correction(beta1, t);
+    const float bc2 = dfo_bias_correction(beta2, t);
+    const float omb1 = 1.0f - beta1, omb2 = 1.0f - beta2;
+    for (int64_t i = 0; i < n; ++i) {
+        const float gr = grad[i] * clip_factor;
+        const float g = gr + wd * p[i];
+        m[i] = beta1 * m[i] + omb1 * g;
+        v[i] = beta2 * v[i] + omb2 * g * g;
+        const float m_hat = m[i] / bc1;
+        const float v_hat = v[i] / bc2;
+        p[i] = p[i] - lr * m_hat / (sqrtf(v_hat) + eps);
+    }
+}

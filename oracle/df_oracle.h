@@ -41,6 +41,17 @@
  *    quantize     : x/s then encode; golden KAT from the reference FC test.
  *    FC loops     : reference KAT y={5.5,10.5} (fully_connected_layer_test.cu
  *                   :266-284), numpy float64 products, closed forms.
+ *    grad norm    : closed forms (sqrt(n) for ones, 3-4-5), numpy binary64
+ *                   pairwise sums, the reference's binary32 host sum on
+ *                   exactly summable inputs and within its error bound.
+ *    clip         : no scaling at norm <= max_norm, clipped norm == max_norm
+ *                   within rounding, factor applied elementwise.
+ *    Adam         : the reference's GTest expectations
+ *                   (tests/optimizers/adam_optimizer_test.cu:21-214), the
+ *                   two-step closed form m_hat = (b1 g1 + g2)/(1 + b1),
+ *                   v_hat = (b2 g1^2 + g2^2)/(1 + b2), the constant-gradient
+ *                   fixed point, coupled (L2) weight decay, exact powers of
+ *                   two for the bias correction.
  */
 #ifndef DF_ORACLE_H
 #define DF_ORACLE_H
@@ -94,6 +105,18 @@ void dfo_fc_backward_input(const float* dY, const float* W, float* dX,
 void dfo_fc_backward_weights(const float* dY, const float* X, float* dW,
                              int N, int in_f, int out_f, int nthreads);
 void dfo_fc_backward_bias(const float* dY, float* db, int N, int out_f);
+
+/* ---- consumer side: global-norm clipping and Adam ----
+ * Follows dnn/utils/clip_grad_norm.cu:13-67 and the float path of
+ * dnn/optimizers/adam_optimizer.cu:11-30,83-109. */
+double dfo_sumsq(const float* x, int64_t n);                  /* sum RN32(x*x), binary64 */
+float dfo_grad_norm(const float* const* g, const int64_t* n, int count);
+float dfo_grad_norm_ref_f32(const float* const* g, const int64_t* n, int count);
+int dfo_clip_scale(float* g, int64_t n, float norm, float max_norm);
+float dfo_bias_correction(float beta, int t);                 /* 1 - RN32(beta^t) */
+void dfo_adam_step(float* p, const float* grad, float* m, float* v, int64_t n,
+                   float lr, float beta1, float beta2, float eps, float wd, int t,
+                   float clip_factor);
 
 #ifdef __cplusplus
 }

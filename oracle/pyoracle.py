@@ -40,6 +40,12 @@ _SIGS = {
     "dfo_fc_backward_input": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "dfo_fc_backward_weights": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "dfo_fc_backward_bias": (None, [_vp, _vp, _i, _i]),
+    "dfo_sumsq": (ctypes.c_double, [_vp, _i64]),
+    "dfo_grad_norm": (_f, [_vp, _vp, _i]),
+    "dfo_grad_norm_ref_f32": (_f, [_vp, _vp, _i]),
+    "dfo_clip_scale": (_i, [_vp, _i64, _f, _f]),
+    "dfo_bias_correction": (_f, [_f, _i]),
+    "dfo_adam_step": (None, [_vp, _vp, _vp, _vp, _i64, _f, _f, _f, _f, _f, _i, _f]),
 }
 
 _lib = None
@@ -190,3 +196,41 @@ def rel_err(y: np.ndarray, r: np.ndarray) -> float:
     den = np.max(np.abs(r)) if r.size else 0.0
     num = np.max(np.abs(y - r)) if r.size else 0.0
     return float(num / den) if den > 0 else float(num)
+
+
+# ---- consumer side: clip and Adam (dnn/utils/clip_grad_norm.cu,
+# dnn/optimizers/adam_optimizer.cu) ----
+def _list(arrays):
+    for a in arrays:
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    ptrs = (_vp * max(len(arrays), 1))(*[a.ctypes.data for a in arrays])
+    sizes = (_i64 * max(len(arrays), 1))(*[a.size for a in arrays])
+    return ptrs, sizes
+
+
+def grad_norm(arrays) -> float:
+    """Product contract: binary32 squares, binary64 sum, one rounding."""
+    ptrs, sizes = _list(arrays)
+    return lib().dfo_grad_norm(ptrs, sizes, len(arrays))
+
+
+def grad_norm_ref_f32(arrays) -> float:
+    """The reference's host loop: binary32 running sums."""
+    ptrs, sizes = _list(arrays)
+    return lib().dfo_grad_norm_ref_f32(ptrs, sizes, len(arrays))
+
+
+def clip_scale(g: np.ndarray, norm: float, max_norm: float) -> bool:
+    assert g.dtype == np.float32
+    return bool(lib().dfo_clip_scale(_p(g), g.size, norm, max_norm))
+
+
+def bias_correction(beta: float, t: int) -> float:
+    return lib().dfo_bias_correction(beta, t)
+
+
+def adam_step(p, g, m, v, t, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.0, clip_factor=1.0):
+    """In place on p, m, v (float32 arrays)."""
+    for a in (p, g, m, v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous and a.size == p.size
+    lib().dfo_adam_step(_p(p), _p(g), _p(m), _p(v), p.size, lr, beta1, beta2, eps, wd, t, clip_factor)

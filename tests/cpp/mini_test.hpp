@@ -122,8 +122,8 @@ inline int run_all(int argc, char** argv) {
 
 #define MT_CMP(fatal, op, a, b)                                                              \
     do {                                                                                     \
-        const auto& mt_a = (a);                                                              \
-        const auto& mt_b = (b);                                                              \
+        const auto mt_a = (a); /* copies: (a) may be an element of a temporary */          \
+        const auto mt_b = (b);                                                               \
         if (!(mt_a op mt_b)) {                                                               \
             mini_test::fail(__FILE__, __LINE__, mini_test::describe(#op, #a, #b, mt_a, mt_b)); \
             if (fatal) throw mini_test::Failure{};                                           \

@@ -1,7 +1,9 @@
 // C++ drop-in tests (namespace dnn), shaped like the reference's GTest
 // suites: tests/core/cuda_test.cu (-> HipTest), tests/core/tensor_test.cu
 // (-> TensorTest), tests/layers/fully_connected_layer_test.cu
-// (-> FullyConnectedLayerTest), plus the fp8 tensor conversions.
+// (-> FullyConnectedLayerTest), tests/optimizers/adam_optimizer_test.cu
+// (-> AdamOptimizerTest), plus the fp8 tensor conversions and gradient
+// clipping (-> ClipGradNormTest).
 //
 // Expected values of the fp8 path come from the CPU oracle
 // (oracle/libdf_oracle.so): the operands are quantized and dequantized by
@@ -23,6 +25,8 @@
 #include "dnn/core/hip.hpp"
 #include "dnn/core/tensor.hpp"
 #include "dnn/layers/fully_connected_layer.hpp"
+#include "dnn/optimizers/adam_optimizer.hpp"
+#include "dnn/utils/common.hpp"
 #include "mini_test.hpp"
 
 using namespace dnn;
@@ -106,6 +110,8 @@ using HipTest = HipFixture;
 using TensorTest = HipFixture;
 using Fp8TensorTest = HipFixture;
 using FullyConnectedLayerTest = HipFixture;
+using AdamOptimizerTest = HipFixture;
+using ClipGradNormTest = HipFixture;
 
 }  // namespace
 
@@ -786,6 +792,204 @@ TEST_F(FullyConnectedLayerTest, SaveFp8LoadsDequantizedWeights) {
         d = std::max(d, std::fabs(ya[i] - yb[i]));
     }
     EXPECT_LE(d, 0.07f * m);
+}
+
+// ---- AdamOptimizer: the reference's cases (adam_optimizer_test.cu:21-214),
+// plus exact agreement with the oracle's step ----
+TEST_F(AdamOptimizerTest, BasicUpdate) {
+    tensor<float> param1({2, 2}), param2({2, 2}), grad1({2, 2}), grad2({2, 2});
+    param1.fill(1.0f);
+    param2.fill(2.0f);
+    grad1.fill(0.1f);
+    grad2.fill(0.2f);
+    AdamOptimizer<float> optimizer(0.001f);
+    optimizer.update_parameters({&param1, &param2}, {&grad1, &grad2});
+    optimizer.step();
+    EXPECT_LT(download(param1)[0], 1.0f);
+    EXPECT_LT(download(param2)[0], 2.0f);
+}
+
+TEST_F(AdamOptimizerTest, MomentumAndRMS) {
+    tensor<float> param({2, 2}), grad({2, 2});
+    param.fill(1.0f);
+    grad.fill(0.1f);
+    AdamOptimizer<float> optimizer(0.001f, 0.9f, 0.999f);
+    optimizer.update_parameters({&param}, {&grad});
+    optimizer.step();
+    const float first = download(param)[0];
+    optimizer.step();
+    EXPECT_NE(first, download(param)[0]);
+}
+
+TEST_F(AdamOptimizerTest, WeightDecay) {
+    tensor<float> param({2, 2}), grad({2, 2});
+    param.fill(1.0f);
+    grad.fill(0.1f);
+    AdamOptimizer<float> optimizer(0.001f, 0.9f, 0.999f, 1e-8f, 0.1f);
+    optimizer.update_parameters({&param}, {&grad});
+    optimizer.step();
+    EXPECT_GT(1.0f - download(param)[0], 0.0f);
+}
+
+TEST_F(AdamOptimizerTest, ZeroGrad) {
+    tensor<float> param({2, 2}), grad({2, 2});
+    param.fill(1.0f);
+    grad.fill(0.1f);
+    AdamOptimizer<float> optimizer(0.001f);
+    optimizer.update_parameters({&param}, {&grad});
+    optimizer.zero_grad();
+    for (float g : download(grad)) EXPECT_EQ(g, 0.0f);
+}
+
+TEST_F(AdamOptimizerTest, LearningRateChange) {
+    tensor<float> param({2, 2}), grad({2, 2});
+    param.fill(1.0f);
+    grad.fill(0.1f);
+    AdamOptimizer<float> optimizer(0.001f);
+    optimizer.update_parameters({&param}, {&grad});
+    optimizer.step();
+    const float first = download(param)[0];
+    optimizer.set_learning_rate(0.002f);
+    optimizer.step();
+    const float second = download(param)[0];
+    EXPECT_GT(std::abs(second - first), std::abs(first - 1.0f));
+}
+
+TEST_F(AdamOptimizerTest, ParameterUpdate) {
+    tensor<float> param1({2, 2}), grad1({2, 2});
+    param1.fill(1.0f);
+    grad1.fill(0.1f);
+    AdamOptimizer<float> optimizer(0.001f);
+    optimizer.update_parameters({&param1}, {&grad1});
+    optimizer.step();
+    const float first = download(param1)[0];
+    tensor<float> new_param({2, 2}), new_grad({2, 2});
+    new_param.fill(3.0f);
+    new_grad.fill(0.3f);
+    optimizer.update_parameters({&new_param}, {&new_grad});
+    optimizer.step();
+    EXPECT_EQ(download(param1)[0], first);
+    EXPECT_NE(download(new_param)[0], 3.0f);
+}
+
+// A Linear layer's parameters through three steps, against the oracle's
+// element-by-element restatement, bit for bit.
+TEST_F(AdamOptimizerTest, LinearLayerStepsMatchOracle) {
+    FullyConnectedLayer<float> fc(96, 40, true);
+    tensor<float> x({33, 96});
+    const auto xh = uniform(33 * 96, -1.0f, 1.0f, 41);
+    x.upload(xh.data());
+    tensor<float> gy({33, 40});
+    const auto gyh = uniform(33 * 40, -1.0f, 1.0f, 42);
+    gy.upload(gyh.data());
+    AdamOptimizer<float> opt(0.01f, 0.9f, 0.999f, 1e-8f, 0.01f);
+    opt.update_parameters(fc.parameters(), fc.gradients());
+    std::vector<std::vector<float>> p, m, v;
+    for (auto* t : fc.parameters()) {
+        p.push_back(download(*t));
+        m.emplace_back(t->size(), 0.0f);
+        v.emplace_back(t->size(), 0.0f);
+    }
+    for (int step = 1; step <= 3; ++step) {
+        fc.forward(x);
+        fc.backward(gy);
+        const auto grads = fc.gradients();
+        std::vector<std::vector<float>> g;
+        for (auto* t : grads) g.push_back(download(*t));
+        opt.step();
+        for (size_t i = 0; i < p.size(); ++i)
+            dfo_adam_step(p[i].data(), g[i].data(), m[i].data(), v[i].data(), (int64_t)p[i].size(), 0.01f, 0.9f,
+                          0.999f, 1e-8f, 0.01f, step, 1.0f);
+    }
+    const auto params = fc.parameters();
+    for (size_t i = 0; i < p.size(); ++i) {
+        EXPECT_TRUE(download(*params[i]) == p[i]);
+        EXPECT_TRUE(download(opt.first_moment(params[i])) == m[i]);
+        EXPECT_TRUE(download(opt.second_moment(params[i])) == v[i]);
+    }
+    EXPECT_EQ(opt.timestep(), 3);
+}
+
+// step_clipped(max_norm) == clip_grad_norm(grads, max_norm) + step(), except
+// that the gradients keep their values.
+TEST_F(AdamOptimizerTest, StepClippedEqualsClipThenStep) {
+    std::vector<std::unique_ptr<tensor<float>>> pa, pb, ga, gb;
+    const int sizes[3] = {5000, 8192 * 3 + 7, 12};
+    for (int i = 0; i < 3; ++i) {
+        const auto ph = uniform(sizes[i], -1.0f, 1.0f, 50 + i);
+        const auto gh = uniform(sizes[i], -2.0f, 2.0f, 60 + i);
+        for (auto* vec : {&pa, &pb}) {
+            vec->push_back(std::make_unique<tensor<float>>(std::vector<int>{sizes[i]}));
+            vec->back()->upload(ph.data());
+        }
+        for (auto* vec : {&ga, &gb}) {
+            vec->push_back(std::make_unique<tensor<float>>(std::vector<int>{sizes[i]}));
+            vec->back()->upload(gh.data());
+        }
+    }
+    auto raw = [](std::vector<std::unique_ptr<tensor<float>>>& v) {
+        std::vector<tensor<float>*> r;
+        for (auto& t : v) r.push_back(t.get());
+        return r;
+    };
+    auto pra = raw(pa), prb = raw(pb), gra = raw(ga), grb = raw(gb);
+    AdamOptimizer<float> a(0.001f), b(0.001f);
+    a.update_parameters(pra, gra);
+    b.update_parameters(prb, grb);
+    const auto g0 = download(*ga[1]);
+    utils::clip_grad_norm(gra, 1.0f);
+    a.step();
+    b.step_clipped(1.0f);
+    for (int i = 0; i < 3; ++i) EXPECT_TRUE(download(*pa[i]) == download(*pb[i]));
+    EXPECT_TRUE(download(*gb[1]) == g0);   // fused: gradients unchanged
+    EXPECT_FALSE(download(*ga[1]) == g0);  // reference order: clipped in place
+}
+
+// ---- clip_grad_norm (clip_grad_norm.cu:31-62) ----
+TEST_F(ClipGradNormTest, ScalesWhenAboveMaxNorm) {
+    tensor<float> a({1}), b({1});
+    const float three = 3.0f, four = 4.0f;
+    a.upload(&three);
+    b.upload(&four);
+    std::vector<tensor<float>*> grads{&a, &b};
+    utils::clip_grad_norm(grads, 1.0f);
+    const float f = 1.0f / 5.0f;
+    EXPECT_EQ(download(a)[0], 3.0f * f);
+    EXPECT_EQ(download(b)[0], 4.0f * f);
+}
+
+TEST_F(ClipGradNormTest, LeavesGradientsAtOrBelowMaxNorm) {
+    tensor<float> a({1}), b({1});
+    const float three = 3.0f, four = 4.0f;
+    a.upload(&three);
+    b.upload(&four);
+    std::vector<tensor<float>*> grads{&a, &b};
+    utils::clip_grad_norm(grads, 5.0f);
+    EXPECT_EQ(download(a)[0], 3.0f);
+    utils::clip_grad_norm(grads, 6.0f);
+    EXPECT_EQ(download(b)[0], 4.0f);
+}
+
+TEST_F(ClipGradNormTest, MatchesOracleOnLayerGradients) {
+    FullyConnectedLayer<float> fc(300, 200, true);
+    tensor<float> x({64, 300}), gy({64, 200});
+    const auto xh = uniform(64 * 300, -1.0f, 1.0f, 71), gh = uniform(64 * 200, -1.0f, 1.0f, 72);
+    x.upload(xh.data());
+    gy.upload(gh.data());
+    fc.forward(x);
+    fc.backward(gy);
+    auto grads = fc.gradients();
+    std::vector<std::vector<float>> host;
+    for (auto* t : grads) host.push_back(download(*t));
+    const float* ptrs[2] = {host[0].data(), host[1].data()};
+    const int64_t n[2] = {(int64_t)host[0].size(), (int64_t)host[1].size()};
+    const float norm = dfo_grad_norm(ptrs, n, 2);
+    EXPECT_GT(norm, 1.0f);
+    utils::clip_grad_norm(grads, 1.0f);
+    for (int i = 0; i < 2; ++i) {
+        dfo_clip_scale(host[i].data(), n[i], norm, 1.0f);
+        EXPECT_TRUE(download(*grads[i]) == host[i]);
+    }
 }
 
 int main(int argc, char** argv) { return mini_test::run_all(argc, argv); }

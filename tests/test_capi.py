@@ -72,6 +72,28 @@ def test_argument_errors():
     assert status("df_fill", FAKE, 4, 3, ctypes.byref(ctypes.c_int(0)), None) == -2
     assert status("df_add", 99, FAKE, FAKE, FAKE, 4, None) == -2
     assert status("df_approx_equal_mask", int(DType.FP8E4M3), FAKE, FAKE, FAKE, 4, 0.1, None) == -2
+    # clip / Adam lists
+    P = ctypes.c_void_p
+    sizes = (ctypes.c_int64 * 3)(8192, 8193, 0)
+    assert df.lib().df_grad_norm_workspace_bytes(3, sizes) == 3 * 8
+    assert df.lib().df_grad_norm_workspace_bytes(0, None) == 8
+    ptrs = (P * 3)(FAKE, FAKE + 16, None)  # the empty entry may be NULL
+    assert status("df_grad_norm_f32", ptrs, sizes, 3, FAKE, FAKE, 16, None) == -5
+    assert status("df_grad_norm_f32", ptrs, sizes, 3, FAKE, FAKE + 4, 64, None) == -4  # ws alignment
+    bad = (P * 3)(FAKE, FAKE + 4, None)
+    assert status("df_clip_grad_norm_f32", bad, sizes, 3, 1.0, FAKE, FAKE, 64, None) == -4
+    neg = (ctypes.c_int64 * 1)(-1)
+    assert status("df_grad_norm_f32", ptrs, neg, 1, FAKE, FAKE, 64, None) == -1
+    nul = (P * 1)(None)
+    one = (ctypes.c_int64 * 1)(4)
+    assert status("df_adam_update_f32", nul, nul, nul, nul, one, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1,
+                  None, 0.0, None) == -1
+    ok = (P * 1)(FAKE)
+    assert status("df_adam_update_f32", ok, ok, ok, ok, one, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 0,
+                  None, 0.0, None) == -1
+    assert "timestep" in err()
+    assert status("df_adam_update_f32", ok, ok, (P * 1)(FAKE + 8), ok, one, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1,
+                  None, 0.0, None) == -4
 
 
 def test_error_raises_in_python_binding():

@@ -11,7 +11,8 @@ import pytest
 HERE = os.path.dirname(os.path.abspath(__file__))
 RUNNER = os.path.join(HERE, "cpp", "dnn_tests")
 
-SUITES = ("HipTest", "TensorTest", "Fp8TensorTest", "FullyConnectedLayerTest")
+SUITES = ("HipTest", "TensorTest", "Fp8TensorTest", "FullyConnectedLayerTest", "AdamOptimizerTest",
+          "ClipGradNormTest")
 
 
 def _runner():
