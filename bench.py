@@ -56,6 +56,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-conversion", action="store_true")
     p.add_argument("--no-streaming", action="store_true", help="skip the config 5 layer-streaming leg")
+    p.add_argument("--no-optimizer", action="store_true", help="skip the clip + Adam leg")
     p.add_argument("--stream-layers", type=int, default=48)
     p.add_argument("--stream-slots", type=int, default=4)
     p.add_argument("--cpu-tokens", type=int, default=3072, help="token slice for the CPU baseline")
@@ -303,6 +304,8 @@ def main():
     }
     if not args.no_conversion:
         out["conversion"] = conversion_bench(torch, df, synth, dev, cur())
+    if not args.no_optimizer:
+        out["optimizer"] = optimizer_bench(torch, df, dev, cur(), layers=args.stream_layers)
     if not args.no_streaming:
         out["streaming"] = streaming_bench(torch, df, synth, dev, layers=args.stream_layers,
                                            slots=args.stream_slots)
@@ -471,6 +474,95 @@ def conversion_bench(torch, df, synth, dev, stream, reps=10):
                 res[f"{kname}_{src}_{fname}"] = {"ms": round(ms, 4), "gbs": round(gbs, 1),
                                                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
     del x32, x16, q, o32, o16
+    torch.cuda.empty_cache()
+    return res
+
+
+def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
+    """Consumer side of dW over the GPT-2 XL stack's Linear parameters
+    (48 x {qkv, proj, fc1, fc2} weights and biases, fp32): the global norm,
+    clip in place, the Adam update, and the two orders of a clipped step --
+    the reference's (clip_grad_norm then Adam::step) and the fused one (norm,
+    then Adam applying the clip factor).  HBM bytes per element: norm 4,
+    clip 4 + 8, Adam 16 read + 12 written; the clipped orders clip on every
+    call."""
+    import ctypes
+    shapes = []
+    for _ in range(layers):
+        for _, k, o in XL_LINEARS:
+            shapes += [(o, k), (o,)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    P = [torch.randn(s, device=dev, generator=gen) * 0.02 for s in shapes]
+    G = [torch.randn(s, device=dev, generator=gen) * 1e-3 for s in shapes]
+    M = [torch.zeros(s, device=dev) for s in shapes]
+    V = [torch.zeros(s, device=dev) for s in shapes]
+    n = sum(t.numel() for t in P)
+    cnt = len(P)
+    arr = lambda ts: (ctypes.c_void_p * cnt)(*[t.data_ptr() for t in ts])
+    pp, gp, mp, vp = arr(P), arr(G), arr(M), arr(V)
+    sizes = (ctypes.c_int64 * cnt)(*[t.numel() for t in P])
+    wsb = df.lib().df_grad_norm_workspace_bytes(cnt, sizes)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    norm = torch.empty(1, dtype=torch.float32, device=dev)
+    step = [0]
+
+    def gnorm():
+        df.call("df_grad_norm_f32", gp, sizes, cnt, norm.data_ptr(), ws.data_ptr(), wsb, stream)
+
+    gnorm()
+    torch.cuda.synchronize()
+    n0 = norm.item()
+    calls = [0]
+
+    def clip():
+        # every call clips: max_norm is half the norm the previous call left
+        # (the k-th call sees norm ~ n0 / 2^k), so each pass rewrites the
+        # gradients, as a clipping step of the reference does
+        k = calls[0]
+        calls[0] += 1
+        df.call("df_clip_grad_norm_f32", gp, sizes, cnt, n0 * 0.5 ** (k + 1), norm.data_ptr(), ws.data_ptr(),
+                wsb, stream)
+
+    def adam(clip_norm=None):
+        step[0] += 1
+        df.call("df_adam_update_f32", pp, gp, mp, vp, sizes, cnt, 1e-4, 0.9, 0.999, 1e-8, 0.0, step[0],
+                clip_norm, 1.0, stream)
+
+    def fused():
+        gnorm()
+        adam(norm.data_ptr())
+
+    def reference_order():
+        clip()
+        adam()
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    res = {"params": n, "tensors": cnt, "layers": layers}
+    # context: a plain device-to-device copy of 4 GiB (read + write)
+    a = torch.empty(1 << 30, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    ms = timed(lambda: b.copy_(a))
+    res["copy_4GiB"] = {"ms": round(ms, 3), "gbs": round(2 * a.numel() * 4 / (ms * 1e-3) / 1e9, 1)}
+    del a, b
+    for name, fn, bpe in (("grad_norm", gnorm, 4), ("adam", adam, 28), ("clip_then_adam", reference_order, 40),
+                          ("fused_clip_adam", fused, 32)):
+        ms = timed(fn)
+        gbs = n * bpe / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 3), "bytes_per_param": bpe, "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    res["fused_saving"] = round(1 - res["fused_clip_adam"]["ms"] / res["clip_then_adam"]["ms"], 3)
+    del P, G, M, V
     torch.cuda.empty_cache()
     return res
 

@@ -102,6 +102,10 @@ _SIGS = {
     "df_streamer_release": (_c_int, [_vp, _c_int, _vp]),
     "df_streamer_slot": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
     "df_streamer_copy_stream": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "df_amax_history_init": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp]),
+    "df_quantize_2d_delayed_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "df_quantize_2d_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp,
+                                        _c_int, _vp, _c_int, _vp, _vp, _c_sz, _vp]),
     "df_grad_norm_workspace_bytes": (_c_sz, [_c_int, _vp]),
     "df_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _vp, _vp, _c_sz, _vp]),
     "df_clip_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _c_f, _vp, _vp, _c_sz, _vp]),
@@ -367,3 +371,35 @@ def adam_update(params, grads, ms, vs, timestep: int, lr=1e-3, beta1=0.9, beta2=
     call("df_adam_update_f32", _ptrs(params), _ptrs(grads), _ptrs(ms), _ptrs(vs), _sizes(params), n,
          float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(timestep),
          _ptr(clip_norm), float(max_norm), _stream())
+
+
+# ----------------------------------------------------------------------------
+# delayed scaling: scale from an amax history, absmax measured in the pass
+# ----------------------------------------------------------------------------
+class DelayedScale:
+    """History and scale of one tensor role (fp32 device tensors)."""
+
+    def __init__(self, fmt: Fmt, length: int, device, seed_amax=None):
+        torch = _torch()
+        self.fmt = Fmt(fmt)
+        self.history = torch.empty(length, dtype=torch.float32, device=device)
+        self.scale = torch.empty(1, dtype=torch.float32, device=device)
+        call("df_amax_history_init", _ptr(seed_amax), int(self.fmt), _ptr(self.history), length,
+             _ptr(self.scale), _stream())
+
+    def quantize_2d(self, x, want_q=True, want_qt=False, colsum=False):
+        """Like :func:`quantize_2d` with the current scale; returns
+        (q, qt[, colsum]) and advances the history."""
+        torch = _torch()
+        rows, cols = x.shape
+        q = torch.empty((rows, round16(cols)), dtype=torch.uint8, device=x.device) if want_q else None
+        qt = torch.empty((cols, round16(rows)), dtype=torch.uint8, device=x.device) if want_qt else None
+        ldq = q.shape[1] if q is not None else 0
+        ldqt = qt.shape[1] if qt is not None else 0
+        cs = torch.empty(cols, dtype=torch.float32, device=x.device) if colsum else None
+        nbytes = lib().df_quantize_2d_delayed_workspace_bytes(rows, cols, ldq, ldqt, int(colsum))
+        ws = _scratch(x.device, nbytes, "delayed")
+        call("df_quantize_2d_delayed", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), int(self.fmt),
+             _ptr(self.scale), _ptr(self.scale), _ptr(self.history), self.history.numel(), _ptr(q), ldq, _ptr(qt),
+             ldqt, _ptr(cs), _ptr(ws), ws.numel(), _stream())
+        return (q, qt, cs) if colsum else (q, qt)

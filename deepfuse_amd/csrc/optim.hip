@@ -93,34 +93,55 @@ __device__ __forceinline__ double block_sum_f64(double s) {
 
 __device__ __forceinline__ double sq(float x) { return (double)(x * x); }
 
-// Stage 1 of the norm: one binary64 partial per block.
+// Stage 1 of the norm: one binary64 partial per block of kNormSub chunks
+// (fewer partials for the single-block stage 2 to fold).
+constexpr int kNormSub = 4;
+constexpr int64_t kNormChunk = kChunk * kNormSub;
+
 __global__ __launch_bounds__(kOThreads) void sumsq_kernel(const NormList L, double* __restrict__ partial,
                                                           int part0) {
     const int b = blockIdx.x;
     const int t = owner(L.first, L.count, b);
     const float* x = L.ptr[t];
     const int64_t n = L.n[t];
-    const int64_t base = (int64_t)(b - L.first[t]) * kChunk;
     double acc = 0.0;
-    if (base + kChunk <= n) {
-        const f32x4* xv = reinterpret_cast<const f32x4*>(x + base);
-        f32x4 r[kVec];
+    for (int sub = 0; sub < kNormSub; ++sub) {
+        const int64_t base = (int64_t)(b - L.first[t]) * kNormChunk + sub * kChunk;
+        if (base + kChunk <= n) {
+            const f32x4* xv = reinterpret_cast<const f32x4*>(x + base);
+            f32x4 r[kVec];
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) r[k] = __builtin_nontemporal_load(xv + k * kOThreads + threadIdx.x);
+            for (int k = 0; k < kVec; ++k) r[k] = __builtin_nontemporal_load(xv + k * kOThreads + threadIdx.x);
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) acc += sq(r[k].x) + sq(r[k].y) + sq(r[k].z) + sq(r[k].w);
-    } else {
-        for (int64_t i = base + threadIdx.x; i < n; i += kOThreads) acc += sq(x[i]);
+            for (int k = 0; k < kVec; ++k) acc += sq(r[k].x) + sq(r[k].y) + sq(r[k].z) + sq(r[k].w);
+        } else {
+            for (int64_t i = base + threadIdx.x; i < n; i += kOThreads) acc += sq(x[i]);
+            break;
+        }
     }
     acc = block_sum_f64(acc);
     if (threadIdx.x == 0) partial[part0 + b] = acc;
 }
 
 // Stage 2: fixed-order fold of every partial; norm = RN32(sqrt(sum)).
+// A GPT-2 XL sized list leaves ~180K partials: each thread keeps kFold
+// independent loads in flight (a single dependent chain per thread made this
+// one-block pass latency-bound).
+constexpr int kFold = 8;
 __global__ __launch_bounds__(kOThreads) void norm_finalize_kernel(const double* __restrict__ partial, int nparts,
                                                                   float* __restrict__ norm_out) {
+    double acc[kFold];
+#pragma unroll
+    for (int j = 0; j < kFold; ++j) acc[j] = 0.0;
+    int i = threadIdx.x;
+    for (; i + (kFold - 1) * kOThreads < nparts; i += kFold * kOThreads) {
+#pragma unroll
+        for (int j = 0; j < kFold; ++j) acc[j] += partial[i + j * kOThreads];
+    }
+    for (; i < nparts; i += kOThreads) acc[0] += partial[i];
     double s = 0.0;
-    for (int i = threadIdx.x; i < nparts; i += kOThreads) s += partial[i];
+#pragma unroll
+    for (int j = 0; j < kFold; ++j) s += acc[j];
     s = block_sum_f64(s);
     if (threadIdx.x == 0) norm_out[0] = (float)sqrt(s);
 }
@@ -194,9 +215,9 @@ __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const
             for (int k = 0; k < kVec / 2; ++k) {
                 const int i = (half * (kVec / 2) + k) * kOThreads + threadIdx.x;
                 rg[k] = __builtin_nontemporal_load(gv + i);
-                rp[k] = pv[i];
-                rm[k] = mv[i];
-                rv[k] = vv[i];
+                rp[k] = __builtin_nontemporal_load(pv + i);
+                rm[k] = __builtin_nontemporal_load(mv + i);
+                rv[k] = __builtin_nontemporal_load(vv + i);
             }
 #pragma unroll
             for (int k = 0; k < kVec / 2; ++k) {
@@ -209,9 +230,9 @@ __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const
                     rm[k][e] = mm;
                     rv[k][e] = ve;
                 }
-                pv[i] = rp[k];
-                mv[i] = rm[k];
-                vv[i] = rv[k];
+                __builtin_nontemporal_store(rp[k], pv + i);
+                __builtin_nontemporal_store(rm[k], mv + i);
+                __builtin_nontemporal_store(rv[k], vv + i);
             }
         }
     } else {
@@ -226,6 +247,7 @@ __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const
 }
 
 int64_t chunks(int64_t n) { return (n + kChunk - 1) / kChunk; }
+int64_t norm_chunks(int64_t n) { return (n + kNormChunk - 1) / kNormChunk; }
 
 // Blocks of a whole list, or -1 when a launch would exceed the grid limit.
 int64_t total_blocks(const int64_t* sizes, int count) {
@@ -261,7 +283,7 @@ int launch_sumsq(const float* const* grads, const int64_t* sizes, int count, dou
             L.ptr[c] = const_cast<float*>(grads[i0]);
             L.n[c] = sizes[i0];
             L.first[c] = blocks;
-            blocks += (int)chunks(sizes[i0]);
+            blocks += (int)norm_chunks(sizes[i0]);
             ++c;
         }
         if (c == 0) break;
@@ -282,7 +304,7 @@ using namespace dfk;
 extern "C" size_t df_grad_norm_workspace_bytes(int count, const int64_t* sizes) {
     if (count < 0 || (count > 0 && !sizes)) return 0;
     int64_t b = 0;
-    for (int i = 0; i < count; ++i) b += sizes[i] > 0 ? chunks(sizes[i]) : 0;
+    for (int i = 0; i < count; ++i) b += sizes[i] > 0 ? norm_chunks(sizes[i]) : 0;
     return (size_t)(b > 0 ? b : 1) * sizeof(double);
 }
 

@@ -305,13 +305,17 @@ template <> struct Ld<uint16_t> {
     static __device__ __forceinline__ float one(const uint16_t* p) { return bf16_to_f32(*p); }
 };
 
-template <typename InT, int FMT, bool COLSUM, bool CODES>
+// With AMAX the block also folds |x| over finite values of its tile into one
+// partial maximum (binary32 bit pattern), amaxpart[tile index], for the
+// delayed-scaling history.
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false>
 __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
                                                                 int cols, int ldx, bool vec_ok,
                                                                 const float* __restrict__ scale,
                                                                 uint8_t* __restrict__ q, int ldq,
                                                                 uint8_t* __restrict__ qt, int ldqt,
-                                                                float* __restrict__ colpart) {
+                                                                float* __restrict__ colpart,
+                                                                uint32_t* __restrict__ amaxpart = nullptr) {
     constexpr int E = Ld<InT>::E;      // elements per 16-byte load
     constexpr int TPR = kT2 / E;       // threads per tile row
     constexpr int RG = kThreads / TPR; // row groups
@@ -327,6 +331,7 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
     const bool full = vec_ok && c + E <= cols;
     uint32_t codes[RPT][E / 4];
     float cs[E];
+    uint32_t am = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) cs[e] = 0.0f;
 #pragma unroll
@@ -343,6 +348,10 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
         if (COLSUM) {
 #pragma unroll
             for (int e = 0; e < E; ++e) cs[e] += v[e];
+        }
+        if (AMAX) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) am = fold_f32(am, __float_as_uint(v[e]));
         }
         if (!CODES) continue;
 #pragma unroll
@@ -391,12 +400,61 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
                     *reinterpret_cast<const u32x4*>(tile + col * TSTRIDE + rc);
         }
     }
-    if (COLSUM && threadIdx.x < kT2 && c0 + threadIdx.x < cols) {
+    if (COLSUM && r0 < rows && threadIdx.x < kT2 && c0 + threadIdx.x < cols) {
         float sum = 0.0f;
 #pragma unroll
         for (int g = 0; g < RG; ++g) sum += csum[g][threadIdx.x];
         colpart[(int64_t)blockIdx.y * cols + c0 + threadIdx.x] = sum;
     }
+    if (AMAX) {
+        am = block_max_u32(am);
+        if (threadIdx.x == 0) amaxpart[blockIdx.y * gridDim.x + blockIdx.x] = am;
+    }
+}
+
+// Delayed scaling, stage 2: one block folds the tile maxima of this pass
+// into its absmax, pushes it into the history (history[0] newest; the others
+// move one place, the oldest drops out) and writes the scale for the next
+// pass from the history's maximum (rule D1/D2).  len <= kMaxHistory.
+constexpr int kMaxHistory = 1024;
+__global__ __launch_bounds__(kThreads) void amax_history_kernel(const uint32_t* __restrict__ partial, int nparts,
+                                                                 int fmt, float* __restrict__ history, int len,
+                                                                 float* __restrict__ scale_out) {
+    __shared__ uint32_t cur;
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
+    m = block_max_u32(m);
+    if (threadIdx.x == 0) cur = m;
+    constexpr int PER = kMaxHistory / kThreads;
+    float old[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = threadIdx.x + k * kThreads;
+        old[k] = i < len ? history[i] : 0.0f;
+    }
+    __syncthreads();  // every old value read, cur published
+    uint32_t hm = cur;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = threadIdx.x + k * kThreads;
+        if (i + 1 < len) {
+            history[i + 1] = old[k];
+            hm = max(hm, __float_as_uint(old[k]));
+        }
+    }
+    if (threadIdx.x == 0) history[0] = __uint_as_float(cur);
+    hm = block_max_u32(hm);
+    if (threadIdx.x == 0) scale_out[0] = scale_from_absmax(__uint_as_float(hm), fmt);
+}
+
+// history[0..len) = amax (or 0 when amax is NULL), scale from it.
+__global__ __launch_bounds__(kThreads) void amax_history_init_kernel(const float* __restrict__ amax, int fmt,
+                                                                      float* __restrict__ history, int len,
+                                                                      float* __restrict__ scale_out) {
+    const float a = amax ? amax[0] : 0.0f;
+    const float v = (a > 0.0f && a <= 3.4028234663852886e38f) ? a : 0.0f;
+    for (int i = threadIdx.x; i < len; i += kThreads) history[i] = v;
+    if (threadIdx.x == 0) scale_out[0] = scale_from_absmax(v, fmt);
 }
 
 // out[c] = sum over tile rows of colpart[t][c].  A block owns 64 columns;
@@ -581,13 +639,32 @@ extern "C" size_t df_quantize_2d_workspace_bytes(int rows, int cols) {
     return (size_t)((rows + kT2 - 1) / kT2) * (size_t)cols * sizeof(float);
 }
 
+// Tile grid of a 2-D quantize: covers the codes' padded extents.
+static dim3 q2d_grid(int rows, int cols, const uint8_t* q, int ldq, const uint8_t* qt, int ldqt) {
+    const int row_ext = qt ? (rows > ldqt ? rows : ldqt) : rows;
+    const int col_ext = q ? (cols > ldq ? cols : ldq) : cols;
+    return dim3((col_ext + kT2 - 1) / kT2, (row_ext + kT2 - 1) / kT2);
+}
+
+// Delayed-scaling workspace: column-sum partials (when asked for), then one
+// tile maximum per block, 16-byte aligned.
+static size_t delayed_ws_layout(int rows, int cols, int ldq, int ldqt, bool colsum, size_t* amax_off) {
+    const size_t cs = colsum ? df_quantize_2d_workspace_bytes(rows, cols) : 0;
+    const size_t off = (cs + 15) & ~(size_t)15;
+    const dim3 g = q2d_grid(rows, cols, (const uint8_t*)1, ldq, ldqt > 0 ? (const uint8_t*)1 : nullptr, ldqt);
+    if (amax_off) *amax_off = off;
+    return off + (size_t)g.x * g.y * sizeof(uint32_t);
+}
+
 static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int rows, int cols, int ldx,
                             int fmt, const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
-                            float* colsum, void* ws, size_t ws_bytes, void* stream) {
+                            float* colsum, void* ws, size_t ws_bytes, void* stream,
+                            float* history = nullptr, int hist_len = 0, float* next_scale = nullptr) {
     clear_error();
-    DF_CHECK(rows >= 0 && cols >= 0 && ldx >= cols, DF_ERR_INVALID,
+    DF_CHECK(rows >= 0 && cols >= 0 && (ldx >= cols || rows == 0), DF_ERR_INVALID,
              "%s: bad shape rows=%d cols=%d ldx=%d", name, rows, cols, ldx);
-    DF_CHECK(q || qt || colsum, DF_ERR_INVALID, "%s: no output", name);
+    const bool empty = rows == 0 || cols == 0;  // nothing to write: outputs may be NULL
+    DF_CHECK(q || qt || colsum || empty, DF_ERR_INVALID, "%s: no output", name);
     DF_CHECK((scale_dev || (!q && !qt)) && (x || rows * (int64_t)cols == 0), DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad format %d", name, fmt);
     DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
@@ -600,30 +677,48 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
         DF_CHECK(ldqt >= rows && ldqt % 16 == 0, DF_ERR_ALIGN, "%s: ldqt=%d must be >= rows and a multiple of 16", name, ldqt);
         DF_CHECK(aligned16(qt), DF_ERR_ALIGN, "%s: qt must be 16-byte aligned", name);
     }
-    if (colsum) {
+    const bool delayed = history != nullptr;
+    size_t amax_off = 0;
+    if (delayed) {
+        DF_CHECK(q || qt || empty, DF_ERR_INVALID, "%s: no code output", name);
+        DF_CHECK(hist_len >= 1 && hist_len <= kMaxHistory, DF_ERR_INVALID, "%s: history length %d not in [1, %d]",
+                 name, hist_len, kMaxHistory);
+        DF_CHECK(aligned4(history) && aligned4(next_scale), DF_ERR_ALIGN, "%s: history/scale misaligned", name);
+        const size_t need = delayed_ws_layout(rows, cols, q ? ldq : 0, qt ? ldqt : 0, colsum != nullptr, &amax_off);
+        DF_CHECK(ws && aligned16(ws), DF_ERR_WORKSPACE, "%s: needs a 16-byte aligned workspace", name);
+        DF_CHECK(ws_bytes >= need, DF_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu", name, ws_bytes, need);
+    } else if (colsum) {
         DF_CHECK(ws && aligned4(ws), DF_ERR_WORKSPACE, "%s: column sums need a workspace", name);
         DF_CHECK(ws_bytes >= df_quantize_2d_workspace_bytes(rows, cols), DF_ERR_WORKSPACE,
                  "%s: workspace %zu bytes < %zu", name, ws_bytes, df_quantize_2d_workspace_bytes(rows, cols));
     }
-    const int row_ext = qt ? (rows > ldqt ? rows : ldqt) : rows;
-    const int col_ext = q ? (cols > ldq ? cols : ldq) : cols;
-    if (row_ext == 0 || col_ext == 0) {
+    const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt);
+    hipStream_t st = as_stream(stream);
+    if (grid.x == 0 || grid.y == 0) {
         if (colsum && cols > 0) {
             const float zero = 0.0f;
-            return df_fill(colsum, cols, 4, &zero, stream);
+            if (int rc = df_fill(colsum, cols, 4, &zero, stream)) return rc;
+        }
+        if (delayed) {  // an empty pass measures absmax 0
+            amax_history_kernel<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, history, hist_len, next_scale);
+            return launch_status(name);
         }
         return DF_OK;
     }
-    const int gy = (row_ext + kT2 - 1) / kT2;
-    DF_CHECK(gy <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
-    dim3 grid((col_ext + kT2 - 1) / kT2, gy);
-    hipStream_t st = as_stream(stream);
+    DF_CHECK(grid.y <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
     float* part = colsum ? static_cast<float*>(ws) : nullptr;
+    uint32_t* amaxpart = delayed ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + amax_off) : nullptr;
     const int esz = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 2;
     const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
-#define DF_Q2D(T, F, CS) \
-    quantize_2d_kernel<T, F, CS, true><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, ldx, vec_ok, \
-                                                                  scale_dev, q, ldq, qt, ldqt, part)
+#define DF_Q2D(T, F, CS)                                                                                        \
+    do {                                                                                                        \
+        if (delayed)                                                                                            \
+            quantize_2d_kernel<T, F, CS, true, true><<<grid, kThreads, 0, st>>>(                                \
+                static_cast<const T*>(x), rows, cols, ldx, vec_ok, scale_dev, q, ldq, qt, ldqt, part, amaxpart); \
+        else                                                                                                    \
+            quantize_2d_kernel<T, F, CS, true><<<grid, kThreads, 0, st>>>(                                      \
+                static_cast<const T*>(x), rows, cols, ldx, vec_ok, scale_dev, q, ldq, qt, ldqt, part);          \
+    } while (0)
     if (!q && !qt) {  // column sums only
         if (in_dtype == DF_DTYPE_FLOAT32)
             quantize_2d_kernel<float, E4M3, true, false><<<grid, kThreads, 0, st>>>(
@@ -642,13 +737,43 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
     if (colsum)
         colsum_reduce_kernel<<<(cols + 63) / 64, kThreads, 0, st>>>(part, rows == 0 ? 0 : (rows + kT2 - 1) / kT2,
                                                                     cols, colsum);
+    if (delayed)
+        amax_history_kernel<<<1, kThreads, 0, st>>>(amaxpart, (int)(grid.x * grid.y), fmt, history, hist_len,
+                                                    next_scale);
     return launch_status(name);
+}
+
+extern "C" int df_amax_history_init(const float* amax_dev, int fmt, float* history, int len, float* scale_dev,
+                                    void* stream) {
+    clear_error();
+    DF_CHECK(history && scale_dev, DF_ERR_INVALID, "df_amax_history_init: NULL pointer");
+    DF_CHECK(len >= 1 && len <= kMaxHistory, DF_ERR_INVALID, "df_amax_history_init: length %d not in [1, %d]", len,
+             kMaxHistory);
+    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "df_amax_history_init: bad format %d", fmt);
+    DF_CHECK(aligned4(history) && aligned4(scale_dev) && (!amax_dev || aligned4(amax_dev)), DF_ERR_ALIGN,
+             "df_amax_history_init: misaligned pointer");
+    amax_history_init_kernel<<<1, kThreads, 0, as_stream(stream)>>>(amax_dev, fmt, history, len, scale_dev);
+    return launch_status("df_amax_history_init");
+}
+
+extern "C" size_t df_quantize_2d_delayed_workspace_bytes(int rows, int cols, int ldq, int ldqt, int colsum) {
+    if (rows < 0 || cols < 0) return 0;
+    return delayed_ws_layout(rows, cols, ldq, ldqt, colsum != 0, nullptr);
+}
+
+extern "C" int df_quantize_2d_delayed(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                                      const float* scale_dev, float* next_scale_dev, float* history, int len,
+                                      uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum, void* ws,
+                                      size_t ws_bytes, void* stream) {
+    DF_CHECK(history && scale_dev && next_scale_dev, DF_ERR_INVALID, "df_quantize_2d_delayed: NULL pointer");
+    return quantize_2d_impl("df_quantize_2d_delayed", in_dtype, x, rows, cols, ldx, fmt, scale_dev, q, ldq, qt,
+                            ldqt, colsum, ws, ws_bytes, stream, history, len, next_scale_dev);
 }
 
 extern "C" int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
                               const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
                               void* stream) {
-    DF_CHECK(q || qt, DF_ERR_INVALID, "df_quantize_2d: no output");
+    DF_CHECK(q || qt || rows == 0 || cols == 0, DF_ERR_INVALID, "df_quantize_2d: no output");
     return quantize_2d_impl("df_quantize_2d", in_dtype, x, rows, cols, ldx, fmt, scale_dev, q, ldq, qt, ldqt,
                             nullptr, nullptr, 0, stream);
 }

@@ -45,6 +45,18 @@ public:
     // comes back as the dequantized weights.
     void save_fp8(std::ostream& out) const;
 
+    // Delayed scaling (an addition: the reference has no quantizer).  With
+    // history_len in [1, 1024] the scales of X, W and dY come from amax
+    // histories of their last history_len passes instead of an absmax pass
+    // over the current data; each pass measures its own absmax on the way
+    // and pushes it.  The first pass of each operand seeds its history with
+    // its own absmax, so it equals the just-in-time pass.  Values beyond the
+    // inherited range saturate.  0 (the default) is the just-in-time path.
+    void set_delayed_scaling(int history_len);
+    int delayed_scaling() const { return history_len_; }
+    // device pointer to an operand's history (0: X, 1: W, 2: dY)
+    const float* amax_history(int operand);
+
 private:
     // device scratch reused across calls, grown on demand
     struct Scratch {
@@ -55,12 +67,28 @@ private:
     };
     void quantize_operand(const TT* x, int rows, int cols, int fmt, float* scale_dev, uint8_t* q, int ldq,
                           uint8_t* qt, int ldqt, float* colsum);
+    // delayed-scaling state of one operand: history, two scale slots used in
+    // turn (the codes' scale stays valid until the pass after next), one
+    // absmax slot for seeding
+    struct Delayed {
+        Scratch hist, scales;
+        int cur = 0;
+        bool seeded = false;
+    };
+    // quantizes with the operand's current scale, pushes this pass's absmax;
+    // returns the device pointer of the scale the codes were made with
+    const float* quantize_delayed(Delayed& d, const TT* x, int rows, int cols, int fmt, uint8_t* q, int ldq,
+                                  uint8_t* qt, int ldqt, float* colsum);
 
     int in_features_;
     int out_features_;
     int cached_n_ = -1;                        // tokens of the cached forward
     std::optional<tensor<fp8_e4m3>> xt_cache_;  // X^T codes [in, round16(N)] + scale
     Scratch absmax_ws_, colsum_ws_, gemm_ws_, codes_a_, codes_b_, codes_c_, scales_, colsum_;
+    int history_len_ = 0;
+    Delayed dx_, dw_, ddy_;
+    const float* sx_used_ = nullptr;  // delayed: scales of the cached forward's X and W codes
+    const float* sw_used_ = nullptr;
 };
 
 }  // namespace dnn

@@ -92,6 +92,57 @@ void FullyConnectedLayer<TT>::quantize_operand(const TT* x, int rows, int cols, 
 }
 
 template <typename TT>
+void FullyConnectedLayer<TT>::set_delayed_scaling(int history_len) {
+    if (history_len < 0 || history_len > 1024)
+        throw std::invalid_argument("FullyConnectedLayer::set_delayed_scaling: history length must be in [0, 1024]");
+    history_len_ = history_len;
+    for (Delayed* d : {&dx_, &dw_, &ddy_}) {
+        d->seeded = false;
+        d->cur = 0;
+        if (history_len > 0) {
+            d->hist.get((size_t)history_len * sizeof(float));
+            d->scales.get(3 * sizeof(float));
+        }
+    }
+    sx_used_ = sw_used_ = nullptr;
+}
+
+template <typename TT>
+const float* FullyConnectedLayer<TT>::amax_history(int operand) {
+    if (history_len_ == 0 || operand < 0 || operand > 2)
+        throw std::invalid_argument("FullyConnectedLayer::amax_history: no such history");
+    Delayed* d = operand == 0 ? &dx_ : operand == 1 ? &dw_ : &ddy_;
+    return reinterpret_cast<const float*>(d->hist.p);
+}
+
+template <typename TT>
+const float* FullyConnectedLayer<TT>::quantize_delayed(Delayed& d, const TT* x, int rows, int cols, int fmt,
+                                                       uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum) {
+    constexpr int dt = dtype_traits<TT>::value;
+    float* hist = reinterpret_cast<float*>(d.hist.get((size_t)history_len_ * sizeof(float)));
+    float* sc = reinterpret_cast<float*>(d.scales.get(3 * sizeof(float)));
+    float* used = sc + d.cur;
+    float* next = sc + (d.cur ^ 1);
+    if (!d.seeded) {
+        // the first pass seeds the history with its own absmax
+        const size_t ab = df_absmax_workspace_bytes();
+        uint8_t* aws = absmax_ws_.get(ab);
+        const int64_t n = (int64_t)rows * cols;
+        if constexpr (std::is_same_v<TT, float>)
+            CHECK_DF_EX(df_absmax_f32(x, n, sc + 2, aws, ab, st()));
+        else
+            CHECK_DF_EX(df_absmax_bf16(reinterpret_cast<const uint16_t*>(x), n, sc + 2, aws, ab, st()));
+        CHECK_DF_EX(df_amax_history_init(sc + 2, fmt, hist, history_len_, used, st()));
+        d.seeded = true;
+    }
+    const size_t wb = df_quantize_2d_delayed_workspace_bytes(rows, cols, q ? ldq : 0, qt ? ldqt : 0, colsum ? 1 : 0);
+    CHECK_DF_EX(df_quantize_2d_delayed(dt, x, rows, cols, cols, fmt, used, next, hist, history_len_, q, ldq, qt, ldqt,
+                                       colsum, colsum_ws_.get(wb), wb, st()));
+    d.cur ^= 1;
+    return used;
+}
+
+template <typename TT>
 tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input) {
     const auto& sh = input.shape();
     if (sh.size() != 2 || sh[1] != in_features_)
@@ -112,12 +163,23 @@ tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input) {
         xt = reinterpret_cast<uint8_t*>(xt_cache_->data());
         sx = xt_cache_->scale_data();
     }
-    quantize_operand(input.data(), N, in_features_, DF_FMT_E4M3, sx, xq, Kp, xt, Np, nullptr);
     uint8_t* wq = codes_b_.get((size_t)out_features_ * Kp);
-    quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, wq, Kp, nullptr, 0,
-                     nullptr);
+    const float* sw = sc + 1;
+    if (history_len_ > 0) {
+        sx = const_cast<float*>(quantize_delayed(dx_, input.data(), N, in_features_, DF_FMT_E4M3, xq, Kp, xt, Np,
+                                                 nullptr));
+        sw = quantize_delayed(dw_, this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, wq, Kp, nullptr,
+                              0, nullptr);
+        sx_used_ = sx;
+        sw_used_ = sw;
+    } else {
+        quantize_operand(input.data(), N, in_features_, DF_FMT_E4M3, sx, xq, Kp, xt, Np, nullptr);
+        quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, wq, Kp, nullptr, 0,
+                         nullptr);
+        sx_used_ = sw_used_ = nullptr;
+    }
     const size_t gb = df_fp8_gemm_workspace_bytes(N, out_features_, in_features_);
-    CHECK_DF_EX(df_fp8_gemm_fwd(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sc + 1, dt, this->bias_.data(), dt,
+    CHECK_DF_EX(df_fp8_gemm_fwd(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sw, dt, this->bias_.data(), dt,
                                 output.data(), out_features_, gemm_ws_.get(gb), gb, st()));
     cached_n_ = this->training_enabled_ ? N : -1;
     return output;
@@ -141,20 +203,33 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
     uint8_t* dyq = codes_a_.get((size_t)N * Op);
     uint8_t* dyt = codes_c_.get((size_t)out_features_ * Np);
     float* db = reinterpret_cast<float*>(colsum_.get((size_t)out_features_ * sizeof(float)));
-    quantize_operand(grad_output.data(), N, out_features_, DF_FMT_E5M2, sc + 2, dyq, Op, dyt, Np, db);
-    // the current weights (reference: backward reads weights_), transposed
     uint8_t* wt = codes_b_.get((size_t)in_features_ * Op);
-    quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, nullptr, 0, wt, Op,
-                     nullptr);
+    const float* sdy = sc + 2;
+    const float* sw = sc + 1;
+    const float* sx = xt_cache_->scale_data();
+    if (history_len_ > 0 && sx_used_) {
+        sdy = quantize_delayed(ddy_, grad_output.data(), N, out_features_, DF_FMT_E5M2, dyq, Op, dyt, Np, db);
+        // W has not changed since the forward: its transposed codes at the
+        // forward's scale, no absmax pass
+        CHECK_DF_EX(df_quantize_2d(dt, this->weights_.data(), out_features_, in_features_, in_features_, DF_FMT_E4M3,
+                                   sw_used_, nullptr, 0, wt, Op, st()));
+        sw = sw_used_;
+        sx = sx_used_;
+    } else {
+        quantize_operand(grad_output.data(), N, out_features_, DF_FMT_E5M2, sc + 2, dyq, Op, dyt, Np, db);
+        // the current weights (reference: backward reads weights_), transposed
+        quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, nullptr, 0, wt, Op,
+                         nullptr);
+    }
     tensor<TT> grad_input({N, in_features_});
     const size_t gb = std::max(df_fp8_gemm_workspace_bytes(N, in_features_, out_features_),
                                df_fp8_gemm_workspace_bytes(out_features_, in_features_, N));
     uint8_t* gws = gemm_ws_.get(gb);
-    CHECK_DF_EX(df_fp8_gemm_bwd_dx(dyq, Op, wt, Op, N, out_features_, in_features_, sc + 2, sc + 1, dt,
-                                   grad_input.data(), in_features_, gws, gb, st()));
+    CHECK_DF_EX(df_fp8_gemm_bwd_dx(dyq, Op, wt, Op, N, out_features_, in_features_, sdy, sw, dt, grad_input.data(),
+                                   in_features_, gws, gb, st()));
     CHECK_DF_EX(df_fp8_gemm_bwd_dw(dyt, Np, reinterpret_cast<const uint8_t*>(xt_cache_->data()), Np, N,
-                                   out_features_, in_features_, sc + 2, xt_cache_->scale_data(), dt,
-                                   this->grad_weights_.data(), in_features_, gws, gb, st()));
+                                   out_features_, in_features_, sdy, sx, dt, this->grad_weights_.data(), in_features_,
+                                   gws, gb, st()));
     CHECK_DF_EX(df_convert(DF_DTYPE_FLOAT32, db, dt, this->grad_bias_.data(), out_features_, st()));
     return grad_input;
 }

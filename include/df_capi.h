@@ -136,6 +136,37 @@ int df_quantize_2d_colsum(int in_dtype, const void* x, int rows, int cols, int l
 int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
               float* out, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- delayed scaling (new: the reference has no quantizer) ----
+ * The scale of a tensor comes from an amax history of earlier passes instead
+ * of an absmax pass over the current data.  history[0..len) (device, fp32,
+ * len <= 1024, history[0] newest) and scale_dev belong to one tensor role
+ * (e.g. one layer's X, W or dY).
+ *  df_amax_history_init    : history[i] = *amax_dev (0 when amax_dev is
+ *                            NULL or *amax_dev is not a positive finite
+ *                            value), *scale_dev = scale rule D1/D2 of it.
+ *  df_quantize_2d_delayed  : df_quantize_2d / df_quantize_2d_colsum at
+ *                            the scale *scale_dev (codes saturate beyond
+ *                            FMAX * scale, D3); the same pass measures the
+ *                            input's absmax (finite values), pushes it to
+ *                            history[0] (older entries move up one, the
+ *                            oldest drops out) and then writes the scale of
+ *                            the maximum over the new history to
+ *                            *next_scale_dev, for the next call.
+ *                            next_scale_dev may equal scale_dev when the
+ *                            caller no longer needs the scale of these codes
+ *                            (the GEMMs that read it are enqueued before the
+ *                            next call otherwise).  colsum may be NULL.  ws
+ *                            holds df_quantize_2d_delayed_workspace_bytes(
+ *                            rows, cols, ldq or 0, ldqt or 0,
+ *                            colsum != NULL) bytes, 16-byte aligned. */
+int df_amax_history_init(const float* amax_dev, int fmt, float* history, int len, float* scale_dev,
+                         void* stream);
+size_t df_quantize_2d_delayed_workspace_bytes(int rows, int cols, int ldq, int ldqt, int colsum);
+int df_quantize_2d_delayed(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                           const float* scale_dev, float* next_scale_dev, float* history, int len,
+                           uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum, void* ws,
+                           size_t ws_bytes, void* stream);
+
 /* ---- fp8 GEMM, "NT": C[m,n] = (sum_k A[m,k] * B[n,k]) * sa * sb + bias[n]
  *   A [M, lda] fp8 (fmt_a), B [N, ldb] fp8 (fmt_b), both row-major with the
  *   reduction dimension contiguous; lda, ldb multiples of 16 and >= K;

@@ -433,3 +433,18 @@ void dfo_adam_step(float* p, const float* grad, float* m, float* v, int64_t n,
         p[i] = p[i] - lr * m_hat / (sqrtf(v_hat) + eps);
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* Delayed scaling: amax history                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Push `amax` as the newest entry (history[0]); the others move up one and
+ * the oldest drops out.  Returns the scale (D1/D2) of the new history's
+ * maximum: the scale the next pass uses. */
+float dfo_history_push(float* history, int len, float amax, int fmt) {
+    for (int i = len - 1; i > 0; --i) history[i] = history[i - 1];
+    history[0] = amax;
+    float m = 0.0f;
+    for (int i = 0; i < len; ++i) m = history[i] > m ? history[i] : m;
+    return dfo_scale(m, fmt);
+}

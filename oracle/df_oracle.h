@@ -118,6 +118,10 @@ void dfo_adam_step(float* p, const float* grad, float* m, float* v, int64_t n,
                    float lr, float beta1, float beta2, float eps, float wd, int t,
                    float clip_factor);
 
+/* ---- delayed scaling: push amax into history[0..len) (newest first) and
+ * return the scale of the new maximum, the one the next pass uses ---- */
+float dfo_history_push(float* history, int len, float amax, int fmt);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,6 +46,7 @@ _SIGS = {
     "dfo_clip_scale": (_i, [_vp, _i64, _f, _f]),
     "dfo_bias_correction": (_f, [_f, _i]),
     "dfo_adam_step": (None, [_vp, _vp, _vp, _vp, _i64, _f, _f, _f, _f, _f, _i, _f]),
+    "dfo_history_push": (_f, [_vp, _i, _f, _i]),
 }
 
 _lib = None
@@ -234,3 +235,9 @@ def adam_step(p, g, m, v, t, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, wd=0.0, 
     for a in (p, g, m, v):
         assert a.dtype == np.float32 and a.flags.c_contiguous and a.size == p.size
     lib().dfo_adam_step(_p(p), _p(g), _p(m), _p(v), p.size, lr, beta1, beta2, eps, wd, t, clip_factor)
+
+
+def history_push(history: np.ndarray, amax: float, fmt: int) -> float:
+    """Delayed scaling: newest amax first; returns the next pass's scale."""
+    assert history.dtype == np.float32 and history.flags.c_contiguous
+    return lib().dfo_history_push(_p(history), history.size, amax, fmt)

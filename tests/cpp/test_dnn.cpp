@@ -794,6 +794,71 @@ TEST_F(FullyConnectedLayerTest, SaveFp8LoadsDequantizedWeights) {
     EXPECT_LE(d, 0.07f * m);
 }
 
+// ---- delayed scaling in the Linear layer ----
+// values the GEMM sees when x is quantized at a given scale s (saturating)
+std::vector<float> fp8_values_at(const std::vector<float>& x, float s, int fmt) {
+    const int64_t n = (int64_t)x.size();
+    std::vector<uint8_t> q(n);
+    std::vector<float> d(n);
+    dfo_quantize_f32(x.data(), n, s, fmt, q.data());
+    dfo_dequantize_f32(q.data(), n, s, fmt, d.data());
+    return d;
+}
+
+// The first step of a delayed-scaling layer seeds every history with the
+// operand's own absmax: bit-identical to the just-in-time layer.
+TEST_F(FullyConnectedLayerTest, DelayedScalingFirstStepEqualsJustInTime) {
+    const int N = 70, in_f = 96, out_f = 40;
+    FullyConnectedLayer<float> a(in_f, out_f, true), b(in_f, out_f, true);
+    const auto w = uniform((size_t)out_f * in_f, -0.2f, 0.2f, 81);
+    for (auto* l : {&a, &b}) l->parameters()[0]->upload(w.data());
+    b.set_delayed_scaling(4);
+    EXPECT_EQ(b.delayed_scaling(), 4);
+    tensor<float> x({N, in_f}), gy({N, out_f});
+    const auto xh = uniform((size_t)N * in_f, -1.0f, 1.0f, 82), gh = uniform((size_t)N * out_f, -0.1f, 0.1f, 83);
+    x.upload(xh.data());
+    gy.upload(gh.data());
+    EXPECT_TRUE(download(a.forward(x)) == download(b.forward(x)));
+    EXPECT_TRUE(download(a.backward(gy)) == download(b.backward(gy)));
+    EXPECT_TRUE(download(*a.grad_weights()) == download(*b.grad_weights()));
+    EXPECT_TRUE(download(*a.grad_bias()) == download(*b.grad_bias()));
+}
+
+// Later steps quantize at the scale of the history: an input that grew 4x
+// saturates at 448 * (the earlier absmax / 448), and the history records
+// both steps.
+TEST_F(FullyConnectedLayerTest, DelayedScalingUsesHistoryScale) {
+    const int N = 33, in_f = 64, out_f = 24;
+    FullyConnectedLayer<float> layer(in_f, out_f, true);
+    const auto w = uniform((size_t)out_f * in_f, -0.3f, 0.3f, 91);
+    const auto bias = std::vector<float>(out_f, 0.0f);
+    layer.parameters()[0]->upload(w.data());
+    layer.set_delayed_scaling(2);
+    const auto x1 = uniform((size_t)N * in_f, -1.0f, 1.0f, 92);
+    auto x2 = uniform((size_t)N * in_f, -1.0f, 1.0f, 93);
+    for (auto& v : x2) v *= 4.0f;
+    tensor<float> t1({N, in_f}), t2({N, in_f});
+    t1.upload(x1.data());
+    t2.upload(x2.data());
+    layer.forward(t1);
+    const auto y2 = download(layer.forward(t2));
+    // oracle: X at the scale of step 1's absmax, W at its own (unchanged) scale
+    const float sx = dfo_scale(dfo_absmax_f32(x1.data(), (int64_t)x1.size()), DFO_E4M3);
+    const auto xd = fp8_values_at(x2, sx, DFO_E4M3), wd = fp8_values(w, DFO_E4M3);
+    std::vector<float> ey((size_t)N * out_f);
+    dfo_fc_forward(xd.data(), wd.data(), bias.data(), ey.data(), N, in_f, out_f, 4);
+    EXPECT_LE(rel_err(y2, ey), 1e-4);
+    // the just-in-time result differs: the saturation is real
+    const auto xj = fp8_values(x2, DFO_E4M3);
+    std::vector<float> ej((size_t)N * out_f);
+    dfo_fc_forward(xj.data(), wd.data(), bias.data(), ej.data(), N, in_f, out_f, 4);
+    EXPECT_GT(rel_err(y2, ej), 1e-2);
+    std::vector<float> h(2);
+    CHECK_HIP_EX(hipMemcpy(h.data(), layer.amax_history(0), 2 * sizeof(float), hipMemcpyDeviceToHost));
+    EXPECT_EQ(h[0], dfo_absmax_f32(x2.data(), (int64_t)x2.size()));
+    EXPECT_EQ(h[1], dfo_absmax_f32(x1.data(), (int64_t)x1.size()));
+}
+
 // ---- AdamOptimizer: the reference's cases (adam_optimizer_test.cu:21-214),
 // plus exact agreement with the oracle's step ----
 TEST_F(AdamOptimizerTest, BasicUpdate) {

@@ -186,3 +186,20 @@ def test_clip_scale_rules():
     assert not orc.clip_scale(h, 4.0, 5.0)
     assert not orc.clip_scale(h, float("nan"), 1.0)  # a NaN norm compares false
     assert np.array_equal(h, np.array([3.0, 4.0], np.float32))
+
+
+# ---- delayed scaling: amax history (oracle dfo_history_push) ----
+def test_history_push_closed_forms():
+    """Newest first, oldest drops out; the next scale is FMAX-normalised
+    max(history) under the D1/D2 rule (zero history -> scale 1)."""
+    h = np.zeros(2, np.float32)
+    assert orc.history_push(h, 0.0, 0) == 1.0
+    assert orc.history_push(h, 1.0, 0) == np.float32(1.0) / np.float32(448.0)
+    assert orc.history_push(h, 5.0, 0) == np.float32(5.0) / np.float32(448.0)
+    assert h.tolist() == [5.0, 1.0]
+    assert orc.history_push(h, 2.0, 0) == np.float32(5.0) / np.float32(448.0)  # 5 still inside
+    assert h.tolist() == [2.0, 5.0]
+    assert orc.history_push(h, 3.0, 1) == np.float32(3.0) / np.float32(57344.0)  # 5 dropped out
+    one = np.zeros(1, np.float32)
+    for a in (7.0, 0.5, 300.0):  # length 1 = most recent amax
+        assert orc.history_push(one, a, 0) == np.float32(a) / np.float32(448.0)
