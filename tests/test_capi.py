@@ -74,7 +74,7 @@ def test_argument_errors():
     assert status("df_approx_equal_mask", int(DType.FP8E4M3), FAKE, FAKE, FAKE, 4, 0.1, None) == -2
     # clip / Adam lists
     P = ctypes.c_void_p
-    sizes = (ctypes.c_int64 * 3)(8192, 8193, 0)
+    sizes = (ctypes.c_int64 * 3)(32768, 32769, 0)  # 32768-element partial blocks
     assert df.lib().df_grad_norm_workspace_bytes(3, sizes) == 3 * 8
     assert df.lib().df_grad_norm_workspace_bytes(0, None) == 8
     ptrs = (P * 3)(FAKE, FAKE + 16, None)  # the empty entry may be NULL
