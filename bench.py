@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--no-conversion", action="store_true")
     p.add_argument("--no-streaming", action="store_true", help="skip the config 5 layer-streaming leg")
     p.add_argument("--no-optimizer", action="store_true", help="skip the clip + Adam leg")
+    p.add_argument("--no-delayed", action="store_true", help="skip the delayed-scaling step leg")
+    p.add_argument("--history", type=int, default=16, help="amax history length of the delayed-scaling leg")
     p.add_argument("--stream-layers", type=int, default=48)
     p.add_argument("--stream-slots", type=int, default=4)
     p.add_argument("--cpu-tokens", type=int, default=3072, help="token slice for the CPU baseline")
@@ -279,6 +281,8 @@ def main():
         else:
             d["gbs"] = round(qbytes[k] / (t / args.steps * 1e-3) / 1e9, 1)
         kernels[k] = d
+    delayed = None if args.no_delayed else delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes,
+                                                                    ms_per_step, step_flops)
     qt_ms = sum(per[k][0] for k in qbytes) / args.steps
     q_gbs = sum(qbytes.values()) / (qt_ms * 1e-3) / 1e9
     gemm_ms = sum(per[k][0] for k in gemm_flops) / args.steps
@@ -302,6 +306,8 @@ def main():
         "roofline": roof,
         "kernels": kernels,
     }
+    if delayed is not None:
+        out["delayed_scaling"] = delayed
     if not args.no_conversion:
         out["conversion"] = conversion_bench(torch, df, synth, dev, cur())
     if not args.no_optimizer:
@@ -476,6 +482,87 @@ def conversion_bench(torch, df, synth, dev, stream, reps=10):
     del x32, x16, q, o32, o16
     torch.cuda.empty_cache()
     return res
+
+
+def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit_ms, step_flops):
+    """The config-4 step with delayed scaling: every operand (X, W, dY of each
+    Linear) is quantized at the scale of its amax history and measures its
+    own absmax in the same pass (df_quantize_2d_delayed), so the separate
+    absmax passes disappear.  Histories are seeded from the operands' own
+    absmax first.  Two steps are captured per graph (the two scale slots of
+    each operand alternate), replayed args.steps // 2 + 1 times."""
+    from deepfuse_amd import DType, Fmt
+    BF, F32 = int(DType.BFLOAT16), int(DType.FLOAT32)
+    E4, E5 = int(Fmt.E4M3), int(Fmt.E5M2)
+    H = args.history
+    dws_bytes = 0
+    roles = []
+    for l in layers:
+        K, N = l["K"], l["N"]
+        r = {}
+        for name, x, rows, cols, fmt, q, qt, cs in (("x", l["X"], M, K, E4, l["Xq"], l["Xt"], None),
+                                                    ("w", l["W"], N, K, E4, l["Wq"], l["Wt"], None),
+                                                    ("dy", l["dY"], M, N, E5, l["dYq"], l["dYt"], l["db"])):
+            st = {"x": x, "rows": rows, "cols": cols, "fmt": fmt, "q": q, "qt": qt, "cs": cs,
+                  "hist": torch.empty(H, dtype=torch.float32, device=x.device),
+                  "sc": torch.empty(3, dtype=torch.float32, device=x.device)}
+            dws_bytes = max(dws_bytes, df.lib().df_quantize_2d_delayed_workspace_bytes(
+                rows, cols, q.stride(0), qt.stride(0), int(cs is not None)))
+            df.call("df_absmax_bf16", x.data_ptr(), x.numel(), st["sc"].data_ptr() + 8, ws.data_ptr(), ws.numel(),
+                    cur())
+            df.call("df_amax_history_init", st["sc"].data_ptr() + 8, fmt, st["hist"].data_ptr(), H,
+                    st["sc"].data_ptr(), cur())
+            r[name] = st
+        roles.append(r)
+    dws = torch.empty(dws_bytes, dtype=torch.uint8, device=layers[0]["X"].device)
+
+    def quant(st, parity):
+        used = st["sc"].data_ptr() + 4 * parity
+        nxt = st["sc"].data_ptr() + 4 * (parity ^ 1)
+        cs = st["cs"]
+        df.call("df_quantize_2d_delayed", BF, st["x"].data_ptr(), st["rows"], st["cols"], st["cols"], st["fmt"],
+                used, nxt, st["hist"].data_ptr(), H, st["q"].data_ptr(), st["q"].stride(0), st["qt"].data_ptr(),
+                st["qt"].stride(0), None if cs is None else cs.data_ptr(), dws.data_ptr(), dws_bytes, cur())
+        return used
+
+    def step(parity):
+        for l, r in zip(layers, roles):
+            K, N = l["K"], l["N"]
+            sx = quant(r["x"], parity)
+            sw = quant(r["w"], parity)
+            df.call("df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["Xq"].stride(0), l["Wq"].data_ptr(),
+                    l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF, l["Y"].data_ptr(), N,
+                    gws.data_ptr(), gws_bytes, cur())
+            sdy = quant(r["dy"], parity)
+            df.call("df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0), l["Wt"].data_ptr(),
+                    l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K, gws.data_ptr(), gws_bytes,
+                    cur())
+            df.call("df_fp8_gemm_bwd_dw", l["dYt"].data_ptr(), l["dYt"].stride(0), l["Xt"].data_ptr(),
+                    l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K, gws.data_ptr(), gws_bytes,
+                    cur())
+
+    for _ in range(max(1, args.warmup)):
+        step(0)
+        step(1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(0)
+        step(1)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 2)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (2 * reps)
+    del graph
+    return {"history": H, "steps": 2 * reps, "ms_per_step": round(ms, 4),
+            "tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
+            "speedup_vs_just_in_time": round(jit_ms / ms, 4)}
 
 
 def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
