@@ -106,6 +106,13 @@ _SIGS = {
     "df_quantize_2d_delayed_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "df_quantize_2d_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp,
                                         _c_int, _vp, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_layernorm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
+    "df_layernorm": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int, _vp, _c_sz, _vp]),
+    "df_layernorm_quantize": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int, _c_int,
+                                       _vp, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+    "df_layernorm_quantize_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int,
+                                               _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz,
+                                               _vp]),
     "df_grad_norm_workspace_bytes": (_c_sz, [_c_int, _vp]),
     "df_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _vp, _vp, _c_sz, _vp]),
     "df_clip_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _c_f, _vp, _vp, _c_sz, _vp]),
@@ -403,3 +410,40 @@ class DelayedScale:
              _ptr(self.scale), _ptr(self.scale), _ptr(self.history), self.history.numel(), _ptr(q), ldq, _ptr(qt),
              ldqt, _ptr(cs), _ptr(ws), ws.numel(), _stream())
         return (q, qt, cs) if colsum else (q, qt)
+
+
+# ----------------------------------------------------------------------------
+# LayerNorm with the fused quantize (dnn/layers/layer_norm_layer.cu:26-63)
+# ----------------------------------------------------------------------------
+def layernorm(x, gamma=None, beta=None, eps=1e-5, fmt: Fmt | None = None, want_y=True, want_q=True,
+              want_qt=False, delayed: "DelayedScale | None" = None):
+    """LayerNorm over the last dim of a 2-D fp32/bf16 tensor.  fmt=None: y
+    only.  Otherwise returns (y or None, q, qt, scale) with the codes of y at
+    the just-in-time scale, or at ``delayed``'s history scale."""
+    torch = _torch()
+    rows, cols = x.shape
+    dt = int(_in_dtype(x))
+    y = torch.empty_like(x) if (want_y or fmt is None) else None
+    ldy = cols if y is not None else 0
+    if fmt is None:
+        nbytes = lib().df_layernorm_workspace_bytes(rows, cols, 0, 0)
+        ws = _scratch(x.device, nbytes, "layernorm")
+        call("df_layernorm", dt, _ptr(x), rows, cols, x.stride(0), _ptr(gamma), _ptr(beta), float(eps), _ptr(y),
+             ldy, _ptr(ws), ws.numel(), _stream())
+        return y
+    q = torch.empty((rows, round16(cols)), dtype=torch.uint8, device=x.device) if want_q else None
+    qt = torch.empty((cols, round16(rows)), dtype=torch.uint8, device=x.device) if want_qt else None
+    ldq = q.shape[1] if q is not None else 0
+    ldqt = qt.shape[1] if qt is not None else 0
+    nbytes = lib().df_layernorm_workspace_bytes(rows, cols, ldq, ldqt)
+    ws = _scratch(x.device, nbytes, "layernorm")
+    if delayed is None:
+        scale = torch.empty(1, dtype=torch.float32, device=x.device)
+        call("df_layernorm_quantize", dt, _ptr(x), rows, cols, x.stride(0), _ptr(gamma), _ptr(beta), float(eps),
+             _ptr(y), ldy, int(fmt), _ptr(scale), _ptr(q), ldq, _ptr(qt), ldqt, _ptr(ws), ws.numel(), _stream())
+    else:
+        scale = delayed.scale.clone()
+        call("df_layernorm_quantize_delayed", dt, _ptr(x), rows, cols, x.stride(0), _ptr(gamma), _ptr(beta),
+             float(eps), _ptr(y), ldy, int(fmt), _ptr(scale), _ptr(delayed.scale), _ptr(delayed.history),
+             delayed.history.numel(), _ptr(q), ldq, _ptr(qt), ldqt, _ptr(ws), ws.numel(), _stream())
+    return y, q, qt, scale

@@ -305,17 +305,69 @@ template <> struct Ld<uint16_t> {
     static __device__ __forceinline__ float one(const uint16_t* p) { return bf16_to_f32(*p); }
 };
 
+// ---------------------------------------------------------------- LayerNorm --
+// Row statistics and the per-element map of the reference's
+// layer_norm_forward_kernel (dnn/layers/layer_norm_layer.cu:26-63):
+//   y = (x - mean) * rstd [* gamma + beta],  mean = sum/C, var = sum((x-mean)^2)/C,
+//   rstd = 1 / sqrt(var + eps)
+// then rounded to the tensor's element type (the reference casts to T).
+// The statistics kernel and the tile kernel evaluate y with the same
+// operations on the same stored (mean, rstd), so the absmax the first
+// measures is the absmax of the values the second quantizes.
+struct LnArgs {
+    const float2* stat = nullptr;  // (mean, rstd) per row
+    const void* gamma = nullptr;   // [cols] in the input type, NULL: no affine map
+    const void* beta = nullptr;
+    void* y = nullptr;             // optional output [rows, ldy] in the input type
+    int ldy = 0;
+    bool y_vec = false;            // y and ldy allow 16-byte row stores
+};
+
+template <typename InT> __device__ __forceinline__ float round_to(float v);
+template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to<uint16_t>(float v) { return bf16_to_f32(f32_to_bf16_rne(v)); }
+
+template <typename InT> __device__ __forceinline__ void store_one(InT* p, float v);
+template <> __device__ __forceinline__ void store_one<float>(float* p, float v) { *p = v; }
+template <> __device__ __forceinline__ void store_one<uint16_t>(uint16_t* p, float v) {
+    *p = (uint16_t)f32_to_bf16_rne(v);
+}
+// 16 bytes of values already rounded to the element type
+template <typename InT> __device__ __forceinline__ void store_vec(InT* p, const float* v);
+template <> __device__ __forceinline__ void store_vec<float>(float* p, const float* v) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+}
+template <> __device__ __forceinline__ void store_vec<uint16_t>(uint16_t* p, const float* v) {
+    u32x4 w;
+    w.x = (__float_as_uint(v[0]) >> 16) | (__float_as_uint(v[1]) & 0xFFFF0000u);
+    w.y = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[3]) & 0xFFFF0000u);
+    w.z = (__float_as_uint(v[4]) >> 16) | (__float_as_uint(v[5]) & 0xFFFF0000u);
+    w.w = (__float_as_uint(v[6]) >> 16) | (__float_as_uint(v[7]) & 0xFFFF0000u);
+    *reinterpret_cast<u32x4*>(p) = w;
+}
+
+template <typename InT>
+__device__ __forceinline__ float ln_apply(float x, float mean, float rstd, bool affine, float g, float b) {
+    float n = (x - mean) * rstd;
+    if (affine) n = __builtin_fmaf(n, g, b);
+    return round_to<InT>(n);
+}
+
 // With AMAX the block also folds |x| over finite values of its tile into one
 // partial maximum (binary32 bit pattern), amaxpart[tile index], for the
-// delayed-scaling history.
-template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false>
+// delayed-scaling history.  With LN the tile holds LayerNorm outputs: each
+// loaded x becomes ln_apply(x, row stats, column gamma/beta), written to
+// ln.y when given, and those values are what the codes, column sums and
+// absmax see.
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false, bool LN = false>
 __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
                                                                 int cols, int ldx, bool vec_ok,
                                                                 const float* __restrict__ scale,
                                                                 uint8_t* __restrict__ q, int ldq,
                                                                 uint8_t* __restrict__ qt, int ldqt,
                                                                 float* __restrict__ colpart,
-                                                                uint32_t* __restrict__ amaxpart = nullptr) {
+                                                                uint32_t* __restrict__ amaxpart = nullptr,
+                                                                LnArgs ln = LnArgs()) {
     constexpr int E = Ld<InT>::E;      // elements per 16-byte load
     constexpr int TPR = kT2 / E;       // threads per tile row
     constexpr int RG = kThreads / TPR; // row groups
@@ -334,6 +386,16 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
     uint32_t am = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) cs[e] = 0.0f;
+    float lg[LN ? E : 1], lb[LN ? E : 1];
+    const bool affine = LN && ln.gamma != nullptr;
+    if (LN) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const bool in = c + e < cols;
+            lg[e] = affine && in ? Ld<InT>::one(static_cast<const InT*>(ln.gamma) + c + e) : 0.0f;
+            lb[e] = affine && in ? Ld<InT>::one(static_cast<const InT*>(ln.beta) + c + e) : 0.0f;
+        }
+    }
 #pragma unroll
     for (int rr = 0; rr < RPT; ++rr) {
         const int r = r0 + rg * RPT + rr;
@@ -344,6 +406,22 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
 #pragma unroll
             for (int e = 0; e < E; ++e)
                 v[e] = (r < rows && c + e < cols) ? Ld<InT>::one(x + (int64_t)r * ldx + c + e) : 0.0f;
+        }
+        if (LN && r < rows) {
+            const float2 st = ln.stat[r];
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                v[e] = c + e < cols ? ln_apply<InT>(v[e], st.x, st.y, affine, lg[e], lb[e]) : 0.0f;
+            if (ln.y) {
+                InT* yr = static_cast<InT*>(ln.y) + (int64_t)r * ln.ldy + c;
+                if (full && ln.y_vec) {
+                    store_vec<InT>(yr, v);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; ++e)
+                        if (c + e < cols) store_one<InT>(yr + e, v[e]);
+                }
+            }
         }
         if (COLSUM) {
 #pragma unroll
@@ -445,6 +523,55 @@ __global__ __launch_bounds__(kThreads) void amax_history_kernel(const uint32_t* 
     if (threadIdx.x == 0) history[0] = __uint_as_float(cur);
     hm = block_max_u32(hm);
     if (threadIdx.x == 0) scale_out[0] = scale_from_absmax(__uint_as_float(hm), fmt);
+}
+
+// LayerNorm row statistics: one wave per row (4 rows per block).  Each lane
+// sums its elements i = lane, lane + 64, ... in order, then a butterfly over
+// the wave (every lane ends with the same bits: IEEE addition commutes).
+// Two passes as in the reference (mean, then squared deviations; the second
+// and third reads of the row hit the caches).  With ABSMAX the block also
+// folds |y| of its rows into amaxpart[block] (the just-in-time scale of the
+// fused quantize).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename InT, bool ABSMAX>
+__global__ __launch_bounds__(kThreads) void ln_stats_kernel(const InT* __restrict__ x, int rows, int cols, int ldx,
+                                                            float eps, const InT* __restrict__ gamma,
+                                                            const InT* __restrict__ beta, float2* __restrict__ stat,
+                                                            uint32_t* __restrict__ amaxpart) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    uint32_t am = 0;
+    if (r < rows) {
+        const InT* xr = x + (int64_t)r * ldx;
+        float s = 0.0f;
+        for (int i = lane; i < cols; i += 64) s += Ld<InT>::one(xr + i);
+        const float mean = wave_sum(s) / (float)cols;
+        float sq = 0.0f;
+        for (int i = lane; i < cols; i += 64) {
+            const float d = Ld<InT>::one(xr + i) - mean;
+            sq = __builtin_fmaf(d, d, sq);
+        }
+        const float var = wave_sum(sq) / (float)cols;
+        const float rstd = 1.0f / __builtin_sqrtf(var + eps);
+        if (lane == 0) stat[r] = make_float2(mean, rstd);
+        if (ABSMAX) {
+            const bool affine = gamma != nullptr;
+            for (int i = lane; i < cols; i += 64) {
+                const float g = affine ? Ld<InT>::one(gamma + i) : 0.0f;
+                const float b = affine ? Ld<InT>::one(beta + i) : 0.0f;
+                am = fold_f32(am, __float_as_uint(ln_apply<InT>(Ld<InT>::one(xr + i), mean, rstd, affine, g, b)));
+            }
+        }
+    }
+    if (ABSMAX) {
+        am = block_max_u32(am);
+        if (threadIdx.x == 0) amaxpart[blockIdx.x] = am;
+    }
 }
 
 // history[0..len) = amax (or 0 when amax is NULL), scale from it.
@@ -792,4 +919,135 @@ extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ld
     DF_CHECK(out, DF_ERR_INVALID, "df_colsum: out is NULL");
     return quantize_2d_impl("df_colsum", in_dtype, x, rows, cols, ldx, E4M3, nullptr, nullptr, 0, nullptr, 0, out,
                             ws, ws_bytes, stream);
+}
+
+// ---------------------------------------------------------------- LayerNorm --
+// Workspace: (mean, rstd) per row, then the absmax partials of the
+// statistics pass or of the tile pass (delayed), 16-byte aligned.
+static size_t ln_ws_layout(int rows, int cols, int ldq, int ldqt, size_t* part_off) {
+    const size_t st = ((size_t)rows * sizeof(float2) + 15) & ~(size_t)15;
+    const size_t stat_parts = (size_t)((rows + 3) / 4);
+    const dim3 g = q2d_grid(rows, cols, (const uint8_t*)1, ldq, ldqt > 0 ? (const uint8_t*)1 : nullptr, ldqt);
+    const size_t tile_parts = (size_t)g.x * g.y;
+    if (part_off) *part_off = st;
+    return st + (stat_parts > tile_parts ? stat_parts : tile_parts) * sizeof(uint32_t) + 16;
+}
+
+extern "C" size_t df_layernorm_workspace_bytes(int rows, int cols, int ldq, int ldqt) {
+    if (rows < 0 || cols < 0) return 0;
+    return ln_ws_layout(rows, cols, ldq, ldqt, nullptr);
+}
+
+// mode 0: LayerNorm alone (y required); 1: just-in-time quantize (absmax of
+// y in the statistics pass, scale written to *scale_dev before the tile
+// pass reads it); 2: delayed (scale_dev read, absmax in the tile pass,
+// history pushed, next scale written)
+static int layernorm_impl(const char* name, int mode, int dtype, const void* x, int rows, int cols, int ldx,
+                          const void* gamma, const void* beta, float eps, void* y, int ldy, int fmt,
+                          const float* scale_dev, float* next_scale, float* history, int len, uint8_t* q, int ldq,
+                          uint8_t* qt, int ldqt, void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    DF_CHECK(rows >= 0 && cols >= 0 && (ldx >= cols || rows == 0), DF_ERR_INVALID,
+             "%s: bad shape rows=%d cols=%d ldx=%d", name, rows, cols, ldx);
+    DF_CHECK(dtype == DF_DTYPE_FLOAT32 || dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED, "%s: dtype %d not supported",
+             name, dtype);
+    DF_CHECK((gamma == nullptr) == (beta == nullptr), DF_ERR_INVALID, "%s: gamma and beta go together", name);
+    DF_CHECK(eps >= 0.0f, DF_ERR_INVALID, "%s: eps < 0", name);
+    const bool empty = rows == 0 || cols == 0;
+    DF_CHECK(x || empty, DF_ERR_INVALID, "%s: x is NULL", name);
+    if (mode == 0) DF_CHECK(y || empty, DF_ERR_INVALID, "%s: y is NULL", name);
+    if (y) DF_CHECK(ldy >= cols, DF_ERR_INVALID, "%s: ldy=%d < cols", name, ldy);
+    if (mode > 0) {
+        DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad format %d", name, fmt);
+        DF_CHECK(scale_dev && aligned4(scale_dev), DF_ERR_INVALID, "%s: scale_dev NULL or misaligned", name);
+        DF_CHECK(q || qt || empty, DF_ERR_INVALID, "%s: no code output", name);
+        if (q) DF_CHECK(ldq >= cols && ldq % 16 == 0 && aligned16(q), DF_ERR_ALIGN, "%s: q layout (ldq=%d)", name, ldq);
+        if (qt)
+            DF_CHECK(ldqt >= rows && ldqt % 16 == 0 && aligned16(qt), DF_ERR_ALIGN, "%s: qt layout (ldqt=%d)", name,
+                     ldqt);
+    } else {
+        q = qt = nullptr;
+    }
+    if (mode == 2) {
+        DF_CHECK(history && next_scale && aligned4(history) && aligned4(next_scale), DF_ERR_INVALID,
+                 "%s: history/next scale NULL or misaligned", name);
+        DF_CHECK(len >= 1 && len <= kMaxHistory, DF_ERR_INVALID, "%s: history length %d not in [1, %d]", name, len,
+                 kMaxHistory);
+    }
+    size_t part_off = 0;
+    const size_t need = ln_ws_layout(rows, cols, q ? ldq : 0, qt ? ldqt : 0, &part_off);
+    DF_CHECK(ws && aligned16(ws), DF_ERR_WORKSPACE, "%s: needs a 16-byte aligned workspace", name);
+    DF_CHECK(ws_bytes >= need, DF_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu", name, ws_bytes, need);
+    hipStream_t st = as_stream(stream);
+    float2* stat = static_cast<float2*>(ws);
+    uint32_t* parts = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + part_off);
+    const bool bf = dtype == DF_DTYPE_BFLOAT16;
+    if (empty) {
+        // no values: absmax 0, scale 1 (stage 2 over no partials)
+        if (mode == 1)
+            absmax_stage2<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, nullptr, const_cast<float*>(scale_dev));
+        if (mode == 2) amax_history_kernel<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, history, len, next_scale);
+        return mode ? launch_status(name) : DF_OK;
+    }
+    // statistics pass
+    const int sblocks = (rows + 3) / 4;
+#define DF_LNS(T, A)                                                                                         \
+    ln_stats_kernel<T, A><<<sblocks, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, ldx, eps,      \
+                                                        static_cast<const T*>(gamma), static_cast<const T*>(beta), \
+                                                        stat, parts)
+    if (bf) { if (mode == 1) DF_LNS(uint16_t, true); else DF_LNS(uint16_t, false); }
+    else { if (mode == 1) DF_LNS(float, true); else DF_LNS(float, false); }
+#undef DF_LNS
+    if (mode == 1)
+        absmax_stage2<<<1, kThreads, 0, st>>>(parts, sblocks, fmt, nullptr, const_cast<float*>(scale_dev));
+    // tile pass
+    LnArgs la;
+    la.stat = stat;
+    la.gamma = gamma;
+    la.beta = beta;
+    la.y = y;
+    la.ldy = ldy;
+    const int esz = bf ? 2 : 4;
+    la.y_vec = y && aligned16(y) && ((int64_t)ldy * esz) % 16 == 0;
+    const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt);
+    DF_CHECK(grid.y <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
+    const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
+#define DF_LNT(T, F, CODES, AMAX)                                                                              \
+    quantize_2d_kernel<T, F, false, CODES, AMAX, true><<<grid, kThreads, 0, st>>>(                             \
+        static_cast<const T*>(x), rows, cols, ldx, vec_ok, scale_dev, q, ldq, qt, ldqt, nullptr, parts, la)
+    if (mode == 0) {
+        if (bf) DF_LNT(uint16_t, E4M3, false, false); else DF_LNT(float, E4M3, false, false);
+    } else if (mode == 1) {
+        if (bf) { if (fmt == E4M3) DF_LNT(uint16_t, E4M3, true, false); else DF_LNT(uint16_t, E5M2, true, false); }
+        else { if (fmt == E4M3) DF_LNT(float, E4M3, true, false); else DF_LNT(float, E5M2, true, false); }
+    } else {
+        if (bf) { if (fmt == E4M3) DF_LNT(uint16_t, E4M3, true, true); else DF_LNT(uint16_t, E5M2, true, true); }
+        else { if (fmt == E4M3) DF_LNT(float, E4M3, true, true); else DF_LNT(float, E5M2, true, true); }
+        amax_history_kernel<<<1, kThreads, 0, st>>>(parts, (int)(grid.x * grid.y), fmt, history, len, next_scale);
+    }
+#undef DF_LNT
+    return launch_status(name);
+}
+
+extern "C" int df_layernorm(int dtype, const void* x, int rows, int cols, int ldx, const void* gamma,
+                            const void* beta, float eps, void* y, int ldy, void* ws, size_t ws_bytes, void* stream) {
+    return layernorm_impl("df_layernorm", 0, dtype, x, rows, cols, ldx, gamma, beta, eps, y, ldy, E4M3, nullptr,
+                          nullptr, nullptr, 0, nullptr, 0, nullptr, 0, ws, ws_bytes, stream);
+}
+
+extern "C" int df_layernorm_quantize(int dtype, const void* x, int rows, int cols, int ldx, const void* gamma,
+                                     const void* beta, float eps, void* y, int ldy, int fmt, float* scale_dev,
+                                     uint8_t* q, int ldq, uint8_t* qt, int ldqt, void* ws, size_t ws_bytes,
+                                     void* stream) {
+    return layernorm_impl("df_layernorm_quantize", 1, dtype, x, rows, cols, ldx, gamma, beta, eps, y, ldy, fmt,
+                          scale_dev, nullptr, nullptr, 0, q, ldq, qt, ldqt, ws, ws_bytes, stream);
+}
+
+extern "C" int df_layernorm_quantize_delayed(int dtype, const void* x, int rows, int cols, int ldx,
+                                             const void* gamma, const void* beta, float eps, void* y, int ldy,
+                                             int fmt, const float* scale_dev, float* next_scale_dev, float* history,
+                                             int len, uint8_t* q, int ldq, uint8_t* qt, int ldqt, void* ws,
+                                             size_t ws_bytes, void* stream) {
+    return layernorm_impl("df_layernorm_quantize_delayed", 2, dtype, x, rows, cols, ldx, gamma, beta, eps, y, ldy,
+                          fmt, scale_dev, next_scale_dev, history, len, q, ldq, qt, ldqt, ws, ws_bytes, stream);
 }

@@ -167,6 +167,43 @@ int df_quantize_2d_delayed(int in_dtype, const void* x, int rows, int cols, int 
                            uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum, void* ws,
                            size_t ws_bytes, void* stream);
 
+/* ---- LayerNorm with the quantize of its output fused in (producer side of
+ * the qkv / fc1 Linears; layer_norm_forward_kernel,
+ * dnn/layers/layer_norm_layer.cu:26-63) ----
+ * Per row of x [rows, cols] (ldx elements apart), dtype fp32 or bf16:
+ *   mean = sum(x)/cols, var = sum((x - mean)^2)/cols, rstd = 1/sqrt(var + eps)
+ *   y = (x - mean) * rstd, then y = fma(y, gamma, beta) when gamma/beta
+ *   (both [cols], same dtype) are given; y is rounded to the dtype (RNE).
+ * Sums are binary32, per-lane strided then a fixed butterfly: deterministic,
+ * not the reference's sequential order.
+ *  df_layernorm                 : writes y [rows, ldy].
+ *  df_layernorm_quantize        : codes of y at the just-in-time scale
+ *                                 (*scale_dev = D1/D2 of absmax(y), measured
+ *                                 in the statistics pass), q [rows, ldq]
+ *                                 and/or qt [cols, ldqt] as df_quantize_2d
+ *                                 writes them; y [rows, ldy] too when
+ *                                 non-NULL.  The codes equal
+ *                                 df_quantize_2d of df_layernorm's y.
+ *  df_layernorm_quantize_delayed: the same at *scale_dev from an amax
+ *                                 history (see df_quantize_2d_delayed).
+ * x is read twice (statistics, then the tile pass) and y need not be
+ * written at all.  ws: df_layernorm_workspace_bytes(rows, cols, ldq or 0,
+ * ldqt or 0) bytes, 16-byte aligned. */
+size_t df_layernorm_workspace_bytes(int rows, int cols, int ldq, int ldqt);
+int df_layernorm(int dtype, const void* x, int rows, int cols, int ldx, const void* gamma,
+                 const void* beta, float eps, void* y, int ldy, void* ws, size_t ws_bytes,
+                 void* stream);
+int df_layernorm_quantize(int dtype, const void* x, int rows, int cols, int ldx,
+                          const void* gamma, const void* beta, float eps, void* y, int ldy,
+                          int fmt, float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
+                          void* ws, size_t ws_bytes, void* stream);
+int df_layernorm_quantize_delayed(int dtype, const void* x, int rows, int cols, int ldx,
+                                  const void* gamma, const void* beta, float eps, void* y,
+                                  int ldy, int fmt, const float* scale_dev,
+                                  float* next_scale_dev, float* history, int len, uint8_t* q,
+                                  int ldq, uint8_t* qt, int ldqt, void* ws, size_t ws_bytes,
+                                  void* stream);
+
 /* ---- fp8 GEMM, "NT": C[m,n] = (sum_k A[m,k] * B[n,k]) * sa * sb + bias[n]
  *   A [M, lda] fp8 (fmt_a), B [N, ldb] fp8 (fmt_b), both row-major with the
  *   reduction dimension contiguous; lda, ldb multiples of 16 and >= K;

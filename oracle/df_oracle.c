@@ -448,3 +448,37 @@ float dfo_history_push(float* history, int len, float amax, int fmt) {
     for (int i = 0; i < len; ++i) m = history[i] > m ? history[i] : m;
     return dfo_scale(m, fmt);
 }
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm (dnn/layers/layer_norm_layer.cu:26-63)                          */
+/* ------------------------------------------------------------------------ */
+
+/* One row per iteration, as the reference's thread 0 does: sequential
+ * binary32 sum for the mean, sequential sum of squared deviations (the
+ * product-add as one fused multiply-add, the contraction nvcc applies by
+ * default), var = sum / C, rstd = 1 / sqrt(var + eps) (correctly rounded
+ * steps; the reference's rsqrtf is an approximation within 2 ulp), then
+ * y = (x - mean) * rstd and, with gamma/beta, fma(y, gamma, beta) (again the
+ * default contraction of `norm * gamma + beta`).  round_bf16 != 0 rounds y
+ * to bf16 (RNE), the reference's cast to T for a bf16 tensor. */
+void dfo_layernorm(const float* x, int rows, int C, const float* gamma, const float* beta,
+                   float eps, int round_bf16, float* y) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (int64_t)r * C;
+        float sum = 0.0f;
+        for (int i = 0; i < C; ++i) sum += xr[i];
+        const float mean = sum / (float)C;
+        float sq = 0.0f;
+        for (int i = 0; i < C; ++i) {
+            const float d = xr[i] - mean;
+            sq = fmaf(d, d, sq);
+        }
+        const float var = sq / (float)C;
+        const float rstd = 1.0f / sqrtf(var + eps);
+        for (int i = 0; i < C; ++i) {
+            float n = (xr[i] - mean) * rstd;
+            if (gamma) n = fmaf(n, gamma[i], beta[i]);
+            y[(int64_t)r * C + i] = round_bf16 ? dfo_bf16_to_f32(dfo_f32_to_bf16(n)) : n;
+        }
+    }
+}

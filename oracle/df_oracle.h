@@ -122,6 +122,11 @@ void dfo_adam_step(float* p, const float* grad, float* m, float* v, int64_t n,
  * return the scale of the new maximum, the one the next pass uses ---- */
 float dfo_history_push(float* history, int len, float amax, int fmt);
 
+/* ---- LayerNorm forward (dnn/layers/layer_norm_layer.cu:26-63), per row of
+ * C; gamma/beta NULL = no affine map; round_bf16 rounds y to bf16 ---- */
+void dfo_layernorm(const float* x, int rows, int C, const float* gamma, const float* beta,
+                   float eps, int round_bf16, float* y);
+
 #ifdef __cplusplus
 }
 #endif

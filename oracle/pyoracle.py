@@ -47,6 +47,7 @@ _SIGS = {
     "dfo_bias_correction": (_f, [_f, _i]),
     "dfo_adam_step": (None, [_vp, _vp, _vp, _vp, _i64, _f, _f, _f, _f, _f, _i, _f]),
     "dfo_history_push": (_f, [_vp, _i, _f, _i]),
+    "dfo_layernorm": (None, [_vp, _i, _i, _vp, _vp, _f, _i, _vp]),
 }
 
 _lib = None
@@ -241,3 +242,16 @@ def history_push(history: np.ndarray, amax: float, fmt: int) -> float:
     """Delayed scaling: newest amax first; returns the next pass's scale."""
     assert history.dtype == np.float32 and history.flags.c_contiguous
     return lib().dfo_history_push(_p(history), history.size, amax, fmt)
+
+
+def layernorm(x: np.ndarray, gamma=None, beta=None, eps=1e-5, round_bf16=False) -> np.ndarray:
+    """LayerNorm over rows of a float32 [rows, C] array (the reference's
+    thread-0 loops); gamma/beta float32 [C] or None."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, C = x.shape
+    y = np.empty_like(x)
+    g = None if gamma is None else np.ascontiguousarray(gamma, np.float32)
+    b = None if beta is None else np.ascontiguousarray(beta, np.float32)
+    lib().dfo_layernorm(_p(x), rows, C, None if g is None else _p(g), None if b is None else _p(b), eps,
+                        int(round_bf16), _p(y))
+    return y
