@@ -58,6 +58,7 @@ def parse():
     p.add_argument("--no-streaming", action="store_true", help="skip the config 5 layer-streaming leg")
     p.add_argument("--no-optimizer", action="store_true", help="skip the clip + Adam leg")
     p.add_argument("--no-delayed", action="store_true", help="skip the delayed-scaling step leg")
+    p.add_argument("--no-producer", action="store_true", help="skip the LayerNorm + quantize leg")
     p.add_argument("--history", type=int, default=16, help="amax history length of the delayed-scaling leg")
     p.add_argument("--stream-layers", type=int, default=48)
     p.add_argument("--stream-slots", type=int, default=4)
@@ -310,6 +311,8 @@ def main():
         out["delayed_scaling"] = delayed
     if not args.no_conversion:
         out["conversion"] = conversion_bench(torch, df, synth, dev, cur())
+    if not args.no_producer:
+        out["producer"] = producer_bench(torch, df, synth, dev, cur())
     if not args.no_optimizer:
         out["optimizer"] = optimizer_bench(torch, df, dev, cur(), layers=args.stream_layers)
     if not args.no_streaming:
@@ -563,6 +566,69 @@ def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit
     return {"history": H, "steps": 2 * reps, "ms_per_step": round(ms, 4),
             "tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
             "speedup_vs_just_in_time": round(jit_ms / ms, 4)}
+
+
+def producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10):
+    """Row f3 at the GPT-2 XL LayerNorm shape (M tokens x d = 1600, bf16, with
+    gamma/beta): the unfused chain the reference's layers imply (LayerNorm
+    writes y; the Linear reads it for the absmax, then again to quantize it
+    into row and transposed e4m3 codes) against the fused producer (row
+    statistics + absmax in one pass, codes in a second; y never written),
+    just-in-time and delayed.  Bytes per element: unfused 2+2 | 2 | 2+2
+    (LN | absmax | quantize), fused 2 | 2+2, minimum 2+2 (read x once,
+    write both code layouts)."""
+    import numpy as np
+    from deepfuse_amd import DType, Fmt
+    BF, E4 = int(DType.BFLOAT16), int(Fmt.E4M3)
+    bf = lambda a: torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+    x = bf(synth.normal((M, C), 2.0, seed=1700, mean=0.5))
+    g = bf(synth.normal((C,), 0.2, seed=1701, mean=1.0))
+    b = bf(synth.normal((C,), 0.5, seed=1702))
+    y = torch.empty_like(x)
+    Cp, Mp = df.round16(C), df.round16(M)
+    q = torch.empty((M, Cp), dtype=torch.uint8, device=dev)
+    qt = torch.empty((C, Mp), dtype=torch.uint8, device=dev)
+    sc = torch.empty(4, dtype=torch.float32, device=dev)
+    hist = torch.zeros(16, dtype=torch.float32, device=dev)
+    lws_b = df.lib().df_layernorm_workspace_bytes(M, C, Cp, Mp)
+    lws = torch.empty(lws_b, dtype=torch.uint8, device=dev)
+    aws = torch.empty(df.lib().df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
+    p = sc.data_ptr()
+
+    def unfused():
+        df.call("df_layernorm", BF, x.data_ptr(), M, C, C, g.data_ptr(), b.data_ptr(), 1e-5, y.data_ptr(), C,
+                lws.data_ptr(), lws_b, stream)
+        df.call("df_absmax_scale_bf16", y.data_ptr(), y.numel(), E4, None, p, aws.data_ptr(), aws.numel(), stream)
+        df.call("df_quantize_2d", BF, y.data_ptr(), M, C, C, E4, p, q.data_ptr(), Cp, qt.data_ptr(), Mp, stream)
+
+    def fused():
+        df.call("df_layernorm_quantize", BF, x.data_ptr(), M, C, C, g.data_ptr(), b.data_ptr(), 1e-5, None, 0,
+                E4, p + 4, q.data_ptr(), Cp, qt.data_ptr(), Mp, lws.data_ptr(), lws_b, stream)
+
+    def fused_delayed():
+        df.call("df_layernorm_quantize_delayed", BF, x.data_ptr(), M, C, C, g.data_ptr(), b.data_ptr(), 1e-5, None,
+                0, E4, p + 8, p + 8, hist.data_ptr(), 16, q.data_ptr(), Cp, qt.data_ptr(), Mp, lws.data_ptr(),
+                lws_b, stream)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    n = M * C
+    res = {"shape": [M, C], "dtype": "bf16", "min_bytes_per_elem": 4}
+    for name, fn, bpe in (("unfused", unfused, 10), ("fused", fused, 6), ("fused_delayed", fused_delayed, 6)):
+        ms = timed(fn)
+        res[name] = {"ms": round(ms, 4), "bytes_per_elem": bpe, "gbs": round(n * bpe / (ms * 1e-3) / 1e9, 1),
+                     "min_bytes_gbs": round(n * 4 / (ms * 1e-3) / 1e9, 1)}
+    res["fused_speedup"] = round(res["unfused"]["ms"] / res["fused"]["ms"], 3)
+    return res
 
 
 def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):

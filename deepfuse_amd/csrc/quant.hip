@@ -285,22 +285,27 @@ constexpr int kT2 = 128;
 template <typename InT> struct Ld;
 template <> struct Ld<float> {
     static constexpr int E = 4;
+    static __device__ __forceinline__ void widen(const u32x4 t, float* v) {
+        v[0] = __uint_as_float(t.x); v[1] = __uint_as_float(t.y);
+        v[2] = __uint_as_float(t.z); v[3] = __uint_as_float(t.w);
+    }
     static __device__ __forceinline__ void vec(const float* p, float* v) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(p);
-        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        widen(*reinterpret_cast<const u32x4*>(p), v);
     }
     static __device__ __forceinline__ float one(const float* p) { return *p; }
 };
 template <> struct Ld<uint16_t> {
     static constexpr int E = 8;
-    static __device__ __forceinline__ void vec(const uint16_t* p, float* v) {
-        const u32x4 t = *reinterpret_cast<const u32x4*>(p);
+    static __device__ __forceinline__ void widen(const u32x4 t, float* v) {
         const uint32_t w[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             v[2 * i] = bf16_to_f32(w[i] & 0xFFFFu);
             v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
         }
+    }
+    static __device__ __forceinline__ void vec(const uint16_t* p, float* v) {
+        widen(*reinterpret_cast<const u32x4*>(p), v);
     }
     static __device__ __forceinline__ float one(const uint16_t* p) { return bf16_to_f32(*p); }
 };
@@ -396,17 +401,9 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
             lb[e] = affine && in ? Ld<InT>::one(static_cast<const InT*>(ln.beta) + c + e) : 0.0f;
         }
     }
-#pragma unroll
-    for (int rr = 0; rr < RPT; ++rr) {
+    // everything after the load of one row's E values
+    auto row = [&](int rr, float* v) {
         const int r = r0 + rg * RPT + rr;
-        float v[E];
-        if (r < rows && full) {
-            Ld<InT>::vec(x + (int64_t)r * ldx + c, v);
-        } else {
-#pragma unroll
-            for (int e = 0; e < E; ++e)
-                v[e] = (r < rows && c + e < cols) ? Ld<InT>::one(x + (int64_t)r * ldx + c + e) : 0.0f;
-        }
         if (LN && r < rows) {
             const float2 st = ln.stat[r];
 #pragma unroll
@@ -431,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
 #pragma unroll
             for (int e = 0; e < E; ++e) am = fold_f32(am, __float_as_uint(v[e]));
         }
-        if (!CODES) continue;
+        if (!CODES) return;
 #pragma unroll
         for (int g = 0; g < E / 4; ++g)
             codes[rr][g] = quant4_fast<FMT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
@@ -440,6 +437,34 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
                 *reinterpret_cast<u32x2*>(q + (int64_t)r * ldq + c) = u32x2{codes[rr][0], codes[rr][E / 4 - 1]};
             else
                 *reinterpret_cast<uint32_t*>(q + (int64_t)r * ldq + c) = codes[rr][0];
+        }
+    };
+    if (full && r0 + kT2 <= rows) {
+        // every row of this thread is in range and 16-byte loadable: issue
+        // all RPT loads before using any, so they are in flight together
+        u32x4 raw[RPT];
+#pragma unroll
+        for (int rr = 0; rr < RPT; ++rr)
+            raw[rr] = *reinterpret_cast<const u32x4*>(x + (int64_t)(r0 + rg * RPT + rr) * ldx + c);
+#pragma unroll
+        for (int rr = 0; rr < RPT; ++rr) {
+            float v[E];
+            Ld<InT>::widen(raw[rr], v);
+            row(rr, v);
+        }
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < RPT; ++rr) {
+            const int r = r0 + rg * RPT + rr;
+            float v[E];
+            if (r < rows && full) {
+                Ld<InT>::vec(x + (int64_t)r * ldx + c, v);
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    v[e] = (r < rows && c + e < cols) ? Ld<InT>::one(x + (int64_t)r * ldx + c + e) : 0.0f;
+            }
+            row(rr, v);
         }
     }
     if (CODES && qt) {
@@ -538,15 +563,76 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Rows of up to kLnRegChunks 16-byte chunks per lane (2048 bf16 or 1024
+// fp32 values) stay in registers: one read of the row, 16-byte loads.
+constexpr int kLnRegChunks = 4;
+
 template <typename InT, bool ABSMAX>
 __global__ __launch_bounds__(kThreads) void ln_stats_kernel(const InT* __restrict__ x, int rows, int cols, int ldx,
-                                                            float eps, const InT* __restrict__ gamma,
+                                                            bool vec_ok, bool gb_vec, float eps,
+                                                            const InT* __restrict__ gamma,
                                                             const InT* __restrict__ beta, float2* __restrict__ stat,
                                                             uint32_t* __restrict__ amaxpart) {
+    constexpr int E = Ld<InT>::E;
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     uint32_t am = 0;
-    if (r < rows) {
+    if (r < rows && vec_ok && cols <= 64 * E * kLnRegChunks) {
+        const InT* xr = x + (int64_t)r * ldx;
+        const int nfull = cols / E;  // whole 16-byte chunks; the tail (< E values) is chunk nfull
+        float v[kLnRegChunks][E];
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kLnRegChunks; ++k) {
+            const int j = lane + 64 * k;
+            if (j < nfull) {
+                Ld<InT>::vec(xr + j * E, v[k]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) v[k][e] = j * E + e < cols ? Ld<InT>::one(xr + j * E + e) : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) s += v[k][e];  // padding adds +0
+        }
+        const float mean = wave_sum(s) / (float)cols;
+        float sq = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kLnRegChunks; ++k) {
+            const int j = lane + 64 * k;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float d = v[k][e] - mean;
+                sq = j * E + e < cols ? __builtin_fmaf(d, d, sq) : sq;
+            }
+        }
+        const float var = wave_sum(sq) / (float)cols;
+        const float rstd = 1.0f / __builtin_sqrtf(var + eps);
+        if (lane == 0) stat[r] = make_float2(mean, rstd);
+        if (ABSMAX) {
+            const bool affine = gamma != nullptr;
+#pragma unroll
+            for (int k = 0; k < kLnRegChunks; ++k) {
+                const int j = lane + 64 * k;
+                float g[E], b[E];
+                if (affine && gb_vec && j < nfull) {
+                    Ld<InT>::vec(gamma + j * E, g);
+                    Ld<InT>::vec(beta + j * E, b);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const bool in = affine && j * E + e < cols;
+                        g[e] = in ? Ld<InT>::one(gamma + j * E + e) : 0.0f;
+                        b[e] = in ? Ld<InT>::one(beta + j * E + e) : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const uint32_t y = __float_as_uint(ln_apply<InT>(v[k][e], mean, rstd, affine, g[e], b[e]));
+                    am = j * E + e < cols ? fold_f32(am, y) : am;
+                }
+            }
+        }
+    } else if (r < rows) {
         const InT* xr = x + (int64_t)r * ldx;
         float s = 0.0f;
         for (int i = lane; i < cols; i += 64) s += Ld<InT>::one(xr + i);
@@ -991,8 +1077,12 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     }
     // statistics pass
     const int sblocks = (rows + 3) / 4;
-#define DF_LNS(T, A)                                                                                         \
-    ln_stats_kernel<T, A><<<sblocks, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, ldx, eps,      \
+    const int esz = bf ? 2 : 4;
+    const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
+    const bool gb_vec = gamma && aligned16(gamma) && aligned16(beta);
+#define DF_LNS(T, A)                                                                                           \
+    ln_stats_kernel<T, A><<<sblocks, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, ldx, vec_ok,     \
+                                                        gb_vec, eps,                                            \
                                                         static_cast<const T*>(gamma), static_cast<const T*>(beta), \
                                                         stat, parts)
     if (bf) { if (mode == 1) DF_LNS(uint16_t, true); else DF_LNS(uint16_t, false); }
@@ -1007,11 +1097,9 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     la.beta = beta;
     la.y = y;
     la.ldy = ldy;
-    const int esz = bf ? 2 : 4;
     la.y_vec = y && aligned16(y) && ((int64_t)ldy * esz) % 16 == 0;
     const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt);
     DF_CHECK(grid.y <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
-    const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
 #define DF_LNT(T, F, CODES, AMAX)                                                                              \
     quantize_2d_kernel<T, F, false, CODES, AMAX, true><<<grid, kThreads, 0, st>>>(                             \
         static_cast<const T*>(x), rows, cols, ldx, vec_ok, scale_dev, q, ldq, qt, ldqt, nullptr, parts, la)
