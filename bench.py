@@ -603,7 +603,7 @@ def producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10):
 
     def fused():
         df.call("df_layernorm_quantize", BF, x.data_ptr(), M, C, C, g.data_ptr(), b.data_ptr(), 1e-5, None, 0,
-                E4, p + 4, q.data_ptr(), Cp, qt.data_ptr(), Mp, lws.data_ptr(), lws_b, stream)
+                E4, p + 4, None, q.data_ptr(), Cp, qt.data_ptr(), Mp, lws.data_ptr(), lws_b, stream)
 
     def fused_delayed():
         df.call("df_layernorm_quantize_delayed", BF, x.data_ptr(), M, C, C, g.data_ptr(), b.data_ptr(), 1e-5, None,

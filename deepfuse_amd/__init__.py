@@ -109,7 +109,7 @@ _SIGS = {
     "df_layernorm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
     "df_layernorm": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_layernorm_quantize": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int, _c_int,
-                                       _vp, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+                                       _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_layernorm_quantize_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int,
                                                _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz,
                                                _vp]),
@@ -440,7 +440,8 @@ def layernorm(x, gamma=None, beta=None, eps=1e-5, fmt: Fmt | None = None, want_y
     if delayed is None:
         scale = torch.empty(1, dtype=torch.float32, device=x.device)
         call("df_layernorm_quantize", dt, _ptr(x), rows, cols, x.stride(0), _ptr(gamma), _ptr(beta), float(eps),
-             _ptr(y), ldy, int(fmt), _ptr(scale), _ptr(q), ldq, _ptr(qt), ldqt, _ptr(ws), ws.numel(), _stream())
+             _ptr(y), ldy, int(fmt), _ptr(scale), None, _ptr(q), ldq, _ptr(qt), ldqt, _ptr(ws), ws.numel(),
+             _stream())
     else:
         scale = delayed.scale.clone()
         call("df_layernorm_quantize_delayed", dt, _ptr(x), rows, cols, x.stride(0), _ptr(gamma), _ptr(beta),

@@ -1026,8 +1026,9 @@ extern "C" size_t df_layernorm_workspace_bytes(int rows, int cols, int ldq, int 
 
 // mode 0: LayerNorm alone (y required); 1: just-in-time quantize (absmax of
 // y in the statistics pass, scale written to *scale_dev before the tile
-// pass reads it); 2: delayed (scale_dev read, absmax in the tile pass,
-// history pushed, next scale written)
+// pass reads it, the absmax itself to *next_scale when non-NULL); 2: delayed
+// (scale_dev read, absmax in the tile pass, history pushed, next scale
+// written)
 static int layernorm_impl(const char* name, int mode, int dtype, const void* x, int rows, int cols, int ldx,
                           const void* gamma, const void* beta, float eps, void* y, int ldy, int fmt,
                           const float* scale_dev, float* next_scale, float* history, int len, uint8_t* q, int ldq,
@@ -1071,7 +1072,7 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     if (empty) {
         // no values: absmax 0, scale 1 (stage 2 over no partials)
         if (mode == 1)
-            absmax_stage2<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, nullptr, const_cast<float*>(scale_dev));
+            absmax_stage2<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, next_scale, const_cast<float*>(scale_dev));
         if (mode == 2) amax_history_kernel<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, history, len, next_scale);
         return mode ? launch_status(name) : DF_OK;
     }
@@ -1089,7 +1090,7 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     else { if (mode == 1) DF_LNS(float, true); else DF_LNS(float, false); }
 #undef DF_LNS
     if (mode == 1)
-        absmax_stage2<<<1, kThreads, 0, st>>>(parts, sblocks, fmt, nullptr, const_cast<float*>(scale_dev));
+        absmax_stage2<<<1, kThreads, 0, st>>>(parts, sblocks, fmt, next_scale, const_cast<float*>(scale_dev));
     // tile pass
     LnArgs la;
     la.stat = stat;
@@ -1125,10 +1126,11 @@ extern "C" int df_layernorm(int dtype, const void* x, int rows, int cols, int ld
 
 extern "C" int df_layernorm_quantize(int dtype, const void* x, int rows, int cols, int ldx, const void* gamma,
                                      const void* beta, float eps, void* y, int ldy, int fmt, float* scale_dev,
-                                     uint8_t* q, int ldq, uint8_t* qt, int ldqt, void* ws, size_t ws_bytes,
-                                     void* stream) {
+                                     float* absmax_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt, void* ws,
+                                     size_t ws_bytes, void* stream) {
+    DF_CHECK(!absmax_dev || aligned4(absmax_dev), DF_ERR_ALIGN, "df_layernorm_quantize: absmax_dev misaligned");
     return layernorm_impl("df_layernorm_quantize", 1, dtype, x, rows, cols, ldx, gamma, beta, eps, y, ldy, fmt,
-                          scale_dev, nullptr, nullptr, 0, q, ldq, qt, ldqt, ws, ws_bytes, stream);
+                          scale_dev, absmax_dev, nullptr, 0, q, ldq, qt, ldqt, ws, ws_bytes, stream);
 }
 
 extern "C" int df_layernorm_quantize_delayed(int dtype, const void* x, int rows, int cols, int ldx,

@@ -22,6 +22,7 @@
 #include <string>
 
 #include "dnn/core/layer.hpp"
+#include "dnn/layers/layer_norm_layer.hpp"
 #include "dnn/core/tensor.hpp"
 
 namespace dnn {
@@ -33,6 +34,13 @@ public:
     ~FullyConnectedLayer() override = default;
 
     tensor<TT> forward(const tensor<TT>& input) override;
+    // forward(norm.forward(input)) with the LayerNorm fused into the
+    // quantize of this layer's input: the normalised tensor is never
+    // written; the codes (and the cached transposed codes for backward) come
+    // straight from `input` (df_layernorm_quantize).  Same values as the
+    // unfused pair.  norm records its input for its own backward as
+    // norm.forward would.
+    tensor<TT> forward(const tensor<TT>& input, LayerNormLayer<TT>& norm);
     tensor<TT> backward(const tensor<TT>& grad_output) override;
 
     std::string name() const override { return "FullyConnected"; }
@@ -79,6 +87,11 @@ private:
     // returns the device pointer of the scale the codes were made with
     const float* quantize_delayed(Delayed& d, const TT* x, int rows, int cols, int fmt, uint8_t* q, int ldq,
                                   uint8_t* qt, int ldqt, float* colsum);
+    // input operand codes: from `input` itself, or from LayerNorm(input)
+    // when norm is given; returns the device pointer of their scale
+    const float* quantize_input(const tensor<TT>& input, int N, const LayerNormLayer<TT>* norm, uint8_t* xq, int Kp,
+                                uint8_t* xt, int Np, float* jit_scale);
+    tensor<TT> forward_impl(const tensor<TT>& input, LayerNormLayer<TT>* norm);
 
     int in_features_;
     int out_features_;

@@ -143,12 +143,73 @@ const float* FullyConnectedLayer<TT>::quantize_delayed(Delayed& d, const TT* x, 
 }
 
 template <typename TT>
+const float* FullyConnectedLayer<TT>::quantize_input(const tensor<TT>& input, int N, const LayerNormLayer<TT>* norm,
+                                                     uint8_t* xq, int Kp, uint8_t* xt, int Np, float* jit_scale) {
+    constexpr int dt = dtype_traits<TT>::value;
+    if (!norm) {
+        if (history_len_ > 0)
+            return quantize_delayed(dx_, input.data(), N, in_features_, DF_FMT_E4M3, xq, Kp, xt, Np, nullptr);
+        quantize_operand(input.data(), N, in_features_, DF_FMT_E4M3, jit_scale, xq, Kp, xt, Np, nullptr);
+        return jit_scale;
+    }
+    // LayerNorm fused into the quantize: statistics pass, then codes
+    const size_t wb = df_layernorm_workspace_bytes(N, in_features_, Kp, xt ? Np : 0);
+    void* ws = colsum_ws_.get(wb);
+    const void* g = norm->affine() ? norm->gamma().data() : nullptr;
+    const void* b = norm->affine() ? norm->beta().data() : nullptr;
+    const float eps = norm->epsilon();
+    if (history_len_ == 0) {
+        CHECK_DF_EX(df_layernorm_quantize(dt, input.data(), N, in_features_, in_features_, g, b, eps, nullptr, 0,
+                                          DF_FMT_E4M3, jit_scale, nullptr, xq, Kp, xt, Np, ws, wb, st()));
+        return jit_scale;
+    }
+    Delayed& d = dx_;
+    float* hist = reinterpret_cast<float*>(d.hist.get((size_t)history_len_ * sizeof(float)));
+    float* sc = reinterpret_cast<float*>(d.scales.get(3 * sizeof(float)));
+    float* used = sc + d.cur;
+    float* next = sc + (d.cur ^ 1);
+    if (!d.seeded) {
+        // the first pass runs at its own absmax, which seeds the history
+        CHECK_DF_EX(df_layernorm_quantize(dt, input.data(), N, in_features_, in_features_, g, b, eps, nullptr, 0,
+                                          DF_FMT_E4M3, used, sc + 2, xq, Kp, xt, Np, ws, wb, st()));
+        CHECK_DF_EX(df_amax_history_init(sc + 2, DF_FMT_E4M3, hist, history_len_, next, st()));
+        d.seeded = true;
+    } else {
+        CHECK_DF_EX(df_layernorm_quantize_delayed(dt, input.data(), N, in_features_, in_features_, g, b, eps, nullptr,
+                                                  0, DF_FMT_E4M3, used, next, hist, history_len_, xq, Kp, xt, Np, ws,
+                                                  wb, st()));
+    }
+    d.cur ^= 1;
+    return used;
+}
+
+template <typename TT>
 tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input) {
+    return forward_impl(input, nullptr);
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input, LayerNormLayer<TT>& norm) {
+    if (norm.norm_size() != in_features_)
+        throw std::invalid_argument("FullyConnectedLayer::forward: LayerNorm over " + std::to_string(norm.norm_size()) +
+                                    " values feeds a layer of " + std::to_string(in_features_) + " inputs");
+    norm.rows_of(input);  // throws on a ragged input
+    norm.note_input(input);
+    return forward_impl(input, &norm);
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerNormLayer<TT>* norm) {
     const auto& sh = input.shape();
-    if (sh.size() != 2 || sh[1] != in_features_)
-        throw std::invalid_argument("FullyConnectedLayer::forward: input must be [N, " +
-                                    std::to_string(in_features_) + "], got " + input.to_string());
-    const int N = sh[0];
+    int N;
+    if (norm) {
+        N = norm->rows_of(input);  // any rank: runs of in_features values
+    } else {
+        if (sh.size() != 2 || sh[1] != in_features_)
+            throw std::invalid_argument("FullyConnectedLayer::forward: input must be [N, " +
+                                        std::to_string(in_features_) + "], got " + input.to_string());
+        N = sh[0];
+    }
     tensor<TT> output({N, out_features_});
     if (N == 0) return output;
     constexpr int dt = dtype_traits<TT>::value;
@@ -156,24 +217,22 @@ tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input) {
     float* sc = reinterpret_cast<float*>(scales_.get(4 * sizeof(float)));
     uint8_t* xq = codes_a_.get((size_t)N * Kp);
     uint8_t* xt = nullptr;
-    float* sx = sc;
+    float* sx_jit = sc;
     if (this->training_enabled_) {
         const std::vector<int> xt_shape{in_features_, Np};
         if (!xt_cache_ || xt_cache_->shape() != xt_shape) xt_cache_.emplace(xt_shape);
         xt = reinterpret_cast<uint8_t*>(xt_cache_->data());
-        sx = xt_cache_->scale_data();
+        sx_jit = xt_cache_->scale_data();
     }
+    const float* sx = quantize_input(input, N, norm, xq, Kp, xt, Np, sx_jit);
     uint8_t* wq = codes_b_.get((size_t)out_features_ * Kp);
     const float* sw = sc + 1;
     if (history_len_ > 0) {
-        sx = const_cast<float*>(quantize_delayed(dx_, input.data(), N, in_features_, DF_FMT_E4M3, xq, Kp, xt, Np,
-                                                 nullptr));
         sw = quantize_delayed(dw_, this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, wq, Kp, nullptr,
                               0, nullptr);
         sx_used_ = sx;
         sw_used_ = sw;
     } else {
-        quantize_operand(input.data(), N, in_features_, DF_FMT_E4M3, sx, xq, Kp, xt, Np, nullptr);
         quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, wq, Kp, nullptr, 0,
                          nullptr);
         sx_used_ = sw_used_ = nullptr;

@@ -179,7 +179,8 @@ int df_quantize_2d_delayed(int in_dtype, const void* x, int rows, int cols, int 
  *  df_layernorm                 : writes y [rows, ldy].
  *  df_layernorm_quantize        : codes of y at the just-in-time scale
  *                                 (*scale_dev = D1/D2 of absmax(y), measured
- *                                 in the statistics pass), q [rows, ldq]
+ *                                 in the statistics pass; *absmax_dev =
+ *                                 absmax(y) when non-NULL), q [rows, ldq]
  *                                 and/or qt [cols, ldqt] as df_quantize_2d
  *                                 writes them; y [rows, ldy] too when
  *                                 non-NULL.  The codes equal
@@ -195,8 +196,8 @@ int df_layernorm(int dtype, const void* x, int rows, int cols, int ldx, const vo
                  void* stream);
 int df_layernorm_quantize(int dtype, const void* x, int rows, int cols, int ldx,
                           const void* gamma, const void* beta, float eps, void* y, int ldy,
-                          int fmt, float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
-                          void* ws, size_t ws_bytes, void* stream);
+                          int fmt, float* scale_dev, float* absmax_dev, uint8_t* q, int ldq,
+                          uint8_t* qt, int ldqt, void* ws, size_t ws_bytes, void* stream);
 int df_layernorm_quantize_delayed(int dtype, const void* x, int rows, int cols, int ldx,
                                   const void* gamma, const void* beta, float eps, void* y,
                                   int ldy, int fmt, const float* scale_dev,

@@ -25,6 +25,7 @@
 #include "dnn/core/hip.hpp"
 #include "dnn/core/tensor.hpp"
 #include "dnn/layers/fully_connected_layer.hpp"
+#include "dnn/layers/layer_norm_layer.hpp"
 #include "dnn/optimizers/adam_optimizer.hpp"
 #include "dnn/utils/common.hpp"
 #include "mini_test.hpp"
@@ -111,6 +112,7 @@ using TensorTest = HipFixture;
 using Fp8TensorTest = HipFixture;
 using FullyConnectedLayerTest = HipFixture;
 using AdamOptimizerTest = HipFixture;
+using LayerNormLayerTest = HipFixture;
 using ClipGradNormTest = HipFixture;
 
 }  // namespace
@@ -857,6 +859,104 @@ TEST_F(FullyConnectedLayerTest, DelayedScalingUsesHistoryScale) {
     CHECK_HIP_EX(hipMemcpy(h.data(), layer.amax_history(0), 2 * sizeof(float), hipMemcpyDeviceToHost));
     EXPECT_EQ(h[0], dfo_absmax_f32(x2.data(), (int64_t)x2.size()));
     EXPECT_EQ(h[1], dfo_absmax_f32(x1.data(), (int64_t)x1.size()));
+}
+
+// ---- LayerNormLayer (dnn/layers/layer_norm_layer.cu) and the fused producer ----
+TEST_F(LayerNormLayerTest, ForwardMatchesOracle) {
+    const int rows = 37, C = 100;
+    LayerNormLayer<float> ln(C, 1e-5f, true, false);
+    EXPECT_EQ(ln.parameters().size(), 2u);
+    const auto g = uniform(C, 0.5f, 1.5f, 101), b = uniform(C, -1.0f, 1.0f, 102);
+    ln.parameters()[0]->upload(g.data());
+    ln.parameters()[1]->upload(b.data());
+    const auto x = uniform((size_t)rows * C, -3.0f, 3.0f, 103);
+    tensor<float> t({rows, C});
+    t.upload(x.data());
+    const auto y = download(ln.forward(t));
+    std::vector<float> e(x.size());
+    dfo_layernorm(x.data(), rows, C, g.data(), b.data(), 1e-5f, 0, e.data());
+    EXPECT_LE(rel_err(y, e), 1e-5);
+}
+
+TEST_F(LayerNormLayerTest, DefaultParametersAreIdentityAffine) {
+    const int rows = 8, C = 1600;  // GPT-2 XL width: beyond a 1024-thread block per row
+    LayerNormLayer<float> a(C), b(C, 1e-5f, false);
+    EXPECT_TRUE(b.parameters().empty());
+    const auto x = uniform((size_t)rows * C, -2.0f, 2.0f, 104);
+    tensor<float> t({rows, C});
+    t.upload(x.data());
+    EXPECT_TRUE(download(a.forward(t)) == download(b.forward(t)));
+    std::vector<float> e(x.size());
+    dfo_layernorm(x.data(), rows, C, nullptr, nullptr, 1e-5f, 0, e.data());
+    EXPECT_LE(rel_err(download(b.forward(t)), e), 1e-5);
+}
+
+TEST_F(LayerNormLayerTest, BackwardPassesTheGradientThrough) {
+    LayerNormLayer<float> ln(16, 1e-5f, true, true);
+    tensor<float> g({4, 16});
+    const auto gh = uniform(64, -1.0f, 1.0f, 105);
+    g.upload(gh.data());
+    bool threw = false;
+    try {
+        ln.backward(g);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    EXPECT_TRUE(threw);  // training mode, no forward yet
+    ln.forward(g);
+    EXPECT_TRUE(download(ln.backward(g)) == gh);
+}
+
+TEST_F(LayerNormLayerTest, SaveLoadRoundTrip) {
+    LayerNormLayer<float> a(24), b(24);
+    const auto g = uniform(24, 0.5f, 1.5f, 106);
+    a.parameters()[0]->upload(g.data());
+    std::stringstream ss;
+    a.save(ss);
+    b.load(ss);
+    EXPECT_TRUE(download(*b.parameters()[0]) == g);
+}
+
+TEST_F(LayerNormLayerTest, BFloat16MatchesOracle) {
+    const int rows = 20, C = 96;
+    LayerNormLayer<bfloat16> ln(C);
+    const auto x = bf16_to_float(float_to_bf16(uniform((size_t)rows * C, -2.0f, 2.0f, 107)));
+    tensor<bfloat16> t({rows, C});
+    upload_bf16(t, x);
+    const auto y = download_f(ln.forward(t));
+    std::vector<float> e(x.size());
+    dfo_layernorm(x.data(), rows, C, nullptr, nullptr, 1e-5f, 1, e.data());
+    EXPECT_LE(rel_err(y, e), 1e-2);  // one bf16 step where the binary32 sums differ in order
+}
+
+// fc.forward(x, ln) == fc.forward(ln.forward(x)), forward and backward, just
+// in time and with delayed scaling
+TEST_F(FullyConnectedLayerTest, LayerNormFusedEqualsUnfused) {
+    const int N = 48, in_f = 160, out_f = 72;
+    for (int hist : {0, 4}) {
+        FullyConnectedLayer<float> a(in_f, out_f, true), b(in_f, out_f, true);
+        const auto w = uniform((size_t)out_f * in_f, -0.2f, 0.2f, 111);
+        for (auto* l : {&a, &b}) {
+            l->parameters()[0]->upload(w.data());
+            l->set_delayed_scaling(hist);
+        }
+        LayerNormLayer<float> ln(in_f, 1e-5f, true, true);
+        const auto g = uniform(in_f, 0.5f, 1.5f, 112), bb = uniform(in_f, -0.5f, 0.5f, 113);
+        ln.parameters()[0]->upload(g.data());
+        ln.parameters()[1]->upload(bb.data());
+        for (int step = 0; step < 2; ++step) {
+            auto xh = uniform((size_t)N * in_f, -2.0f, 2.0f, 114 + step);
+            tensor<float> x({N, in_f}), gy({N, out_f});
+            x.upload(xh.data());
+            const auto gh = uniform((size_t)N * out_f, -0.1f, 0.1f, 120 + step);
+            gy.upload(gh.data());
+            const auto ya = download(a.forward(ln.forward(x)));
+            const auto yb = download(b.forward(x, ln));
+            EXPECT_TRUE(ya == yb);
+            EXPECT_TRUE(download(a.backward(gy)) == download(b.backward(gy)));
+            EXPECT_TRUE(download(*a.grad_weights()) == download(*b.grad_weights()));
+        }
+    }
 }
 
 // ---- AdamOptimizer: the reference's cases (adam_optimizer_test.cu:21-214),

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 RUNNER = os.path.join(HERE, "cpp", "dnn_tests")
 
 SUITES = ("HipTest", "TensorTest", "Fp8TensorTest", "FullyConnectedLayerTest", "AdamOptimizerTest",
-          "ClipGradNormTest")
+          "ClipGradNormTest", "LayerNormLayerTest")
 
 
 def _runner():
