@@ -469,11 +469,11 @@ __device__ __forceinline__ constexpr int waitcnt_vm_lgkm0(int n) {
     return (n & 15) | ((n >> 4) << 14) | 0x70;
 }
 
-template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT = false>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
     const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
-    OutT* __restrict__ C, int ldc, int vec_out) {
+    OutT* __restrict__ C, int ldc, int vec_out, int ksteps = 0, int nsplit = 1) {
     constexpr int FM = 4, FN = 2;                 // 32x32 MFMA tiles per wave
     constexpr int ES = (int)sizeof(OutT);
     constexpr int SR = ES == 2 ? 16 : 8;          // epilogue slab rows
@@ -498,10 +498,24 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const int q = P >> 3, rr = P & 7;
     const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int bl = xcd < rr ? xcd * (q + 1) + idx : rr * (q + 1) + (xcd - rr) * q + idx;
-    const int my_tiles = bl < ntiles ? (ntiles - bl + P - 1) / P : 0;
-    const int S = my_tiles * nk;  // DMA steps of this block
-    auto tile_mn = [&](int r, int& m0, int& n0) {
-        const int lt = bl + r * P;
+    // Work units: unit u of the nunits is (K slice u / ntiles, tile u % ntiles
+    // of the grouped order); block bl takes units bl, bl+P, ...  Unsplit: one
+    // slice of all nk steps.  SPLIT: nsplit slices of L = ksteps steps (the
+    // last one shorter); a unit's fp32 partial tile goes to slice ks of C
+    // ([nsplit][M][N], ldc = N).  Units running at the same time share a K
+    // slice, so tiles of one row (column) meet their A (B) panel in L2.
+    const int L = SPLIT ? ksteps : nk;
+    const int nunits = SPLIT ? ntiles * nsplit : ntiles;
+    const int my_tiles = bl < nunits ? (nunits - bl + P - 1) / P : 0;  // work units of this block
+    auto tile_mn = [&](int r, int& m0, int& n0, int& kb, int& nku, int& slot) {
+        int lt = bl + r * P;
+        slot = 0;
+        if (SPLIT) {
+            slot = lt / ntiles;
+            lt -= slot * ntiles;
+        }
+        kb = slot * L;
+        nku = min(nk - kb, L);
         const int per_group = kGroupM * tiles_n;
         const int group = lt / per_group;
         const int first_m = group * kGroupM;
@@ -510,6 +524,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         m0 = (first_m + in_group % gsize) * kPBM;
         n0 = (in_group / gsize) * kPBN;
     };
+    int S = 0;  // DMA steps of this block
+    for (int r = 0; r < my_tiles; ++r) {
+        int m0, n0, kb, nku, slot;
+        tile_mn(r, m0, n0, kb, nku, slot);
+        S += nku;
+    }
 
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * lda, 0x00020000);
     const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, N * ldb, 0x00020000);
@@ -527,11 +547,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const int dch0 = ((lane & 7) ^ (lane >> 4)) << 4;
     const int dch1 = dch0 ^ 64;
     const uint32_t a16 = 16u * (uint32_t)lda, b16 = 16u * (uint32_t)ldb;
-    int d_tile = 0, d_k = 0, d_m0 = 0, d_n0 = 0, d_g = 0;
+    int d_tile = 0, d_k = 0, d_m0 = 0, d_n0 = 0, d_g = 0, d_kb = 0, d_nku = 0, d_slot = 0;
     uint32_t oa0 = kOOB, oa1 = kOOB, ob0 = kOOB, ob1 = kOOB, obias = kOOB;
     auto dprep = [&]() {
         const bool live = d_g < S;
-        const int k0 = d_k * kPKB + dch0, k1 = d_k * kPKB + dch1;
+        const int kstep = d_kb + d_k;
+        const int k0 = kstep * kPKB + dch0, k1 = kstep * kPKB + dch1;
         const uint32_t ra = (uint32_t)(d_m0 + w * 32 + drow), rb = (uint32_t)(d_n0 + w * 32 + drow);
         oa0 = (live && k0 < K) ? ra * (uint32_t)lda + (uint32_t)k0 : kOOB;
         oa1 = (live && k1 < K) ? (ra + 8u) * (uint32_t)lda + (uint32_t)k1 : kOOB;
@@ -559,14 +580,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 4, obias, 0, 0, 0);
     };
     auto dadvance = [&]() {
-        if (d_g < S && ++d_k == nk) {
+        if (d_g < S && ++d_k == d_nku) {
             d_k = 0;
-            if (++d_tile < my_tiles) tile_mn(d_tile, d_m0, d_n0);
+            if (++d_tile < my_tiles) tile_mn(d_tile, d_m0, d_n0, d_kb, d_nku, d_slot);
         }
         ++d_g;
         dprep();
     };
-    if (my_tiles > 0) tile_mn(0, d_m0, d_n0);
+    if (my_tiles > 0) tile_mn(0, d_m0, d_n0, d_kb, d_nku, d_slot);
     dprep();
 
     // ---- fragments (v_mfma_f32_32x32x64_f8f6f4 operand layout: lane l
@@ -593,7 +614,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     v16f acc[FM][FN];
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
     int after_epi = 0, c_h = 0;
-    const float sab = sa[0] * sb[0];
+    const float sab = SPLIT ? 1.0f : sa[0] * sb[0];
 
     // One half-step: MFMAs on (fa, fb); fragments of half-step c_h+1 into
     // (na, nb).  Odd half-steps first wait for the DMA step that half-step
@@ -649,8 +670,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     };
 
     auto epilogue = [&](int tile) {
-        int tm0, tn0;
-        tile_mn(tile, tm0, tn0);
+        int tm0, tn0, tkb, tnku, tslot;
+        tile_mn(tile, tm0, tn0, tkb, tnku, tslot);
+        OutT* const Cu = SPLIT ? C + (int64_t)tslot * M * N : C;
         const int rowb = tm0 + wm * 128;
         const int colw = tn0 + wn * 64;
         const int h4 = (lane >> 5) * 4;
@@ -730,7 +752,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                     const u32x4 val = *reinterpret_cast<const u32x4*>(slab + sr * SROW + rc * 16);
                     const int row = rowb + i * 32 + p * SR + sr;
                     if (row < M) {
-                        OutT* dst = C + (int64_t)row * ldc + scol;
+                        OutT* dst = Cu + (int64_t)row * ldc + scol;
                         if (col_full) {
                             *reinterpret_cast<u32x4*>(dst) = val;
                         } else {
@@ -765,9 +787,11 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     // a tile is 2*max(nk,1) half-steps; the fragments of its first half-step
     // are in (fa0, fb0) when it starts
     for (int tile = 0; tile < my_tiles; ++tile) {
+        int um0, un0, ukb, unku, uslot;
+        tile_mn(tile, um0, un0, ukb, unku, uslot);
         half(Z{}, EVEN{}, fa0, fb0, fa1, fb1);
         half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
-        for (int k = 1; k < nk; ++k) {
+        for (int k = 1; k < unku; ++k) {
             half(NZ{}, EVEN{}, fa0, fb0, fa1, fb1);
             half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
         }
@@ -904,16 +928,45 @@ static void launch_cfg(const GemmArgs& g) {
 // (smaller ones keep the split-K plan below).  Its per-lane buffer offsets
 // reach a tile past the last row, so M*lda and N*ldb stay below 2^31 (and
 // lda, ldb below 2^23); its bias DMA reads whole dwords.
-template <typename BiasT>
-static int persistent_grid(const GemmArgs& g) {
-    const int cus = device_cu_count();
-    if (cus <= 0) return 0;
-    const int64_t tiles = (int64_t)((g.M + kPBM - 1) / kPBM) * ((g.N + kPBN - 1) / kPBN);
-    if (tiles < cus) return 0;
-    if ((int64_t)g.M * g.lda >= (1ll << 31) || (int64_t)g.N * g.ldb >= (1ll << 31)) return 0;
-    if (g.lda >= (1 << 23) || g.ldb >= (1 << 23)) return 0;
-    if (g.bias && !aligned4(g.bias)) return 0;
-    return cus;
+static bool persistent_ok(const GemmArgs& g) {
+    if ((int64_t)g.M * g.lda >= (1ll << 31) || (int64_t)g.N * g.ldb >= (1ll << 31)) return false;
+    if (g.lda >= (1 << 23) || g.ldb >= (1 << 23)) return false;
+    return !g.bias || aligned4(g.bias);
+}
+
+// Outputs with fewer 256x256 tiles than CUs (the dW GEMMs): the persistent
+// kernel over S K slices of L DMA steps (S * tiles work units, fp32 partial
+// tiles, then splitk_reduce_kernel sums the slices in order), S from the
+// rounds cost model of plan_gemm in units of one 128-byte K step of a
+// 256x256 tile plus the partial-tile traffic.  S = 1: one unit per tile.
+// (A stream-K cut into equal per-CU ranges balanced the rounds better but
+// ran 25% slower on the GPT-2 XL dW shapes: the CUs then read their A and B
+// panels at unrelated K offsets and L2 reuse was lost.)
+struct PSplit {
+    int S, L;
+};
+
+static PSplit persistent_split_plan(int M, int N, int K, size_t ws_bytes, int cus) {
+    constexpr double kOverheadSteps = 3.0;
+    const double red_steps_per_byte = 2.0 / 10e6;
+    const int nk = (K + kPKB - 1) / kPKB;
+    const int64_t tiles = (int64_t)((M + kPBM - 1) / kPBM) * ((N + kPBN - 1) / kPBN);
+    PSplit best{1, nk};
+    double best_cost = (double)((tiles + cus - 1) / cus) * (nk + kOverheadSteps);
+    for (int s = 2; s <= 8; ++s) {
+        const int span = (nk + s - 1) / s;
+        if (span < 4) break;
+        const int se = (nk + span - 1) / span;
+        if ((size_t)se * M * N * sizeof(float) > ws_bytes) break;
+        const double rounds = (double)((tiles * se + cus - 1) / cus);
+        const double cost =
+            rounds * (span + kOverheadSteps) + (double)(se + 1) * M * N * sizeof(float) * red_steps_per_byte;
+        if (cost < best_cost * 0.97) {
+            best_cost = cost;
+            best = PSplit{se, span};
+        }
+    }
+    return best;
 }
 
 template <int FA, int FB, typename OutT, typename BiasT>
@@ -930,8 +983,27 @@ static void launch_persistent(const GemmArgs& g, int grid) {
 
 template <int FA, int FB, typename OutT, typename BiasT>
 static void launch_shape(const GemmArgs& g) {
-    if (const int grid = persistent_grid<BiasT>(g)) {
-        launch_persistent<FA, FB, OutT, BiasT>(g, grid);
+    const int cus = device_cu_count();
+    if (cus > 0 && persistent_ok(g)) {
+        const int64_t tiles = (int64_t)((g.M + kPBM - 1) / kPBM) * ((g.N + kPBN - 1) / kPBN);
+        if (tiles >= cus) {
+            launch_persistent<FA, FB, OutT, BiasT>(g, cus);
+            return;
+        }
+        const PSplit ps = persistent_split_plan(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0, cus);
+        if (ps.S == 1) {
+            launch_persistent<FA, FB, OutT, BiasT>(g, (int)tiles);
+            return;
+        }
+        const int grid = (int)std::min<int64_t>(tiles * ps.S, cus);
+        gemm_nt_persistent_kernel<FA, FB, float, BiasT, false, true><<<grid, 512, 0, g.st>>>(
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, g.ws, g.N, g.N % 4 == 0, ps.L, ps.S);
+        const int64_t total = (int64_t)g.M * g.N;
+        const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+        const bool vec_red = (g.N % 4 == 0) && ((int64_t)g.ldc * (int64_t)sizeof(OutT)) % 16 == 0 && aligned16(g.C);
+        splitk_reduce_kernel<OutT, BiasT><<<blocks, 256, 0, g.st>>>(g.ws, ps.S, g.M, g.N, g.sa, g.sb,
+                                                                    static_cast<const BiasT*>(g.bias),
+                                                                    static_cast<OutT*>(g.C), g.ldc, vec_red);
         return;
     }
     if (plan_gemm(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0).big)
@@ -958,8 +1030,20 @@ using namespace dfk;
 
 extern "C" size_t df_fp8_gemm_workspace_bytes(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const int S = plan_split(M, N, (K + 15) & ~15, SIZE_MAX);
-    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+    const int Kp = (K + 15) & ~15;
+    // the larger of the two plans' needs: the persistent split (when the
+    // operands fit its offsets) and the tiled kernels' split
+    const int S = plan_split(M, N, Kp, SIZE_MAX);
+    size_t need = S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+    const int cus = device_cu_count();
+    if (cus > 0) {
+        const int64_t tiles = (int64_t)((M + kPBM - 1) / kPBM) * ((N + kPBN - 1) / kPBN);
+        if (tiles < cus) {
+            const PSplit ps = persistent_split_plan(M, N, Kp, SIZE_MAX, cus);
+            if (ps.S > 1) need = std::max(need, (size_t)ps.S * (size_t)M * (size_t)N * sizeof(float));
+        }
+    }
+    return need;
 }
 
 extern "C" int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda, int fmt_b, const uint8_t* B,
