@@ -340,19 +340,39 @@ def measured_traffic(kernel_family):
 # MI355X, with TMPDIR=/tmp), and the directories they write.
 PROFILE_COMMANDS = {
     "stats": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_bench -o bench -- "
-              "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion --no-streaming"),
+              "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion --no-streaming "
+              "--no-optimizer --no-producer --no-delayed"),
     "fetch": ("timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_fetch -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
-              "--no-conversion --no-streaming --no-graph --copy-calibration"),
+              "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-graph "
+              "--copy-calibration"),
     "write": ("timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_write -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
-              "--no-conversion --no-streaming --no-graph --copy-calibration"),
+              "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-graph "
+              "--copy-calibration"),
+    "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
+                       "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
+                       "--no-producer --no-delayed"),
+    "stats_producer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_producer -o bench "
+                       "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
+                       "--no-optimizer --no-delayed"),
 }
+# extra kernel-stat summaries: (command key, csv directory, output file, title,
+# substrings that select the leg's own kernels)
+EXTRA_STATS = (
+    ("stats_consumer", "prof_consumer", "consumer_clip_adam_kernel_stats.md",
+     "clip + Adam over GPT-2 XL's 48 x 4 Linears (1.475 G fp32 parameters)",
+     ("adam_kernel", "sumsq_kernel", "clip_kernel", "norm_finalize_kernel")),
+    ("stats_producer", "prof_producer", "layernorm_quantize_kernel_stats.md",
+     "LayerNorm + e4m3 codes, 16384 x 1600 bf16 (unfused chain, fused, fused delayed)",
+     ("ln_stats_kernel", "true>(unsigned short const*", "amax_history_kernel")),
+)
 # GEMM families whose C-ABI call is exactly one kernel, by the persistent
-# kernel's template arguments: <A format, B format, output, bias type, bias>.
+# kernel's template arguments: <A format, B format, output, bias type, bias,
+# K-split>.
 TRAFFIC_FAMILIES = {
-    "gemm_fwd": ("gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true>",),
-    "gemm_dx": ("gemm_nt_persistent_kernel<1, 0, unsigned short, float, false>",),
+    "gemm_fwd": ("gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true, false>",),
+    "gemm_dx": ("gemm_nt_persistent_kernel<1, 0, unsigned short, float, false, false>",),
 }
 
 
@@ -440,7 +460,25 @@ def summarize_profiles():
         lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:.1f} | {write[k][0]:.1f} | {mb:.1f} |")
     with open(os.path.join(prof, "hbm_traffic_config4.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
-    print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)})")
+    extra = []
+    for key, sub, fname, title, keep in EXTRA_STATS:
+        path = os.path.join(out_dir, sub, "bench_kernel_stats.csv")
+        if not os.path.exists(path):
+            continue
+        with open(path) as fh:
+            rows_x = [r for r in csv.DictReader(fh) if any(k in r["Name"] for k in keep)]
+        lines = [f"# rocprofv3 kernel statistics -- {title}", "",
+                 "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS[key], "",
+                 "Only this leg's own kernels are listed (the config-4 step also runs in the same process).  "
+                 "Durations in microseconds.", "",
+                 "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+        for r in rows_x:
+            lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
+        with open(os.path.join(prof, fname), "w") as fh:
+            fh.write("\n".join(lines) + "\n")
+        extra.append(fname)
+    print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)}, extra {extra})")
 
 
 def conversion_bench(torch, df, synth, dev, stream, reps=10):

@@ -36,7 +36,6 @@
 #pragma clang fp contract(off)
 
 namespace dfk {
-namespace {
 
 constexpr int kOThreads = 256;
 constexpr int kVec = 8;                                        // float4 per thread per block
@@ -68,7 +67,7 @@ struct AdamHyper {
 };
 
 // tensor that owns block b: the last t with first[t] <= b
-__device__ __forceinline__ int owner(const int* first, int count, int b) {
+static __device__ __forceinline__ int owner(const int* first, int count, int b) {
     int lo = 0, hi = count - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -77,7 +76,7 @@ __device__ __forceinline__ int owner(const int* first, int count, int b) {
     return lo;
 }
 
-__device__ __forceinline__ double block_sum_f64(double s) {
+static __device__ __forceinline__ double block_sum_f64(double s) {
     __shared__ double red[kOThreads / 64];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
@@ -91,7 +90,7 @@ __device__ __forceinline__ double block_sum_f64(double s) {
     return s;  // valid in thread 0
 }
 
-__device__ __forceinline__ double sq(float x) { return (double)(x * x); }
+static __device__ __forceinline__ double sq(float x) { return (double)(x * x); }
 
 // Stage 1 of the norm: one binary64 partial per block of kNormSub chunks
 // (fewer partials for the single-block stage 2 to fold).
@@ -178,7 +177,7 @@ __global__ __launch_bounds__(kOThreads) void clip_kernel(const NormList L, const
 //   m_hat = m / (1 - b1^t);  v_hat = v / (1 - b2^t);
 //   p = p - lr * m_hat / (sqrt(v_hat) + eps)
 // with grad first multiplied by the clip factor f (1 when not clipping).
-__device__ __forceinline__ void adam1(float& p, float gr, float& m, float& v, const AdamHyper& h, float f) {
+static __device__ __forceinline__ void adam1(float& p, float gr, float& m, float& v, const AdamHyper& h, float f) {
     const float g = gr * f + h.wd * p;
     m = h.b1 * m + h.omb1 * g;
     v = h.b2 * v + h.omb2 * g * g;
@@ -246,11 +245,11 @@ __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const
     }
 }
 
-int64_t chunks(int64_t n) { return (n + kChunk - 1) / kChunk; }
-int64_t norm_chunks(int64_t n) { return (n + kNormChunk - 1) / kNormChunk; }
+static int64_t chunks(int64_t n) { return (n + kChunk - 1) / kChunk; }
+static int64_t norm_chunks(int64_t n) { return (n + kNormChunk - 1) / kNormChunk; }
 
 // Blocks of a whole list, or -1 when a launch would exceed the grid limit.
-int64_t total_blocks(const int64_t* sizes, int count) {
+static int64_t total_blocks(const int64_t* sizes, int count) {
     int64_t b = 0;
     for (int i = 0; i < count; ++i) b += chunks(sizes[i]);
     return b;
@@ -258,7 +257,7 @@ int64_t total_blocks(const int64_t* sizes, int count) {
 
 // Shared argument checks of a tensor list: non-null pointers, sizes >= 0,
 // 16-byte aligned pointers (the float4 path).
-int check_list(const char* fn, const void* const* ptrs, const int64_t* sizes, int count, const char* what) {
+static int check_list(const char* fn, const void* const* ptrs, const int64_t* sizes, int count, const char* what) {
     for (int i = 0; i < count; ++i) {
         DF_CHECK(sizes[i] >= 0, DF_ERR_INVALID, "%s: %s size[%d] = %lld is negative", fn, what, i,
                  (long long)sizes[i]);
@@ -271,7 +270,7 @@ int check_list(const char* fn, const void* const* ptrs, const int64_t* sizes, in
 
 // Launches sumsq_kernel over the list in groups of kNormList tensors; the
 // partials of all groups land back to back in `partial`.
-int launch_sumsq(const float* const* grads, const int64_t* sizes, int count, double* partial,
+static int launch_sumsq(const float* const* grads, const int64_t* sizes, int count, double* partial,
                  hipStream_t st, int* nparts) {
     int parts = 0;
     for (int i0 = 0; i0 < count;) {
@@ -296,7 +295,6 @@ int launch_sumsq(const float* const* grads, const int64_t* sizes, int count, dou
     return launch_status("sumsq_kernel");
 }
 
-}  // namespace
 }  // namespace dfk
 
 using namespace dfk;

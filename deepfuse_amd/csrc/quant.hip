@@ -47,28 +47,37 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t m) {
     return m;  // valid in thread 0
 }
 
-// Stage 1, fp32: 16-byte loads, four in flight per thread per iteration.
+// Streaming layout shared by the flat kernels: the vector index space (16
+// bytes of input per vector) is cut into chunks of kThreads * kU vectors;
+// block b takes chunks b, b + G, ... and each thread issues kU 16-byte
+// loads, kThreads apart, before using any of them (a wave instruction
+// covers 1 KiB contiguous).  Only the last, partial chunk takes the
+// element-guarded loop.
+constexpr int kU = 8;
+constexpr int64_t kChunkVec = (int64_t)kThreads * kU;
+
+// Stage 1, fp32: one partial maximum per block.
 __global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __restrict__ x,
                                                                int64_t n,
                                                                uint32_t* __restrict__ partial) {
     uint32_t m = 0;
     const int64_t nvec = n >> 2;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + 3 * stride < nvec; i += 4 * stride) {
-        u32x4 v0 = __builtin_nontemporal_load(xv + i);
-        u32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
-        u32x4 v2 = __builtin_nontemporal_load(xv + i + 2 * stride);
-        u32x4 v3 = __builtin_nontemporal_load(xv + i + 3 * stride);
-        m = fold_f32(m, v0.x); m = fold_f32(m, v0.y); m = fold_f32(m, v0.z); m = fold_f32(m, v0.w);
-        m = fold_f32(m, v1.x); m = fold_f32(m, v1.y); m = fold_f32(m, v1.z); m = fold_f32(m, v1.w);
-        m = fold_f32(m, v2.x); m = fold_f32(m, v2.y); m = fold_f32(m, v2.z); m = fold_f32(m, v2.w);
-        m = fold_f32(m, v3.x); m = fold_f32(m, v3.y); m = fold_f32(m, v3.z); m = fold_f32(m, v3.w);
-    }
-    for (; i < nvec; i += stride) {
-        u32x4 v = xv[i];
-        m = fold_f32(m, v.x); m = fold_f32(m, v.y); m = fold_f32(m, v.z); m = fold_f32(m, v.w);
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            u32x4 v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                m = fold_f32(m, v[u].x); m = fold_f32(m, v[u].y); m = fold_f32(m, v[u].z); m = fold_f32(m, v[u].w);
+            }
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
+                const u32x4 v = xv[i];
+                m = fold_f32(m, v.x); m = fold_f32(m, v.y); m = fold_f32(m, v.z); m = fold_f32(m, v.w);
+            }
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3))
         m = fold_f32(m, __float_as_uint(x[(nvec << 2) + threadIdx.x]));
@@ -83,21 +92,22 @@ __global__ __launch_bounds__(kThreads) void absmax_bf16_stage1(const uint16_t* _
     uint32_t m = 0;
     const int64_t nvec = n >> 3;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + 3 * stride < nvec; i += 4 * stride) {
-        u32x4 v0 = __builtin_nontemporal_load(xv + i);
-        u32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
-        u32x4 v2 = __builtin_nontemporal_load(xv + i + 2 * stride);
-        u32x4 v3 = __builtin_nontemporal_load(xv + i + 3 * stride);
-        m = fold_bf16x2(m, v0.x); m = fold_bf16x2(m, v0.y); m = fold_bf16x2(m, v0.z); m = fold_bf16x2(m, v0.w);
-        m = fold_bf16x2(m, v1.x); m = fold_bf16x2(m, v1.y); m = fold_bf16x2(m, v1.z); m = fold_bf16x2(m, v1.w);
-        m = fold_bf16x2(m, v2.x); m = fold_bf16x2(m, v2.y); m = fold_bf16x2(m, v2.z); m = fold_bf16x2(m, v2.w);
-        m = fold_bf16x2(m, v3.x); m = fold_bf16x2(m, v3.y); m = fold_bf16x2(m, v3.z); m = fold_bf16x2(m, v3.w);
-    }
-    for (; i < nvec; i += stride) {
-        u32x4 v = xv[i];
-        m = fold_bf16x2(m, v.x); m = fold_bf16x2(m, v.y); m = fold_bf16x2(m, v.z); m = fold_bf16x2(m, v.w);
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            u32x4 v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                m = fold_bf16x2(m, v[u].x); m = fold_bf16x2(m, v[u].y);
+                m = fold_bf16x2(m, v[u].z); m = fold_bf16x2(m, v[u].w);
+            }
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
+                const u32x4 v = xv[i];
+                m = fold_bf16x2(m, v.x); m = fold_bf16x2(m, v.y); m = fold_bf16x2(m, v.z); m = fold_bf16x2(m, v.w);
+            }
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 7))
         m = fold_f32(m, (uint32_t)x[(nvec << 3) + threadIdx.x] << 16);
@@ -137,7 +147,7 @@ __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* _
 // x / s (correctly rounded: qdiv, contract D1), then the fp8 encoder
 // (encode2_hw: hardware round-to-nearest-even after saturation, NaN kept).
 
-// fp32 -> fp8: one 16-byte load -> one 4-byte store per thread per step.
+// fp32 -> fp8: a 16-byte load of 4 values -> a 4-byte store of 4 codes.
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __restrict__ x,
                                                                  int64_t n,
@@ -147,21 +157,21 @@ __global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __r
     const int64_t nvec = n >> 2;
     const f32x4* xv = reinterpret_cast<const f32x4*>(x);
     uint32_t* qv = reinterpret_cast<uint32_t*>(q);
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + 3 * stride < nvec; i += 4 * stride) {
-        const f32x4 v0 = __builtin_nontemporal_load(xv + i);
-        const f32x4 v1 = __builtin_nontemporal_load(xv + i + stride);
-        const f32x4 v2 = __builtin_nontemporal_load(xv + i + 2 * stride);
-        const f32x4 v3 = __builtin_nontemporal_load(xv + i + 3 * stride);
-        __builtin_nontemporal_store(quant4_fast<FMT>(v0.x, v0.y, v0.z, v0.w, d), qv + i);
-        __builtin_nontemporal_store(quant4_fast<FMT>(v1.x, v1.y, v1.z, v1.w, d), qv + i + stride);
-        __builtin_nontemporal_store(quant4_fast<FMT>(v2.x, v2.y, v2.z, v2.w, d), qv + i + 2 * stride);
-        __builtin_nontemporal_store(quant4_fast<FMT>(v3.x, v3.y, v3.z, v3.w, d), qv + i + 3 * stride);
-    }
-    for (; i < nvec; i += stride) {
-        const f32x4 v = xv[i];
-        qv[i] = quant4_fast<FMT>(v.x, v.y, v.z, v.w, d);
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            f32x4 v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                __builtin_nontemporal_store(quant4_fast<FMT>(v[u].x, v[u].y, v[u].z, v[u].w, d),
+                                            qv + base + u * kThreads + threadIdx.x);
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
+                const f32x4 v = xv[i];
+                qv[i] = quant4_fast<FMT>(v.x, v.y, v.z, v.w, d);
+            }
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const int64_t j = (nvec << 2) + threadIdx.x;
@@ -185,26 +195,27 @@ __global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t*
     const int64_t nvec = n >> 3;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
     u32x2* qv = reinterpret_cast<u32x2*>(q);
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i + 3 * stride < nvec; i += 4 * stride) {
-        u32x4 v[4];
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            u32x4 v[kU];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(xv + i + u * stride);
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            u32x2 o;
-            o.x = quant_bf16x4<FMT>(v[u].x, v[u].y, d);
-            o.y = quant_bf16x4<FMT>(v[u].z, v[u].w, d);
-            __builtin_nontemporal_store(o, qv + i + u * stride);
+            for (int u = 0; u < kU; ++u) {
+                u32x2 o;
+                o.x = quant_bf16x4<FMT>(v[u].x, v[u].y, d);
+                o.y = quant_bf16x4<FMT>(v[u].z, v[u].w, d);
+                __builtin_nontemporal_store(o, qv + base + u * kThreads + threadIdx.x);
+            }
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
+                const u32x4 v = xv[i];
+                u32x2 o;
+                o.x = quant_bf16x4<FMT>(v.x, v.y, d);
+                o.y = quant_bf16x4<FMT>(v.z, v.w, d);
+                qv[i] = o;
+            }
         }
-    }
-    for (; i < nvec; i += stride) {
-        const u32x4 v = xv[i];
-        u32x2 o;
-        o.x = quant_bf16x4<FMT>(v.x, v.y, d);
-        o.y = quant_bf16x4<FMT>(v.z, v.w, d);
-        qv[i] = o;
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t j = (nvec << 3) + threadIdx.x;
@@ -213,7 +224,8 @@ __global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t*
 }
 
 // -------------------------------------------------------------- dequantize --
-// fp8 -> fp32: one 4-byte load (4 codes) -> one 16-byte store.
+// fp8 -> fp32: a 4-byte load (4 codes) -> a 16-byte store; the chunks count
+// output vectors.
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void dequantize_f32_kernel(const uint8_t* __restrict__ q,
                                                                    int64_t n,
@@ -223,15 +235,24 @@ __global__ __launch_bounds__(kThreads) void dequantize_f32_kernel(const uint8_t*
     const int64_t nvec = n >> 2;
     const uint32_t* qv = reinterpret_cast<const uint32_t*>(q);
     f32x4* ov = reinterpret_cast<f32x4*>(out);
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
-        const uint32_t w = __builtin_nontemporal_load(qv + i);
+    auto deq4 = [&](uint32_t w) {
         f32x4 o;
         o.x = dequant_fp8<FMT>(w & 0xFFu, s);
         o.y = dequant_fp8<FMT>((w >> 8) & 0xFFu, s);
         o.z = dequant_fp8<FMT>((w >> 16) & 0xFFu, s);
         o.w = dequant_fp8<FMT>(w >> 24, s);
-        __builtin_nontemporal_store(o, ov + i);
+        return o;
+    };
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            uint32_t w[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(deq4(w[u]), ov + base + u * kThreads + threadIdx.x);
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) ov[i] = deq4(qv[i]);
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const int64_t j = (nvec << 2) + threadIdx.x;
@@ -254,15 +275,24 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
     const int64_t nvec = n >> 3;
     const u32x2* qv = reinterpret_cast<const u32x2*>(q);
     u32x4* ov = reinterpret_cast<u32x4*>(out);
-    const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
-        const u32x2 w = __builtin_nontemporal_load(qv + i);
+    auto deq8 = [&](u32x2 w) {
         u32x4 o;
         o.x = deq_bf16x2<FMT>(w.x & 0xFFu, (w.x >> 8) & 0xFFu, s);
         o.y = deq_bf16x2<FMT>((w.x >> 16) & 0xFFu, w.x >> 24, s);
         o.z = deq_bf16x2<FMT>(w.y & 0xFFu, (w.y >> 8) & 0xFFu, s);
         o.w = deq_bf16x2<FMT>((w.y >> 16) & 0xFFu, w.y >> 24, s);
-        __builtin_nontemporal_store(o, ov + i);
+        return o;
+    };
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            u32x2 w[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(deq8(w[u]), ov + base + u * kThreads + threadIdx.x);
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) ov[i] = deq8(qv[i]);
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t j = (nvec << 3) + threadIdx.x;
@@ -728,7 +758,7 @@ static int absmax_impl(int in_dtype, const void* x, int64_t n, int fmt, float* a
     hipStream_t st = as_stream(stream);
     uint32_t* part = static_cast<uint32_t*>(ws);
     const int per = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 8;
-    int blocks = grid_for((n / per + 3) / 4, kMaxReduceBlocks);
+    int blocks = grid_for((n / per + kU - 1) / kU, kMaxReduceBlocks);
     if (in_dtype == DF_DTYPE_FLOAT32)
         absmax_f32_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), n, part);
     else if (in_dtype == DF_DTYPE_BFLOAT16)
@@ -774,7 +804,7 @@ static int quantize_f32_impl(const float* x, int64_t n, const float* scale, uint
     if (n == 0) return DF_OK;
     DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned16(x) && aligned4(q), DF_ERR_ALIGN, "%s: x must be 16-byte and q 4-byte aligned", name);
-    const int blocks = grid_for(n / 4 + 1, kStreamBlocks);
+    const int blocks = grid_for((n / 4 + 1 + kU - 1) / kU, kStreamBlocks);
     quantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
     return launch_status(name);
 }
@@ -788,7 +818,7 @@ static int quantize_bf16_impl(const uint16_t* x, int64_t n, const float* scale, 
     DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned16(x) && (((uintptr_t)q & 7u) == 0), DF_ERR_ALIGN,
              "%s: x must be 16-byte and q 8-byte aligned", name);
-    const int blocks = grid_for(n / 8 + 1, kStreamBlocks);
+    const int blocks = grid_for((n / 8 + 1 + kU - 1) / kU, kStreamBlocks);
     quantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
     return launch_status(name);
 }
@@ -815,7 +845,7 @@ static int dequantize_f32_impl(const uint8_t* q, int64_t n, const float* scale, 
     DF_CHECK(q && scale && out, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned4(q) && aligned16(out), DF_ERR_ALIGN, "%s: q must be 4-byte and out 16-byte aligned",
              name);
-    const int blocks = grid_for(n / 4 + 1, kStreamBlocks);
+    const int blocks = grid_for((n / 4 + 1 + kU - 1) / kU, kStreamBlocks);
     dequantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
     return launch_status(name);
 }
@@ -829,7 +859,7 @@ static int dequantize_bf16_impl(const uint8_t* q, int64_t n, const float* scale,
     DF_CHECK(q && scale && out, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK((((uintptr_t)q & 7u) == 0) && aligned16(out), DF_ERR_ALIGN,
              "%s: q must be 8-byte and out 16-byte aligned", name);
-    const int blocks = grid_for(n / 8 + 1, kStreamBlocks);
+    const int blocks = grid_for((n / 8 + 1 + kU - 1) / kU, kStreamBlocks);
     dequantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
     return launch_status(name);
 }
