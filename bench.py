@@ -59,6 +59,8 @@ def parse():
     p.add_argument("--no-optimizer", action="store_true", help="skip the clip + Adam leg")
     p.add_argument("--no-delayed", action="store_true", help="skip the delayed-scaling step leg")
     p.add_argument("--no-producer", action="store_true", help="skip the LayerNorm + quantize leg")
+    p.add_argument("--vendor-compare", action="store_true",
+                   help="also time the 12 GEMM shapes on torch._scaled_mm (hipBLASLt) for comparison")
     p.add_argument("--history", type=int, default=16, help="amax history length of the delayed-scaling leg")
     p.add_argument("--stream-layers", type=int, default=48)
     p.add_argument("--stream-slots", type=int, default=4)
@@ -311,6 +313,8 @@ def main():
         out["delayed_scaling"] = delayed
     if not args.no_conversion:
         out["conversion"] = conversion_bench(torch, df, synth, dev, cur())
+    if args.vendor_compare:
+        out["vendor_compare"] = vendor_bench(torch, df, dev, cur())
     if not args.no_producer:
         out["producer"] = producer_bench(torch, df, synth, dev, cur())
     if not args.no_optimizer:
@@ -604,6 +608,68 @@ def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit
     return {"history": H, "steps": 2 * reps, "ms_per_step": round(ms, 4),
             "tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
             "speedup_vs_just_in_time": round(jit_ms / ms, 4)}
+
+
+def vendor_bench(torch, df, dev, stream, M=16384, reps=10):
+    """The 12 config-4 GEMM shapes on the vendor fp8 GEMM (hipBLASLt through
+    torch._scaled_mm, OCP fp8, bf16 output) next to this library's GEMM on
+    the same operands: a comparison, not part of the product path.  Each
+    shape is C[m,n] = sum_k A[m,k] B[n,k] with A in e4m3 (forward) or e5m2
+    (backward) and B in e4m3."""
+    from deepfuse_amd import DType, Fmt
+    shapes = []
+    for _, K, N in XL_LINEARS:
+        shapes += [("fwd", M, N, K, Fmt.E4M3), ("dx", M, K, N, Fmt.E5M2), ("dw", N, K, M, Fmt.E5M2)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    one = torch.ones(1, dtype=torch.float32, device=dev)
+    tdt = {Fmt.E4M3: torch.float8_e4m3fn, Fmt.E5M2: torch.float8_e5m2}
+    res = {"shapes": len(shapes)}
+    tot_flop = tot_ours = tot_vendor = 0.0
+    errors = []
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    for fam, m, n, k, fa in shapes:
+        a = (torch.randn(m, k, device=dev, generator=gen) * 4).to(tdt[fa])
+        b = (torch.randn(n, k, device=dev, generator=gen) * 4).to(torch.float8_e4m3fn)
+        c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        wsb = df.lib().df_fp8_gemm_workspace_bytes(m, n, k)
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+        ours = lambda: df.call("df_fp8_gemm_nt", int(fa), a.data_ptr(), k, int(Fmt.E4M3), b.data_ptr(), k, m, n, k,
+                               one.data_ptr(), one.data_ptr(), int(DType.BFLOAT16), None, int(DType.BFLOAT16),
+                               c.data_ptr(), n, ws.data_ptr(), wsb, stream)
+        vendor = lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+        flop = 2.0 * m * n * k
+        t_ours = timed(ours)
+        try:
+            t_vendor = timed(vendor)
+        except Exception as exc:  # the vendor path may refuse a format pair
+            errors.append(f"{fam} {m}x{n}x{k}: {type(exc).__name__}")
+            t_vendor = None
+        tot_flop += flop
+        tot_ours += t_ours
+        if t_vendor is not None:
+            tot_vendor += t_vendor
+        del a, b, c, ws
+    res["ours_tflops"] = round(tot_flop / (tot_ours * 1e-3) / 1e12, 1)
+    if not errors:
+        res["vendor_tflops"] = round(tot_flop / (tot_vendor * 1e-3) / 1e12, 1)
+        res["ratio"] = round(tot_vendor / tot_ours, 3)
+    res["vendor"] = "torch._scaled_mm (hipBLASLt), bf16 output, unit scales"
+    if errors:
+        res["vendor_errors"] = errors
+    torch.cuda.empty_cache()
+    return res
 
 
 def producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10):
