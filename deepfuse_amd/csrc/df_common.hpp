@@ -93,14 +93,21 @@ __device__ __forceinline__ QDiv make_qdiv(float s) {
     return d;
 }
 
-__device__ __forceinline__ float qdiv(float x, const QDiv& d) {
-    if (!d.fast) return x / d.s;
+// FAST selects the form at compile time: kernels test d.fast once and run a
+// loop instantiated for it, so no per-element branch splits their code.
+template <bool FAST>
+__device__ __forceinline__ float qdiv_t(float x, const QDiv& d) {
+    if (!FAST) return x / d.s;
     const float y0 = x * d.r;
     const float e0 = __builtin_fmaf(-d.s, y0, x);
     const float y1 = __builtin_fmaf(e0, d.r, y0);
     const float e1 = __builtin_fmaf(-d.s, y1, x);
     const float q = __builtin_copysignf(__builtin_fmaf(e1, d.r, y1), x);
     return __builtin_fabsf(x) <= 0x1p60f ? q : x;  // NaN and huge inputs pass through
+}
+
+__device__ __forceinline__ float qdiv(float x, const QDiv& d) {
+    return d.fast ? qdiv_t<true>(x, d) : qdiv_t<false>(x, d);
 }
 
 // Two values -> two fp8 codes with the hardware converter
@@ -122,9 +129,10 @@ __device__ __forceinline__ uint32_t encode2_hw(float a, float b) {
 }
 
 // four elements x / s -> four packed codes (byte i = element i)
-template <int FMT>
-__device__ __forceinline__ uint32_t quant4_fast(float a, float b, float c, float d, const QDiv& q) {
-    return encode2_hw<FMT>(qdiv(a, q), qdiv(b, q)) | (encode2_hw<FMT>(qdiv(c, q), qdiv(d, q)) << 16);
+template <int FMT, bool FAST>
+__device__ __forceinline__ uint32_t quant4_t(float a, float b, float c, float d, const QDiv& q) {
+    return encode2_hw<FMT>(qdiv_t<FAST>(a, q), qdiv_t<FAST>(b, q)) |
+           (encode2_hw<FMT>(qdiv_t<FAST>(c, q), qdiv_t<FAST>(d, q)) << 16);
 }
 
 // ----------------------------------------------------------------- decode --

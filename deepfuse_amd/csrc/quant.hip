@@ -148,12 +148,9 @@ __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* _
 // (encode2_hw: hardware round-to-nearest-even after saturation, NaN kept).
 
 // fp32 -> fp8: a 16-byte load of 4 values -> a 4-byte store of 4 codes.
-template <int FMT>
-__global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __restrict__ x,
-                                                                 int64_t n,
-                                                                 const float* __restrict__ scale,
-                                                                 uint8_t* __restrict__ q) {
-    const QDiv d = make_qdiv(scale[0]);
+template <int FMT, bool FAST>
+__device__ __forceinline__ void quantize_f32_body(const float* __restrict__ x, int64_t n, const QDiv& d,
+                                                  uint8_t* __restrict__ q) {
     const int64_t nvec = n >> 2;
     const f32x4* xv = reinterpret_cast<const f32x4*>(x);
     uint32_t* qv = reinterpret_cast<uint32_t*>(q);
@@ -164,34 +161,43 @@ __global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __r
             for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
 #pragma unroll
             for (int u = 0; u < kU; ++u)
-                __builtin_nontemporal_store(quant4_fast<FMT>(v[u].x, v[u].y, v[u].z, v[u].w, d),
+                __builtin_nontemporal_store(quant4_t<FMT, FAST>(v[u].x, v[u].y, v[u].z, v[u].w, d),
                                             qv + base + u * kThreads + threadIdx.x);
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
                 const f32x4 v = xv[i];
-                qv[i] = quant4_fast<FMT>(v.x, v.y, v.z, v.w, d);
+                qv[i] = quant4_t<FMT, FAST>(v.x, v.y, v.z, v.w, d);
             }
         }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const int64_t j = (nvec << 2) + threadIdx.x;
-        q[j] = (uint8_t)encode2_hw<FMT>(qdiv(x[j], d), 0.0f);
+        q[j] = (uint8_t)encode2_hw<FMT>(qdiv_t<FAST>(x[j], d), 0.0f);
     }
 }
 
-// bf16 -> fp8: one 16-byte load (8 values) -> one 8-byte store.
 template <int FMT>
-__device__ __forceinline__ uint32_t quant_bf16x4(uint32_t w0, uint32_t w1, const QDiv& d) {
-    return quant4_fast<FMT>(bf16_to_f32(w0 & 0xFFFFu), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xFFFFu),
-                            bf16_to_f32(w1 >> 16), d);
+__global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __restrict__ x,
+                                                                 int64_t n,
+                                                                 const float* __restrict__ scale,
+                                                                 uint8_t* __restrict__ q) {
+    const QDiv d = make_qdiv(scale[0]);
+    if (d.fast)
+        quantize_f32_body<FMT, true>(x, n, d, q);
+    else
+        quantize_f32_body<FMT, false>(x, n, d, q);
 }
 
-template <int FMT>
-__global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t* __restrict__ x,
-                                                                  int64_t n,
-                                                                  const float* __restrict__ scale,
-                                                                  uint8_t* __restrict__ q) {
-    const QDiv d = make_qdiv(scale[0]);
+// bf16 -> fp8: one 16-byte load (8 values) -> one 8-byte store.
+template <int FMT, bool FAST>
+__device__ __forceinline__ uint32_t quant_bf16x4(uint32_t w0, uint32_t w1, const QDiv& d) {
+    return quant4_t<FMT, FAST>(bf16_to_f32(w0 & 0xFFFFu), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xFFFFu),
+                               bf16_to_f32(w1 >> 16), d);
+}
+
+template <int FMT, bool FAST>
+__device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ x, int64_t n, const QDiv& d,
+                                                   uint8_t* __restrict__ q) {
     const int64_t nvec = n >> 3;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
     u32x2* qv = reinterpret_cast<u32x2*>(q);
@@ -203,24 +209,36 @@ __global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t*
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
                 u32x2 o;
-                o.x = quant_bf16x4<FMT>(v[u].x, v[u].y, d);
-                o.y = quant_bf16x4<FMT>(v[u].z, v[u].w, d);
+                o.x = quant_bf16x4<FMT, FAST>(v[u].x, v[u].y, d);
+                o.y = quant_bf16x4<FMT, FAST>(v[u].z, v[u].w, d);
                 __builtin_nontemporal_store(o, qv + base + u * kThreads + threadIdx.x);
             }
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
                 const u32x4 v = xv[i];
                 u32x2 o;
-                o.x = quant_bf16x4<FMT>(v.x, v.y, d);
-                o.y = quant_bf16x4<FMT>(v.z, v.w, d);
+                o.x = quant_bf16x4<FMT, FAST>(v.x, v.y, d);
+                o.y = quant_bf16x4<FMT, FAST>(v.z, v.w, d);
                 qv[i] = o;
             }
         }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
         const int64_t j = (nvec << 3) + threadIdx.x;
-        q[j] = (uint8_t)encode2_hw<FMT>(qdiv(bf16_to_f32(x[j]), d), 0.0f);
+        q[j] = (uint8_t)encode2_hw<FMT>(qdiv_t<FAST>(bf16_to_f32(x[j]), d), 0.0f);
     }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t* __restrict__ x,
+                                                                  int64_t n,
+                                                                  const float* __restrict__ scale,
+                                                                  uint8_t* __restrict__ q) {
+    const QDiv d = make_qdiv(scale[0]);
+    if (d.fast)
+        quantize_bf16_body<FMT, true>(x, n, d, q);
+    else
+        quantize_bf16_body<FMT, false>(x, n, d, q);
 }
 
 // -------------------------------------------------------------- dequantize --
@@ -394,24 +412,18 @@ __device__ __forceinline__ float ln_apply(float x, float mean, float rstd, bool 
 // loaded x becomes ln_apply(x, row stats, column gamma/beta), written to
 // ln.y when given, and those values are what the codes, column sums and
 // absmax see.
-template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false, bool LN = false>
-__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
-                                                                int cols, int ldx, bool vec_ok,
-                                                                const float* __restrict__ scale,
-                                                                uint8_t* __restrict__ q, int ldq,
-                                                                uint8_t* __restrict__ qt, int ldqt,
-                                                                float* __restrict__ colpart,
-                                                                uint32_t* __restrict__ amaxpart = nullptr,
-                                                                LnArgs ln = LnArgs()) {
+// The tile pass proper, instantiated for both division forms (FAST: see
+// qdiv_t); the kernel below owns the LDS and picks the form once per block.
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bool FAST>
+__device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, int cols, int ldx, bool vec_ok,
+                                         const QDiv& d, uint8_t* __restrict__ q, int ldq, uint8_t* __restrict__ qt,
+                                         int ldqt, float* __restrict__ colpart, uint32_t* __restrict__ amaxpart,
+                                         const LnArgs& ln, uint8_t* tile, float (*csum)[kT2]) {
     constexpr int E = Ld<InT>::E;      // elements per 16-byte load
     constexpr int TPR = kT2 / E;       // threads per tile row
     constexpr int RG = kThreads / TPR; // row groups
     constexpr int RPT = kT2 / RG;      // rows per thread (8 for bf16, 16 for fp32)
     constexpr int TSTRIDE = kT2 + 16;  // LDS tile row (bytes), [column][row]
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * TSTRIDE];
-    __shared__ float csum[COLSUM ? RG : 1][kT2];
-
-    const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
     const int r0 = blockIdx.y * kT2, c0 = blockIdx.x * kT2;
     const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
     const int c = c0 + tc;
@@ -461,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
         if (!CODES) return;
 #pragma unroll
         for (int g = 0; g < E / 4; ++g)
-            codes[rr][g] = quant4_fast<FMT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
+            codes[rr][g] = quant4_t<FMT, FAST>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
         if (q && r < rows && c < ldq) {
             if (E == 8)
                 *reinterpret_cast<u32x2*>(q + (int64_t)r * ldq + c) = u32x2{codes[rr][0], codes[rr][E / 4 - 1]};
@@ -698,6 +710,28 @@ __global__ __launch_bounds__(kThreads) void amax_history_init_kernel(const float
     const float v = (a > 0.0f && a <= 3.4028234663852886e38f) ? a : 0.0f;
     for (int i = threadIdx.x; i < len; i += kThreads) history[i] = v;
     if (threadIdx.x == 0) scale_out[0] = scale_from_absmax(v, fmt);
+}
+
+
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false, bool LN = false>
+__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
+                                                                int cols, int ldx, bool vec_ok,
+                                                                const float* __restrict__ scale,
+                                                                uint8_t* __restrict__ q, int ldq,
+                                                                uint8_t* __restrict__ qt, int ldqt,
+                                                                float* __restrict__ colpart,
+                                                                uint32_t* __restrict__ amaxpart = nullptr,
+                                                                LnArgs ln = LnArgs()) {
+    constexpr int RG = kThreads / (kT2 / Ld<InT>::E);
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2 + 16)];
+    __shared__ float csum[COLSUM ? RG : 1][kT2];
+    const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
+    if (!CODES || d.fast)
+        q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, true>(x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart,
+                                                          amaxpart, ln, tile, csum);
+    else
+        q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, false>(x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart,
+                                                           amaxpart, ln, tile, csum);
 }
 
 // out[c] = sum over tile rows of colpart[t][c].  A block owns 64 columns;
