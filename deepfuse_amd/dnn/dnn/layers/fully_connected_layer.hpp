@@ -13,7 +13,10 @@
 // backward quantizes dY to e5m2 (its column sums give grad_bias in the same
 // pass), dX = dYq . W * sdy * sw, dW = dYq^T . X * sdy * sx, all with fp32
 // accumulation.  Instead of a full clone of the input, training caches the
-// transposed e4m3 codes of X (one byte per element) and their scale.
+// transposed e4m3 codes of X (one byte per element) and their scale, and the
+// forward's pass over W also writes W's transposed codes for the backward:
+// backward uses the weights its forward used (the reference re-reads
+// weights_, which is the same unless they are changed in between).
 // TT: float or bfloat16.
 #pragma once
 
@@ -98,6 +101,7 @@ private:
     int cached_n_ = -1;                        // tokens of the cached forward
     std::optional<tensor<fp8_e4m3>> xt_cache_;  // X^T codes [in, round16(N)] + scale
     Scratch absmax_ws_, colsum_ws_, gemm_ws_, codes_a_, codes_b_, codes_c_, scales_, colsum_;
+    Scratch codes_wt_;  // W^T codes [in, round16(out)] from the training forward, read by backward
     int history_len_ = 0;
     Delayed dx_, dw_, ddy_;
     const float* sx_used_ = nullptr;  // delayed: scales of the cached forward's X and W codes

@@ -226,15 +226,20 @@ tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerN
     }
     const float* sx = quantize_input(input, N, norm, xq, Kp, xt, Np, sx_jit);
     uint8_t* wq = codes_b_.get((size_t)out_features_ * Kp);
+    // in training, the same pass also writes W's transposed codes for the
+    // backward's dX GEMM (the weights cannot change before the backward that
+    // follows): one read of W per step instead of two, and no second absmax
+    const int Op = round16(out_features_);
+    uint8_t* wt = this->training_enabled_ ? codes_wt_.get((size_t)in_features_ * Op) : nullptr;
     const float* sw = sc + 1;
     if (history_len_ > 0) {
-        sw = quantize_delayed(dw_, this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, wq, Kp, nullptr,
-                              0, nullptr);
+        sw = quantize_delayed(dw_, this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, wq, Kp, wt,
+                              wt ? Op : 0, nullptr);
         sx_used_ = sx;
         sw_used_ = sw;
     } else {
-        quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, wq, Kp, nullptr, 0,
-                         nullptr);
+        quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, wq, Kp, wt,
+                         wt ? Op : 0, nullptr);
         sx_used_ = sw_used_ = nullptr;
     }
     const size_t gb = df_fp8_gemm_workspace_bytes(N, out_features_, in_features_);
@@ -262,23 +267,17 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
     uint8_t* dyq = codes_a_.get((size_t)N * Op);
     uint8_t* dyt = codes_c_.get((size_t)out_features_ * Np);
     float* db = reinterpret_cast<float*>(colsum_.get((size_t)out_features_ * sizeof(float)));
-    uint8_t* wt = codes_b_.get((size_t)in_features_ * Op);
+    // W^T codes and their scale: written by the forward's W pass
+    const uint8_t* wt = codes_wt_.p;
     const float* sdy = sc + 2;
     const float* sw = sc + 1;
     const float* sx = xt_cache_->scale_data();
     if (history_len_ > 0 && sx_used_) {
         sdy = quantize_delayed(ddy_, grad_output.data(), N, out_features_, DF_FMT_E5M2, dyq, Op, dyt, Np, db);
-        // W has not changed since the forward: its transposed codes at the
-        // forward's scale, no absmax pass
-        CHECK_DF_EX(df_quantize_2d(dt, this->weights_.data(), out_features_, in_features_, in_features_, DF_FMT_E4M3,
-                                   sw_used_, nullptr, 0, wt, Op, st()));
         sw = sw_used_;
         sx = sx_used_;
     } else {
         quantize_operand(grad_output.data(), N, out_features_, DF_FMT_E5M2, sc + 2, dyq, Op, dyt, Np, db);
-        // the current weights (reference: backward reads weights_), transposed
-        quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, nullptr, 0, wt, Op,
-                         nullptr);
     }
     tensor<TT> grad_input({N, in_features_});
     const size_t gb = std::max(df_fp8_gemm_workspace_bytes(N, in_features_, out_features_),
