@@ -256,8 +256,8 @@ def main():
     # dominant kernel = the largest summed time among the families whose
     # C-ABI call is exactly one kernel launch: gemm_fwd (the persistent
     # kernel, e4m3 x e4m3 -> bf16 + bias) and gemm_dx (persistent, e5m2 x e4m3
-    # -> bf16).  gemm_dw is several kernels (split-K partial tiles + their
-    # reduction on the small outputs) and each quantize family two or three
+    # -> bf16).  gemm_dw is several kernels (K-slice partial tiles + their
+    # ordered reduction on the split outputs) and each quantize family two or three
     # (absmax passes, 2-D quantize, column-sum fold); they are reported in
     # `kernels` but a per-launch roofline needs one kernel.
     dom = max(SINGLE_KERNEL_FAMILIES, key=lambda k: per[k][0])
