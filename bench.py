@@ -63,7 +63,8 @@ def parse():
                    help="also time the 12 GEMM shapes on torch._scaled_mm (hipBLASLt) for comparison")
     p.add_argument("--history", type=int, default=16, help="amax history length of the delayed-scaling leg")
     p.add_argument("--stream-layers", type=int, default=48)
-    p.add_argument("--stream-slots", type=int, default=4)
+    p.add_argument("--stream-slots", type=int, default=6,
+                   help="device weight slots of the streaming leg (>= 3: loads run slots-2 layers ahead)")
     p.add_argument("--cpu-tokens", type=int, default=3072, help="token slice for the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     p.add_argument("--copy-calibration", action="store_true",
@@ -113,6 +114,9 @@ def main():
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding of this path is designed, not built)", file=sys.stderr)
+        sys.exit(2)
+    if args.stream_slots < 3:
+        print("bench.py: --stream-slots must be at least 3", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -824,7 +828,7 @@ def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
     return res
 
 
-def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=3, steps=2):
+def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, steps=2):
     """Config 5: a 48-layer GPT-2 XL Linear stack (4 Linears per layer) at
     `tokens` tokens, forward then backward, with every layer's e4m3 weight
     codes in pinned host memory: the forward sweep streams W [N, K] per layer,
@@ -945,16 +949,19 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=3, step
         step_flops = 3 * 2 * M * sum(K * N for _, K, N in XL_LINEARS) * layers
 
         def streamed_step(st):
-            pending, nxt = [], 0
+            # load idx + slots - 2 right after layer idx's launches: the load
+            # blocks until layer idx - 2 is done, layers idx - 1 and idx stay
+            # queued on the compute stream
+            ahead = slots - 2
+            pending = [st.load(hp.value + (2 * ll + dd) * blob, blob) for dd, ll in seq[:ahead]]
             for idx, (d, l) in enumerate(seq):
-                while nxt < len(seq) and nxt <= idx + slots - 1:
-                    dd, ll = seq[nxt]
-                    pending.append(st.load(hp.value + (2 * ll + dd) * blob, blob))
-                    nxt += 1
                 slot, base = pending.pop(0)
                 st.wait(slot)
                 (fwd_layer if d == 0 else bwd_layer)(l, base)
                 st.release(slot)
+                if idx + ahead < len(seq):
+                    dd, ll = seq[idx + ahead]
+                    pending.append(st.load(hp.value + (2 * ll + dd) * blob, blob))
 
         def timed(fn, reps):
             torch.cuda.synchronize()

@@ -1,14 +1,16 @@
 // stream.hip -- layer weight streaming: a ring of device slots filled from
 // pinned host memory by hipMemcpyAsync on the streamer's own copy stream,
 // ordered against the compute stream with events in both directions:
-//   load(l)    : the copy into slot s waits for the event recorded when the
-//                slot's previous contents were released, then records
-//                loaded[s] on the copy stream;
+//   load(l)    : the calling thread waits until the event recorded when the
+//                slot's previous contents were released has completed, then
+//                enqueues the copy and records loaded[s] on the copy stream;
 //   wait(s)    : the compute stream waits for loaded[s];
 //   release(s) : records released[s] on the compute stream after the last
 //                launch that reads the slot.
-// With S slots and loads issued S-1 layers ahead, the copy of layer l+S-1
-// runs while layer l computes (it only waits for layer l-1's kernels).
+// With S slots and loads issued S-2 layers ahead (load l+S-2 right after
+// layer l's launches), the thread blocks until layer l-2 has finished while
+// layers l-1 and l are queued, and the copies run S-2 layers ahead of the
+// kernels that read them.
 //
 // The reference describes this as layer-serialized execution
 // (README.md:212-226) but implements only the host side of it: pinned
@@ -25,6 +27,7 @@
 namespace dfk {
 
 constexpr int kMaxSlots = 16;
+
 constexpr size_t kSlotAlign = 4096;
 
 enum SlotState : int { kEmpty = 0, kLoaded = 1, kReleased = 2 };
@@ -138,7 +141,11 @@ extern "C" int df_streamer_load(df_streamer_s* s, const void* host_src, size_t b
     const int k = s->next;
     DF_CHECK(s->state[k] != kLoaded, DF_ERR_INVALID,
              "df_streamer_load: slot %d is still in use (df_streamer_release was not called for it)", k);
-    if (s->state[k] == kReleased) DF_HIP(hipStreamWaitEvent(s->copy, s->released[k], 0), "df_streamer_load");
+    // The calling thread, not the copy engine, waits for the release: a copy
+    // made to wait on the GPU for an event of the compute stream delays the
+    // compute stream's own work (measured: 81.5 ms instead of 65.5 ms for a
+    // 96-layer sweep whose kernels alone take 57.6 ms).
+    if (s->state[k] == kReleased) DF_HIP(hipEventSynchronize(s->released[k]), "df_streamer_load");
     uint8_t* dst = s->dev + (size_t)k * s->slot_bytes;
     if (bytes) DF_HIP(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, s->copy), "df_streamer_load");
     DF_HIP(hipEventRecord(s->loaded[k], s->copy), "df_streamer_load");

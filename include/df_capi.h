@@ -255,14 +255,18 @@ int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ld
  * apps/host-multi/NVMeLoader_Linux.hpp:20-26,64-71,123-125) ----
  * A streamer owns `slots` device buffers of slot_bytes (rounded up to 4 KiB)
  * and a copy stream of default priority.  Per layer:
- *   df_streamer_load    : copies `bytes` from host memory (pinned, for the
- *                         copy to be asynchronous) into the next slot in ring
- *                         order on the copy stream, after the work recorded
- *                         by that slot's last df_streamer_release;
+ *   df_streamer_load    : blocks the calling thread until the work recorded
+ *                         by the next slot's last df_streamer_release has
+ *                         completed, then enqueues the copy of `bytes` from
+ *                         host memory (pinned, for the copy to be
+ *                         asynchronous) into that slot (ring order) on the
+ *                         copy stream;
  *   df_streamer_wait    : makes `stream` wait until the slot's copy landed;
  *   df_streamer_release : records, on `stream`, the point after which the
  *                         slot may be overwritten (call it after enqueuing
  *                         every launch that reads the slot).
+ * Issue load(l + slots - 2) right after layer l's launches: the thread then
+ * blocks only until layer l-2 has finished, with layers l-1 and l queued.
  * Loading into a slot that was loaded but not released is DF_ERR_INVALID.
  * One streamer is used by one host thread at a time. */
 typedef struct df_streamer_s df_streamer;

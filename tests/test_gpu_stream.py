@@ -100,11 +100,13 @@ def run_stack(dev, slots, layers, shapes, M, prefetch):
         df.call("df_host_free", host_ptr)
 
 
-@pytest.mark.parametrize("slots", [2, 3])
-def test_streamed_stack_matches_resident(dev, slots):
+@pytest.mark.parametrize("slots,prefetch", [(2, 1), (3, 2), (4, 1), (6, 3)])
+def test_streamed_stack_matches_resident(dev, slots, prefetch):
     # long GEMMs keep the compute stream busy, so a refill that did not wait
-    # for the release event would overwrite weights still being read
-    run_stack(dev, slots, layers=7, shapes=[(1600, 1600), (320, 4800)], M=4096, prefetch=slots - 1)
+    # for the release event would overwrite weights still being read;
+    # prefetch = slots - 1 makes every load wait for the layer just queued,
+    # prefetch = slots - 3 is the pattern that keeps two layers queued
+    run_stack(dev, slots, layers=9, shapes=[(1600, 1600), (320, 4800)], M=4096, prefetch=prefetch)
 
 
 def test_streamer_refuses_unreleased_slot(dev):
