@@ -46,6 +46,7 @@ FP8_PEAK_TFLOPS = 5000.0
 M_TOKENS = 16384
 SINGLE_KERNEL_FAMILIES = ("gemm_fwd", "gemm_dx")
 XL_LINEARS = [("qkv", 1600, 4800), ("attn_proj", 1600, 1600), ("fc", 1600, 6400), ("proj", 6400, 1600)]
+SMALL_LINEARS = [("qkv", 768, 2304), ("attn_proj", 768, 768), ("fc", 768, 3072), ("proj", 3072, 768)]
 
 
 def parse():
@@ -59,6 +60,7 @@ def parse():
     p.add_argument("--no-optimizer", action="store_true", help="skip the clip + Adam leg")
     p.add_argument("--no-delayed", action="store_true", help="skip the delayed-scaling step leg")
     p.add_argument("--no-producer", action="store_true", help="skip the LayerNorm + quantize leg")
+    p.add_argument("--no-config3", action="store_true", help="skip the GPT-2 small forward leg (config 3)")
     p.add_argument("--vendor-compare", action="store_true",
                    help="also time the 12 GEMM shapes on torch._scaled_mm (hipBLASLt) for comparison")
     p.add_argument("--history", type=int, default=16, help="amax history length of the delayed-scaling leg")
@@ -319,6 +321,8 @@ def main():
         out["conversion"] = conversion_bench(torch, df, synth, dev, cur())
     if args.vendor_compare:
         out["vendor_compare"] = vendor_bench(torch, df, dev, cur())
+    if not args.no_config3:
+        out["config3"] = config3_bench(torch, df, synth, dev, cur())
     if not args.no_producer:
         out["producer"] = producer_bench(torch, df, synth, dev, cur())
     if not args.no_optimizer:
@@ -349,21 +353,21 @@ def measured_traffic(kernel_family):
 PROFILE_COMMANDS = {
     "stats": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_bench -o bench -- "
               "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion --no-streaming "
-              "--no-optimizer --no-producer --no-delayed"),
+              "--no-optimizer --no-producer --no-delayed --no-config3"),
     "fetch": ("timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_fetch -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
-              "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-graph "
+              "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph "
               "--copy-calibration"),
     "write": ("timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_write -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
-              "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-graph "
+              "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph "
               "--copy-calibration"),
     "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
-                       "--no-producer --no-delayed"),
+                       "--no-producer --no-delayed --no-config3"),
     "stats_producer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_producer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
-                       "--no-optimizer --no-delayed"),
+                       "--no-optimizer --no-delayed --no-config3"),
 }
 # extra kernel-stat summaries: (command key, csv directory, output file, title,
 # substrings that select the leg's own kernels)
@@ -673,6 +677,80 @@ def vendor_bench(torch, df, dev, stream, M=16384, reps=10):
     if errors:
         res["vendor_errors"] = errors
     torch.cuda.empty_cache()
+    return res
+
+
+def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20):
+    """Config 3: the four GPT-2 small Linears at 8192 tokens, forward only.
+    Per Linear: absmax + e4m3 codes of X [M, K] and W [N, K] (bf16), then
+    the fp8 GEMM with the fused scale, bf16 bias and bf16 output.  Reported:
+    each GEMM alone (average launch), the four GEMMs, and the whole forward
+    with its quantization, against the per-shape attainable bound
+    min(5.0 PF, AI x 8 TB/s) (AI: fp8 A and B read once, bf16 C written
+    once)."""
+    import numpy as np
+    from deepfuse_amd import DType, Fmt
+    BF, E4 = int(DType.BFLOAT16), int(Fmt.E4M3)
+    bf = lambda a: torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+    aws = torch.empty(df.lib().df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
+    gws_b = max(df.lib().df_fp8_gemm_workspace_bytes(M, n, k) for _, k, n in SMALL_LINEARS)
+    gws = torch.empty(max(gws_b, 16), dtype=torch.uint8, device=dev)
+    lin = []
+    for i, (name, K, N) in enumerate(SMALL_LINEARS):
+        seed = synth.SEED_BASE + 3 + 10 * i
+        lin.append(dict(name=name, K=K, N=N, X=bf(synth.normal((M, K), 1.0, seed=seed)),
+                        W=bf(synth.normal((N, K), 0.02, seed=seed + 1)), b=bf(synth.normal((N,), 0.02, seed=seed + 2)),
+                        Xq=torch.empty((M, K), dtype=torch.uint8, device=dev),
+                        Wq=torch.empty((N, K), dtype=torch.uint8, device=dev),
+                        Y=torch.empty((M, N), dtype=torch.bfloat16, device=dev),
+                        sc=torch.empty(4, dtype=torch.float32, device=dev)))
+
+    def quant(l):
+        s = l["sc"].data_ptr()
+        for t, q, am, sp in ((l["X"], l["Xq"], s, s + 4), (l["W"], l["Wq"], s + 8, s + 12)):
+            df.call("df_absmax_scale_bf16", t.data_ptr(), t.numel(), E4, am, sp, aws.data_ptr(), aws.numel(), stream)
+            df.call("df_quantize_bf16_e4m3", t.data_ptr(), t.numel(), sp, q.data_ptr(), stream)
+
+    def gemm(l):
+        s = l["sc"].data_ptr()
+        df.call("df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["K"], l["Wq"].data_ptr(), l["K"], M, l["N"], l["K"], s + 4,
+                s + 12, BF, l["b"].data_ptr(), BF, l["Y"].data_ptr(), l["N"], gws.data_ptr(), gws.numel(), stream)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    res = {"workload": f"config 3: GPT-2 small Linears, M={M} tokens, forward, bf16 out + fused bias", "linears": {}}
+    tot_flops, tot_ms = 0, 0.0
+    for l in lin:
+        quant(l)
+        K, N = l["K"], l["N"]
+        flops = 2 * M * N * K
+        ms = timed(lambda: gemm(l))
+        ai = flops / (M * K + N * K + 2 * M * N)
+        bound = min(5.0e15, ai * 8.0e12)
+        res["linears"][l["name"]] = {"shape": [M, N, K], "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                                     "attainable_tflops": round(bound / 1e12, 1),
+                                     "frac_of_attainable": round(flops / (ms * 1e-3) / bound, 4)}
+        tot_flops += flops
+        tot_ms += ms
+    res["gemm_only"] = {"ms": round(tot_ms, 4), "tflops": round(tot_flops / (tot_ms * 1e-3) / 1e12, 1),
+                        "frac_of_fp8_peak": round(tot_flops / (tot_ms * 1e-3) / 5.0e15, 4)}
+
+    def forward():
+        for l in lin:
+            quant(l)
+            gemm(l)
+
+    ms = timed(forward)
+    res["forward_with_quantize"] = {"ms": round(ms, 4), "tflops": round(tot_flops / (ms * 1e-3) / 1e12, 1)}
     return res
 
 
