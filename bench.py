@@ -1147,10 +1147,27 @@ def cpu_baseline(tokens):
                     break
     except OSError:
         pass
+    # the conversion contract on the first 2^26 elements of the config-2 fp32
+    # tensor (outliers, +-inf, NaN, subnormals), e4m3
+    n = 1 << 26
+    x = synth.conversion_input(n)
+    conv = {"n": n, "input": "config-2 fp32 tensor, first 2^26 elements", "fmt": "e4m3"}
+    t0 = time.perf_counter()
+    am = orc.absmax(x)
+    conv["absmax_gbs_1thread"] = round(4 * n / (time.perf_counter() - t0) / 1e9, 3)
+    sc = orc.scale(am, orc.E4M3)
+    for nt in (1, threads):
+        t0 = time.perf_counter()
+        q = orc.quantize(x, sc, orc.E4M3, threads=nt)
+        conv[f"quantize_gbs_{nt}thread" + ("s" if nt > 1 else "")] = round(5 * n / (time.perf_counter() - t0) / 1e9, 3)
+    t0 = time.perf_counter()
+    orc.dequantize(q, sc, orc.E4M3)
+    conv["dequantize_f32_gbs_1thread"] = round(5 * n / (time.perf_counter() - t0) / 1e9, 3)
     return {"value": round(flops / t_total / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port", "seconds": round(t_total, 2), "cpu": model,
             "sample": f"oracle fp32 kernel-order loops, fwd+dX+dW of the 4 GPT-2 XL Linears on a "
-                      f"{tokens}-token slice ({flops} flop), {threads} threads"}
+                      f"{tokens}-token slice ({flops} flop), {threads} threads",
+            "conversion": conv}
 
 
 if __name__ == "__main__":
