@@ -773,8 +773,11 @@ static int grid_for(int64_t units, int64_t per_block_unit_cap) {
 
 using namespace dfk;
 
-// Grid for streaming kernels: 256 CUs x 8 blocks, grid-stride beyond that.
-static constexpr int64_t kStreamBlocks = 2048;
+// Grid cap for the quantize/dequantize kernels: about one chunk per block up
+// to 2^28 fp32 elements, grid-stride beyond.  Many short-lived blocks keep
+// more of the chip's store traffic in flight than 2048 looping blocks:
+// +5-7% at config 2 (e.g. fp32 -> e4m3 5.52-5.65 -> 5.91-6.01 TB/s).
+static constexpr int64_t kStreamBlocks = 32768;
 
 extern "C" size_t df_absmax_workspace_bytes(void) { return kMaxReduceBlocks * sizeof(uint32_t); }
 
