@@ -53,7 +53,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-conversion", action="store_true")
     p.add_argument("--no-streaming", action="store_true", help="skip the config 5 layer-streaming leg")
@@ -61,6 +61,8 @@ def parse():
     p.add_argument("--no-delayed", action="store_true", help="skip the delayed-scaling step leg")
     p.add_argument("--no-producer", action="store_true", help="skip the LayerNorm + quantize leg")
     p.add_argument("--no-config3", action="store_true", help="skip the GPT-2 small forward leg (config 3)")
+    p.add_argument("--separate-backward", action="store_true",
+                   help="time the backward as separate dX and dW launches instead of df_fp8_gemm_bwd")
     p.add_argument("--vendor-compare", action="store_true",
                    help="also time the 12 GEMM shapes on torch._scaled_mm (hipBLASLt) for comparison")
     p.add_argument("--history", type=int, default=16, help="amax history length of the delayed-scaling leg")
@@ -149,6 +151,7 @@ def main():
     ws = torch.empty(L.df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
     gws_bytes = max(L.df_fp8_gemm_workspace_bytes(M, n, k) for _, k, n in XL_LINEARS)
     gws_bytes = max(gws_bytes, max(L.df_fp8_gemm_workspace_bytes(n, k, M) for _, k, n in XL_LINEARS))
+    gws_bytes = max(gws_bytes, max(L.df_fp8_gemm_bwd_workspace_bytes(M, n, k) for _, k, n in XL_LINEARS))
     gws = torch.empty(gws_bytes, dtype=torch.uint8, device=dev)
     cws = torch.empty(max(L.df_quantize_2d_workspace_bytes(M, n) for _, _, n in XL_LINEARS), dtype=torch.uint8,
                       device=dev)
@@ -189,7 +192,7 @@ def main():
                    sc, q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), db.data_ptr(), cws.data_ptr(),
                    cws.numel(), cur())
 
-    def step(tm):
+    def step(tm, grouped=not args.separate_backward):
         for l in layers:
             K, N = l["K"], l["N"]
             s = l["sc"].data_ptr()
@@ -200,6 +203,13 @@ def main():
                    l["Wq"].data_ptr(), l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF,
                    l["Y"].data_ptr(), N, gws.data_ptr(), gws_bytes, cur())
             quant(tm, l["dY"], M, N, E5, sdy_am, sdy, l["dYq"], l["dYt"], "grad", db=l["db"])
+            if grouped:
+                # dX and dW in one launch (df_fp8_gemm_bwd)
+                tm.run("gemm_bwd", df.call, "df_fp8_gemm_bwd", l["dYq"].data_ptr(), l["dYq"].stride(0),
+                       l["Wt"].data_ptr(), l["Wt"].stride(0), l["dYt"].data_ptr(), l["dYt"].stride(0),
+                       l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sw, sx, BF, l["dX"].data_ptr(), K,
+                       F32, l["dW"].data_ptr(), K, gws.data_ptr(), gws_bytes, cur())
+                continue
             tm.run("gemm_dx", df.call, "df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0),
                    l["Wt"].data_ptr(), l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K,
                    gws.data_ptr(), gws_bytes, cur())
@@ -208,12 +218,13 @@ def main():
                    gws.data_ptr(), gws_bytes, cur())
 
     # algorithmic work per step: 2*M*N*K per GEMM on unpadded shapes
-    gemm_flops = {"gemm_fwd": 0, "gemm_dx": 0, "gemm_dw": 0}
+    families = ("gemm_fwd", "gemm_dx", "gemm_dw") if args.separate_backward else ("gemm_fwd", "gemm_bwd")
+    gemm_flops = {k: 0 for k in families}
     qbytes = {}
     for (_, K, N) in XL_LINEARS:
         f = 2 * M * N * K
         for k in gemm_flops:
-            gemm_flops[k] += f
+            gemm_flops[k] += 2 * f if k == "gemm_bwd" else f
         for tag, r, c in (("act", M, K), ("weight", N, K), ("grad", M, N)):
             qbytes["absmax_" + tag] = qbytes.get("absmax_" + tag, 0) + 2 * r * c
             qbytes["quantize2d_" + tag] = qbytes.get("quantize2d_" + tag, 0) + 2 * r * c + 2 * r * c
@@ -233,7 +244,10 @@ def main():
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step(null)
-        graph.replay()
+        # the warm-up steps again, replayed like the timed ones (the first
+        # replays after capture run a few percent slower)
+        for _ in range(max(1, args.warmup)):
+            graph.replay()
         torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -252,6 +266,41 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     value = step_flops / (elapsed / args.steps) / 1e12
 
+    # Outside the timed region: the same step with the backward as the two
+    # separate dX and dW launches, for comparison.
+    separate = None
+    if not args.separate_backward:
+        g2 = None
+        if not args.no_graph:
+            g2 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g2):
+                step(null, grouped=False)
+        run_sep = g2.replay if g2 is not None else (lambda: step(null, grouped=False))
+        run_grp = graph.replay if graph is not None else (lambda: step(null))
+        run_sep()
+        torch.cuda.synchronize()
+
+        def avg_ms(fn):
+            s0 = torch.cuda.Event(enable_timing=True)
+            s1 = torch.cuda.Event(enable_timing=True)
+            s0.record()
+            for _ in range(args.steps):
+                fn()
+            s1.record()
+            torch.cuda.synchronize()
+            return s0.elapsed_time(s1) / args.steps
+
+        # alternate the two, three times each; best of each
+        sep_t, grp_t = [], []
+        for _ in range(3):
+            sep_t.append(avg_ms(run_sep))
+            grp_t.append(avg_ms(run_grp))
+        sep_ms, grp_ms = min(sep_t), min(grp_t)
+        separate = {"ms_per_step": round(sep_ms, 4), "tflops": round(step_flops / (sep_ms * 1e-3) / 1e12, 2),
+                    "grouped_ms_per_step": round(grp_ms, 4), "grouped_speedup": round(sep_ms / grp_ms, 4),
+                    "note": "best of 3 alternating runs of the two step variants, after the timed region"}
+        del g2
+
     # Per-kernel durations: the same step launched eagerly with a HIP-event
     # pair around every C-ABI call, over as many steps as the timed region.
     tm = Timer(torch)
@@ -266,7 +315,7 @@ def main():
     # ordered reduction on the split outputs) and each quantize family two or three
     # (absmax passes, 2-D quantize, column-sum fold); they are reported in
     # `kernels` but a per-launch roofline needs one kernel.
-    dom = max(SINGLE_KERNEL_FAMILIES, key=lambda k: per[k][0])
+    dom = max((k for k in SINGLE_KERNEL_FAMILIES if k in per), key=lambda k: per[k][0])
     tot_ms, cnt = per[dom]
     avg_ms = tot_ms / cnt
     if dom in gemm_flops:
@@ -315,6 +364,8 @@ def main():
         "roofline": roof,
         "kernels": kernels,
     }
+    if separate is not None:
+        out["backward_separate_launches"] = separate
     if delayed is not None:
         out["delayed_scaling"] = delayed
     if not args.no_conversion:
@@ -587,12 +638,18 @@ def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit
                     l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF, l["Y"].data_ptr(), N,
                     gws.data_ptr(), gws_bytes, cur())
             sdy = quant(r["dy"], parity)
-            df.call("df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0), l["Wt"].data_ptr(),
-                    l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K, gws.data_ptr(), gws_bytes,
-                    cur())
-            df.call("df_fp8_gemm_bwd_dw", l["dYt"].data_ptr(), l["dYt"].stride(0), l["Xt"].data_ptr(),
-                    l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K, gws.data_ptr(), gws_bytes,
-                    cur())
+            if args.separate_backward:
+                df.call("df_fp8_gemm_bwd_dx", l["dYq"].data_ptr(), l["dYq"].stride(0), l["Wt"].data_ptr(),
+                        l["Wt"].stride(0), M, N, K, sdy, sw, BF, l["dX"].data_ptr(), K, gws.data_ptr(),
+                        gws_bytes, cur())
+                df.call("df_fp8_gemm_bwd_dw", l["dYt"].data_ptr(), l["dYt"].stride(0), l["Xt"].data_ptr(),
+                        l["Xt"].stride(0), M, N, K, sdy, sx, F32, l["dW"].data_ptr(), K, gws.data_ptr(),
+                        gws_bytes, cur())
+            else:
+                df.call("df_fp8_gemm_bwd", l["dYq"].data_ptr(), l["dYq"].stride(0), l["Wt"].data_ptr(),
+                        l["Wt"].stride(0), l["dYt"].data_ptr(), l["dYt"].stride(0), l["Xt"].data_ptr(),
+                        l["Xt"].stride(0), M, N, K, sdy, sw, sx, BF, l["dX"].data_ptr(), K, F32,
+                        l["dW"].data_ptr(), K, gws.data_ptr(), gws_bytes, cur())
 
     for _ in range(max(1, args.warmup)):
         step(0)
@@ -987,7 +1044,7 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
         sc = torch.empty((len(XL_LINEARS), 4), dtype=torch.float32, device=dev)
         cws = torch.empty(max(df.lib().df_quantize_2d_workspace_bytes(M, N) for _, _, N in XL_LINEARS),
                           dtype=torch.uint8, device=dev)
-        gws_b = max(max(df.lib().df_fp8_gemm_workspace_bytes(M, n, k), df.lib().df_fp8_gemm_workspace_bytes(n, k, M))
+        gws_b = max(max(df.lib().df_fp8_gemm_workspace_bytes(M, n, k), df.lib().df_fp8_gemm_bwd_workspace_bytes(M, n, k))
                     for _, k, n in XL_LINEARS)
         gws = torch.empty(max(gws_b, 16), dtype=torch.uint8, device=dev)
         BF, F32, E4, E5 = int(DType.BFLOAT16), int(DType.FLOAT32), int(Fmt.E4M3), int(Fmt.E5M2)
@@ -1015,13 +1072,12 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
                         dyq[i].stride(0), dyt[i].data_ptr(), Mp, db[i].data_ptr(), cws.data_ptr(), cws.numel(),
                         cur())
                 swp = sw.data_ptr() + 4 * (l * len(XL_LINEARS) + i)
-                df.call("df_fp8_gemm_bwd_dx", dyq[i].data_ptr(), dyq[i].stride(0), base + bwd_off[i], r16(N), M, N,
-                        K, s + 12, swp, BF, dX[i].data_ptr(), K, gws.data_ptr(), gws.numel(), cur())
-                # the activation scale of layer l's forward is the one cached
-                # with xt[l]; every layer sees the same activations here, so
-                # sc[i][1] still holds it
-                df.call("df_fp8_gemm_bwd_dw", dyt[i].data_ptr(), Mp, xt[l][i].data_ptr(), Mp, M, N, K, s + 12,
-                        s + 4, F32, dW[l][i].data_ptr(), K, gws.data_ptr(), gws.numel(), cur())
+                # dX and dW in one launch; the activation scale of layer l's
+                # forward is the one cached with xt[l]; every layer sees the
+                # same activations here, so sc[i][1] still holds it
+                df.call("df_fp8_gemm_bwd", dyq[i].data_ptr(), dyq[i].stride(0), base + bwd_off[i], r16(N),
+                        dyt[i].data_ptr(), Mp, xt[l][i].data_ptr(), Mp, M, N, K, s + 12, swp, s + 4, BF,
+                        dX[i].data_ptr(), K, F32, dW[l][i].data_ptr(), K, gws.data_ptr(), gws.numel(), cur())
 
         seq = [(0, l) for l in range(layers)] + [(1, l) for l in reversed(range(layers))]
         step_flops = 3 * 2 * M * sum(K * N for _, K, N in XL_LINEARS) * layers

@@ -88,6 +88,10 @@ _SIGS = {
                                     _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_bwd_dw": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                     _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+    "df_fp8_gemm_bwd_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
+    "df_fp8_gemm_bwd_plan": (_c_int, [_c_int, _c_int, _c_int, _c_sz, _vp, _vp]),
+    "df_fp8_gemm_bwd": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                 _vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fill": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp]),
     "df_add": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
     "df_convert": (_c_int, [_c_int, _vp, _c_int, _vp, _c_i64, _vp]),
@@ -285,6 +289,37 @@ def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dty
          M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _ptr(ws),
          ws.numel() if ws is not None else 0, _stream())
     return c
+
+
+def gemm_bwd(dy_q, wt_q, dyt_q, xt_q, M: int, N: int, K: int, sdy, sw, sx, dx_dtype=None, dw_dtype=None,
+             workspace=True):
+    """dX [M, K] and dW [N, K] of one Linear in one call (df_fp8_gemm_bwd):
+    dy_q [M, >=N] and dyt_q [N, >=M] e5m2, wt_q [K, >=N] and xt_q [K, >=M]
+    e4m3, as df_quantize_2d writes them."""
+    torch = _torch()
+    dx_dtype = dx_dtype or torch.float32
+    dw_dtype = dw_dtype or torch.float32
+    dev = dy_q.device
+    dX = torch.empty((M, K), dtype=dx_dtype, device=dev)
+    dW = torch.empty((N, K), dtype=dw_dtype, device=dev)
+    dt = lambda t: int(DType.FLOAT32) if t == torch.float32 else int(DType.BFLOAT16)
+    ws = None
+    if workspace:
+        ws = _scratch(dev, max(int(lib().df_fp8_gemm_bwd_workspace_bytes(M, N, K)), 16), "gemm_bwd")
+    call("df_fp8_gemm_bwd", _ptr(dy_q), dy_q.stride(0), _ptr(wt_q), wt_q.stride(0), _ptr(dyt_q), dyt_q.stride(0),
+         _ptr(xt_q), xt_q.stride(0), M, N, K, _ptr(sdy), _ptr(sw), _ptr(sx), dt(dx_dtype), _ptr(dX), K,
+         dt(dw_dtype), _ptr(dW), K, _ptr(ws), ws.numel() if ws is not None else 0, _stream())
+    return dX, dW
+
+
+def gemm_bwd_plan(M: int, N: int, K: int, ws_bytes: int | None = None):
+    """(grouped, dW slices) that df_fp8_gemm_bwd picks; ws_bytes defaults
+    to df_fp8_gemm_bwd_workspace_bytes."""
+    if ws_bytes is None:
+        ws_bytes = int(lib().df_fp8_gemm_bwd_workspace_bytes(M, N, K))
+    g, s = _c_int(), _c_int()
+    call("df_fp8_gemm_bwd_plan", M, N, K, ws_bytes, ctypes.byref(g), ctypes.byref(s))
+    return bool(g.value), s.value
 
 
 def colsum(x):

@@ -37,6 +37,7 @@
 #include <type_traits>
 
 #include "df_common.hpp"
+#include "gemm_sched.hpp"
 
 namespace dfk {
 
@@ -471,20 +472,49 @@ __device__ __forceinline__ constexpr int waitcnt_vm_lgkm0(int n) {
     return (n & 15) | ((n >> 4) << 14) | 0x70;
 }
 
-template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT = false>
+// Epilogue geometry for an output element of ES bytes: each 32-row block of
+// a wave's 128x64 quarter passes through an LDS slab of SR rows.
+template <int ES>
+struct EpiGeom {
+    static constexpr int SR = ES == 2 ? 16 : 8;          // slab rows
+    static constexpr int SROW = 64 * ES + 16;            // padded slab row (bytes)
+    static constexpr int SLAB = SR * SROW;
+    static constexpr int NPASS = 32 / SR;                // slab passes per 32-row block
+    static constexpr int SPP = SR * 64 * ES / 1024;      // 16-byte stores per lane per pass
+    static constexpr int NST = 4 * NPASS * SPP;          // epilogue stores per wave
+};
+
+// The second GEMM of a grouped launch (see gemm_sched.hpp): its operands,
+// output and scales; never split, no bias.
+struct PProb {
+    const uint8_t* A;
+    const uint8_t* B;
+    void* C;
+    const float* sa;
+    const float* sb;
+    int lda, ldb, M, N, K, ldc, vec_out;
+};
+
+// cost of a work unit beyond its DMA steps (pipeline fill, epilogue), in
+// the steps of the grouped schedule
+constexpr int kUnitOverhead = 3;
+
+template <typename T> struct Tag { using type = T; };
+
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT = false, typename OutT1 = void>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
     const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
-    OutT* __restrict__ C, int ldc, int vec_out, int ksteps = 0, int nsplit = 1) {
+    OutT* __restrict__ C, int ldc, int vec_out, int ksteps = 0, int nsplit = 1, PProb p1 = {}) {
+    constexpr bool GROUPED = !std::is_void<OutT1>::value;
+    using Out1 = typename std::conditional<GROUPED, OutT1, OutT>::type;
     constexpr int FM = 4, FN = 2;                 // 32x32 MFMA tiles per wave
-    constexpr int ES = (int)sizeof(OutT);
-    constexpr int SR = ES == 2 ? 16 : 8;          // epilogue slab rows
-    constexpr int SROW = 64 * ES + 16;            // padded slab row (bytes)
-    constexpr int SLAB = SR * SROW;
-    constexpr int NPASS = 32 / SR;                // slab passes per 32-row block
-    constexpr int SPP = SR * 64 * ES / 1024;      // 16-byte stores per lane per pass
-    constexpr int NST = FM * NPASS * SPP;         // epilogue stores per wave
-    constexpr int W_AFTER = NST > 63 ? 63 : NST;
+    using G0 = EpiGeom<(int)sizeof(OutT)>;
+    using G1 = EpiGeom<(int)sizeof(Out1)>;
+    constexpr int SLAB = G0::SLAB > G1::SLAB ? G0::SLAB : G1::SLAB;
+    // after an epilogue, a wait that leaves the smaller store count in flight
+    constexpr int NSTMIN = G0::NST < G1::NST ? G0::NST : G1::NST;
+    constexpr int W_AFTER = NSTMIN > 63 ? 63 : NSTMIN;
     constexpr uint32_t kOOB = 0x80000000u;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kPStage + kPBiasSlots * kPBiasSlot + 8 * SLAB];
     uint8_t* const lbias = lds + 2 * kPStage;
@@ -506,35 +536,50 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     // last one shorter); a unit's fp32 partial tile goes to slice ks of C
     // ([nsplit][M][N], ldc = N).  Units running at the same time share a K
     // slice, so tiles of one row (column) meet their A (B) panel in L2.
+    //
+    // GROUPED: the units of a second GEMM p1 (unsplit tiles) follow in the
+    // same grid, dealt by the static schedule of gemm_sched.hpp: this
+    // problem's units round-robin first, then p1's in start-time order.
     const int L = SPLIT ? ksteps : nk;
     const int nunits = SPLIT ? ntiles * nsplit : ntiles;
-    const int my_tiles = bl < nunits ? (nunits - bl + P - 1) / P : 0;  // work units of this block
-    auto tile_mn = [&](int r, int& m0, int& n0, int& kb, int& nku, int& slot) {
+    const int tiles_m1 = GROUPED ? (p1.M + kPBM - 1) / kPBM : 1, tiles_n1 = GROUPED ? (p1.N + kPBN - 1) / kPBN : 1;
+    const int nk1 = GROUPED ? (p1.K + kPKB - 1) / kPKB : 0;
+    const GroupSched gs{P, nunits, L + kUnitOverhead, GROUPED ? tiles_m1 * tiles_n1 : 0, nk1 + kUnitOverhead};
+    const int my_tiles = GROUPED ? gs_d0(gs, bl) + gs_d1(gs, bl)
+                                 : (bl < nunits ? (nunits - bl + P - 1) / P : 0);  // work units of this block
+    auto tile_mn = [&](int r, int& pr, int& m0, int& n0, int& kb, int& nku, int& slot) {
         int lt = bl + r * P;
+        pr = 0;
+        if (GROUPED) gs_unit(gs, bl, r, pr, lt);
         slot = 0;
-        if (SPLIT) {
+        if (SPLIT && pr == 0) {
             slot = lt / ntiles;
             lt -= slot * ntiles;
         }
         kb = slot * L;
-        nku = min(nk - kb, L);
-        const int per_group = kGroupM * tiles_n;
+        nku = pr ? nk1 : min(nk - kb, L);
+        const int tm_ = pr ? tiles_m1 : tiles_m, tn_ = pr ? tiles_n1 : tiles_n;
+        const int per_group = kGroupM * tn_;
         const int group = lt / per_group;
         const int first_m = group * kGroupM;
-        const int gsize = min(tiles_m - first_m, kGroupM);
+        const int gsize = min(tm_ - first_m, kGroupM);
         const int in_group = lt - group * per_group;
         m0 = (first_m + in_group % gsize) * kPBM;
         n0 = (in_group / gsize) * kPBN;
     };
     int S = 0;  // DMA steps of this block
     for (int r = 0; r < my_tiles; ++r) {
-        int m0, n0, kb, nku, slot;
-        tile_mn(r, m0, n0, kb, nku, slot);
+        int pr, m0, n0, kb, nku, slot;
+        tile_mn(r, pr, m0, n0, kb, nku, slot);
         S += nku;
     }
 
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * lda, 0x00020000);
     const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, N * ldb, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rA1 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p1.A, (short)0, GROUPED ? p1.M * p1.lda : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB1 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p1.B, (short)0, GROUPED ? p1.N * p1.ldb : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t rBias =
         __builtin_amdgcn_make_buffer_rsrc((void*)bias, (short)0, HAS_BIAS ? N * (int)sizeof(BiasT) : 0, 0x00020000);
 
@@ -548,31 +593,35 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const int drow = lane >> 3;
     const int dch0 = ((lane & 7) ^ (lane >> 4)) << 4;
     const int dch1 = dch0 ^ 64;
-    const uint32_t a16 = 16u * (uint32_t)lda, b16 = 16u * (uint32_t)ldb;
-    int d_tile = 0, d_k = 0, d_m0 = 0, d_n0 = 0, d_g = 0, d_kb = 0, d_nku = 0, d_slot = 0;
+    int d_tile = 0, d_k = 0, d_m0 = 0, d_n0 = 0, d_g = 0, d_kb = 0, d_nku = 0, d_slot = 0, d_p = 0;
     uint32_t oa0 = kOOB, oa1 = kOOB, ob0 = kOOB, ob1 = kOOB, obias = kOOB;
     auto dprep = [&]() {
         const bool live = d_g < S;
+        const bool q1 = GROUPED && d_p;
+        const int lda_ = q1 ? p1.lda : lda, ldb_ = q1 ? p1.ldb : ldb, K_ = q1 ? p1.K : K;
         const int kstep = d_kb + d_k;
         const int k0 = kstep * kPKB + dch0, k1 = kstep * kPKB + dch1;
         const uint32_t ra = (uint32_t)(d_m0 + w * 32 + drow), rb = (uint32_t)(d_n0 + w * 32 + drow);
-        oa0 = (live && k0 < K) ? ra * (uint32_t)lda + (uint32_t)k0 : kOOB;
-        oa1 = (live && k1 < K) ? (ra + 8u) * (uint32_t)lda + (uint32_t)k1 : kOOB;
-        ob0 = (live && k0 < K) ? rb * (uint32_t)ldb + (uint32_t)k0 : kOOB;
-        ob1 = (live && k1 < K) ? (rb + 8u) * (uint32_t)ldb + (uint32_t)k1 : kOOB;
+        oa0 = (live && k0 < K_) ? ra * (uint32_t)lda_ + (uint32_t)k0 : kOOB;
+        oa1 = (live && k1 < K_) ? (ra + 8u) * (uint32_t)lda_ + (uint32_t)k1 : kOOB;
+        ob0 = (live && k0 < K_) ? rb * (uint32_t)ldb_ + (uint32_t)k0 : kOOB;
+        ob1 = (live && k1 < K_) ? (rb + 8u) * (uint32_t)ldb_ + (uint32_t)k1 : kOOB;
         if (HAS_BIAS) obias = live ? (uint32_t)(d_n0 * (int)sizeof(BiasT) + w * 256 + lane * 4) : kOOB;
     };
     auto dissue = [&]() {
         uint8_t* base = lds + ((uint32_t)d_g & 1u) * kPStage;
+        const bool q1 = GROUPED && d_p;
+        const __amdgpu_buffer_rsrc_t ra_ = q1 ? rA1 : rA, rb_ = q1 ? rB1 : rB;
+        const uint32_t a16 = 16u * (uint32_t)(q1 ? p1.lda : lda), b16 = 16u * (uint32_t)(q1 ? p1.ldb : ldb);
 #pragma unroll
         for (int d = 0; d < 4; ++d)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rA, (__attribute__((address_space(3))) void*)(base + (w * 4 + d) * 1024), 16,
+                ra_, (__attribute__((address_space(3))) void*)(base + (w * 4 + d) * 1024), 16,
                 ((d & 1) ? oa1 : oa0) + (uint32_t)(d >> 1) * a16, 0, 0, 0);
 #pragma unroll
         for (int d = 0; d < 4; ++d)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rB, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
+                rb_, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
                 ((d & 1) ? ob1 : ob0) + (uint32_t)(d >> 1) * b16, 0, 0, 0);
         if (HAS_BIAS)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -584,12 +633,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     auto dadvance = [&]() {
         if (d_g < S && ++d_k == d_nku) {
             d_k = 0;
-            if (++d_tile < my_tiles) tile_mn(d_tile, d_m0, d_n0, d_kb, d_nku, d_slot);
+            if (++d_tile < my_tiles) tile_mn(d_tile, d_p, d_m0, d_n0, d_kb, d_nku, d_slot);
         }
         ++d_g;
         dprep();
     };
-    if (my_tiles > 0) tile_mn(0, d_m0, d_n0, d_kb, d_nku, d_slot);
+    if (my_tiles > 0) tile_mn(0, d_p, d_m0, d_n0, d_kb, d_nku, d_slot);
     dprep();
 
     // ---- fragments (v_mfma_f32_32x32x64_f8f6f4 operand layout: lane l
@@ -617,6 +666,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
     int after_epi = 0, c_h = 0;
     const float sab = SPLIT ? 1.0f : sa[0] * sb[0];
+    const float sab1 = GROUPED ? p1.sa[0] * p1.sb[0] : 0.0f;
 
     // One half-step: MFMAs on (fa, fb); fragments of half-step c_h+1 into
     // (na, nb).  Odd half-steps first wait for the DMA step that half-step
@@ -671,10 +721,16 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         if (decltype(odd)::value) dadvance();
     };
 
-    auto epilogue = [&](int tile) {
-        int tm0, tn0, tkb, tnku, tslot;
-        tile_mn(tile, tm0, tn0, tkb, tnku, tslot);
-        OutT* const Cu = SPLIT ? C + (int64_t)tslot * M * N : C;
+    // Stores one finished tile: scale, bias, conversion to T, the slab pass
+    // and the 16-byte row-segment stores (tile: this block's unit index, for
+    // the bias slot).
+    auto store_tile = [&](auto tag, auto with_bias, typename decltype(tag)::type* const Cu, int Mo, int No,
+                          int ldco, int veco, float sabo, int tile, int tm0, int tn0) {
+        using T = typename decltype(tag)::type;
+        constexpr bool BIAS = decltype(with_bias)::value;
+        constexpr int ES = (int)sizeof(T);
+        constexpr int SR = EpiGeom<ES>::SR, SROW = EpiGeom<ES>::SROW;
+        constexpr int NPASS = EpiGeom<ES>::NPASS, SPP = EpiGeom<ES>::SPP;
         const int rowb = tm0 + wm * 128;
         const int colw = tn0 + wn * 64;
         const int h4 = (lane >> 5) * 4;
@@ -684,7 +740,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         // of the buffer, which the dword DMA returned as zero.
         float bv[FN][4][4];
         float btail = 0.f;
-        if (HAS_BIAS && sizeof(BiasT) == 2 && (N & 1) && colw + 64 >= N) btail = bias_ld(bias, N - 1);
+        if (BIAS && sizeof(BiasT) == 2 && (No & 1) && colw + 64 >= No) btail = bias_ld(bias, No - 1);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -692,7 +748,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 const int lc = wn * 64 + j * 32 + 8 * g + h4;
                 const int col = tn0 + lc;
                 float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-                if (HAS_BIAS) {
+                if (BIAS) {
                     if (sizeof(BiasT) == 4) {
                         const f32x4 v = *reinterpret_cast<const f32x4*>(bsl + lc * 4);
                         b0 = v.x; b1 = v.y; b2 = v.z; b3 = v.w;
@@ -700,11 +756,11 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                         const u32x2 v = *reinterpret_cast<const u32x2*>(bsl + lc * 2);
                         b0 = bf16_to_f32(v.x & 0xFFFFu); b1 = bf16_to_f32(v.x >> 16);
                         b2 = bf16_to_f32(v.y & 0xFFFFu); b3 = bf16_to_f32(v.y >> 16);
-                        if (N & 1) {
-                            b0 = col == N - 1 ? btail : b0;
-                            b1 = col + 1 == N - 1 ? btail : b1;
-                            b2 = col + 2 == N - 1 ? btail : b2;
-                            b3 = col + 3 == N - 1 ? btail : b3;
+                        if (No & 1) {
+                            b0 = col == No - 1 ? btail : b0;
+                            b1 = col + 1 == No - 1 ? btail : b1;
+                            b2 = col + 2 == No - 1 ? btail : b2;
+                            b3 = col + 3 == No - 1 ? btail : b3;
                         }
                     }
                 }
@@ -715,7 +771,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         constexpr int RPS = 64 / CPR;
         const int srow = lane / CPR, rc = lane % CPR;
         const int scol = colw + rc * (16 / ES);
-        const bool col_full = vec_out && scol + 16 / ES <= N;
+        const bool col_full = veco && scol + 16 / ES <= No;
         const int my_sr = fr % SR, my_pass = fr / SR;
         typedef typename std::conditional<ES == 2, u32x2, f32x4>::type Pk;
         Pk pk[FM][FN][4];
@@ -726,8 +782,8 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const v16f& a = acc[i][j];
-                    const float v0 = a[4 * g] * sab + bv[j][g][0], v1 = a[4 * g + 1] * sab + bv[j][g][1];
-                    const float v2 = a[4 * g + 2] * sab + bv[j][g][2], v3 = a[4 * g + 3] * sab + bv[j][g][3];
+                    const float v0 = a[4 * g] * sabo + bv[j][g][0], v1 = a[4 * g + 1] * sabo + bv[j][g][1];
+                    const float v2 = a[4 * g + 2] * sabo + bv[j][g][2], v3 = a[4 * g + 3] * sabo + bv[j][g][3];
                     if constexpr (ES == 2)
                         pk[i][j][g] = u32x2{pack_bf16_rne(v0, v1), pack_bf16_rne(v2, v3)};
                     else
@@ -753,20 +809,31 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                     const int sr = s * RPS + srow;
                     const u32x4 val = *reinterpret_cast<const u32x4*>(slab + sr * SROW + rc * 16);
                     const int row = rowb + i * 32 + p * SR + sr;
-                    if (row < M) {
-                        OutT* dst = Cu + (int64_t)row * ldc + scol;
+                    if (row < Mo) {
+                        T* dst = Cu + (int64_t)row * ldco + scol;
                         if (col_full) {
                             __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
                         } else {
-                            const OutT* ev = reinterpret_cast<const OutT*>(&val);
+                            const T* ev = reinterpret_cast<const T*>(&val);
 #pragma unroll
                             for (int x = 0; x < 16 / ES; ++x)
-                                if (scol + x < N) dst[x] = ev[x];
+                                if (scol + x < No) dst[x] = ev[x];
                         }
                     }
                 }
                 asm volatile("" ::: "memory");
             }
+    };
+
+    auto epilogue = [&](int tile) {
+        int tp, tm0, tn0, tkb, tnku, tslot;
+        tile_mn(tile, tp, tm0, tn0, tkb, tnku, tslot);
+        if (GROUPED && tp)
+            store_tile(Tag<Out1>{}, std::false_type{}, static_cast<Out1*>(p1.C), p1.M, p1.N, p1.ldc, p1.vec_out,
+                       sab1, tile, tm0, tn0);
+        else
+            store_tile(Tag<OutT>{}, std::integral_constant<bool, HAS_BIAS>{}, SPLIT ? C + (int64_t)tslot * M * N : C,
+                       M, N, ldc, vec_out, sab, tile, tm0, tn0);
         after_epi = 1;
     };
 
@@ -789,8 +856,8 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     // a tile is 2*max(nk,1) half-steps; the fragments of its first half-step
     // are in (fa0, fb0) when it starts
     for (int tile = 0; tile < my_tiles; ++tile) {
-        int um0, un0, ukb, unku, uslot;
-        tile_mn(tile, um0, un0, ukb, unku, uslot);
+        int up, um0, un0, ukb, unku, uslot;
+        tile_mn(tile, up, um0, un0, ukb, unku, uslot);
         half(Z{}, EVEN{}, fa0, fb0, fa1, fb1);
         half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
         for (int k = 1; k < unku; ++k) {
@@ -1014,6 +1081,76 @@ static void launch_shape(const GemmArgs& g) {
         launch_cfg<128, 128, 2, 2, FA, FB, OutT, BiasT>(g);
 }
 
+// Grouped backward launch: dW (problem 0, in S K slices when that balances
+// better) and dX (problem 1) in one persistent grid of `cus` blocks, dealt by
+// the static schedule of gemm_sched.hpp.  The plan compares, in the rounds
+// cost model's steps, the schedule's makespan (plus the slice reduce) with
+// the two launches it replaces: dX's rounds plus dW's own plan.
+struct GroupPlan {
+    bool grouped;
+    int S, L;
+};
+
+static int64_t group_makespan(int cus, int64_t units0, int c0, int64_t units1, int c1) {
+    const GroupSched gs{cus, (int)units0, c0, (int)units1, c1};
+    int64_t mk = 0;
+    for (int b = 0; b < cus; ++b) mk = std::max(mk, gs_finish(gs, b));
+    return mk;
+}
+
+static GroupPlan grouped_plan(const GemmArgs& dw, const GemmArgs& dx, size_t ws_bytes, int cus) {
+    constexpr double kOverheadSteps = kUnitOverhead;
+    const double red_steps_per_byte = 2.0 / 10e6;
+    const int nk0 = (dw.K + kPKB - 1) / kPKB, nk1 = (dx.K + kPKB - 1) / kPKB;
+    const int64_t t0 = (int64_t)((dw.M + kPBM - 1) / kPBM) * ((dw.N + kPBN - 1) / kPBN);
+    const int64_t t1 = (int64_t)((dx.M + kPBM - 1) / kPBM) * ((dx.N + kPBN - 1) / kPBN);
+    // the two launches it replaces
+    double separate = (double)((t1 + cus - 1) / cus) * (nk1 + kOverheadSteps);
+    if (t0 >= cus) {
+        separate += (double)((t0 + cus - 1) / cus) * (nk0 + kOverheadSteps);
+    } else {
+        const PSplit ps = persistent_split_plan(dw.M, dw.N, dw.K, ws_bytes, cus);
+        separate += (double)((t0 * ps.S + cus - 1) / cus) * (ps.L + kOverheadSteps);
+        if (ps.S > 1) separate += (double)(ps.S + 1) * dw.M * dw.N * sizeof(float) * red_steps_per_byte;
+    }
+    GroupPlan best{false, 1, nk0};
+    double best_cost = separate;
+    for (int s = 1; s <= 8; ++s) {
+        const int span = (nk0 + s - 1) / s;
+        if (s > 1 && span < 4) break;
+        const int se = (nk0 + span - 1) / span;
+        if (se > 1 && (size_t)se * dw.M * dw.N * sizeof(float) > ws_bytes) break;
+        double cost = (double)group_makespan(cus, t0 * se, span + kUnitOverhead, t1, nk1 + kUnitOverhead);
+        if (se > 1) cost += (double)(se + 1) * dw.M * dw.N * sizeof(float) * red_steps_per_byte;
+        if (cost < best_cost * 0.97) {
+            best_cost = cost;
+            best = GroupPlan{true, se, span};
+        }
+    }
+    return best;
+}
+
+template <typename DwT, typename DxT>
+static void launch_grouped(const GemmArgs& dw, const GemmArgs& dx, const GroupPlan& gp, int cus) {
+    const PProb p1{dx.A, dx.B, dx.C, dx.sa, dx.sb, dx.lda, dx.ldb, dx.M, dx.N, dx.K, dx.ldc,
+                   ((int64_t)dx.ldc * (int64_t)sizeof(DxT)) % 16 == 0 && aligned16(dx.C)};
+    if (gp.S == 1) {
+        const int vec_out = ((int64_t)dw.ldc * (int64_t)sizeof(DwT)) % 16 == 0 && aligned16(dw.C);
+        gemm_nt_persistent_kernel<E5M2, E4M3, DwT, float, false, false, DxT><<<cus, 512, 0, dw.st>>>(
+            dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, static_cast<DwT*>(dw.C), dw.ldc,
+            vec_out, 0, 1, p1);
+        return;
+    }
+    gemm_nt_persistent_kernel<E5M2, E4M3, float, float, false, true, DxT><<<cus, 512, 0, dw.st>>>(
+        dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, dw.ws, dw.N, dw.N % 4 == 0, gp.L, gp.S,
+        p1);
+    const int64_t total = (int64_t)dw.M * dw.N;
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+    const bool vec_red = (dw.N % 4 == 0) && ((int64_t)dw.ldc * (int64_t)sizeof(DwT)) % 16 == 0 && aligned16(dw.C);
+    splitk_reduce_kernel<DwT, float><<<blocks, 256, 0, dw.st>>>(dw.ws, gp.S, dw.M, dw.N, dw.sa, dw.sb, nullptr,
+                                                                 static_cast<DwT*>(dw.C), dw.ldc, vec_red);
+}
+
 template <int FA, int FB>
 static void dispatch_out(const GemmArgs& g, int bias_dtype, int c_dtype) {
     const bool bf16_bias = g.bias && bias_dtype == DF_DTYPE_BFLOAT16;
@@ -1048,29 +1185,44 @@ extern "C" size_t df_fp8_gemm_workspace_bytes(int M, int N, int K) {
     return need;
 }
 
+// Argument checks of one NT GEMM; on success fills g (empty: nothing to
+// compute, M or N is 0).
+static int nt_args(const char* fn, int fmt_a, const uint8_t* A, int lda, int fmt_b, const uint8_t* B, int ldb,
+                   int M, int N, int K, const float* scale_a_dev, const float* scale_b_dev, int bias_dtype,
+                   const void* bias, int c_dtype, void* C, int ldc, void* ws, size_t ws_bytes, void* stream,
+                   GemmArgs& g, bool& empty) {
+    DF_CHECK(M >= 0 && N >= 0 && K >= 0, DF_ERR_INVALID, "%s: negative size M=%d N=%d K=%d", fn, M, N, K);
+    DF_CHECK((fmt_a == E4M3 || fmt_a == E5M2) && (fmt_b == E4M3 || fmt_b == E5M2), DF_ERR_UNSUPPORTED,
+             "%s: bad fp8 formats %d %d", fn, fmt_a, fmt_b);
+    DF_CHECK(c_dtype == DF_DTYPE_FLOAT32 || c_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
+             "%s: output dtype %d not supported", fn, c_dtype);
+    DF_CHECK(!bias || bias_dtype == DF_DTYPE_FLOAT32 || bias_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
+             "%s: bias dtype %d not supported", fn, bias_dtype);
+    DF_CHECK(ldc >= N, DF_ERR_INVALID, "%s: ldc=%d < N=%d", fn, ldc, N);
+    empty = M == 0 || N == 0;
+    if (empty) return DF_OK;
+    DF_CHECK(A && B && C && scale_a_dev && scale_b_dev, DF_ERR_INVALID, "%s: NULL pointer", fn);
+    DF_CHECK(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0, DF_ERR_ALIGN,
+             "%s: lda=%d ldb=%d must be multiples of 16 and >= K=%d", fn, lda, ldb, K);
+    DF_CHECK(aligned16(A) && aligned16(B), DF_ERR_ALIGN, "%s: A and B must be 16-byte aligned", fn);
+    DF_CHECK(!ws || aligned16(ws), DF_ERR_ALIGN, "%s: workspace must be 16-byte aligned", fn);
+    // K is rounded up to the 16-byte granule: the operand rows are zero
+    // there (df_quantize_2d pads ld with zeros), so the products vanish.
+    g = GemmArgs{A, lda, B, ldb, M, N, (K + 15) & ~15, scale_a_dev, scale_b_dev, bias, C, ldc,
+                 static_cast<float*>(ws), ws ? ws_bytes : 0, as_stream(stream)};
+    return DF_OK;
+}
+
 extern "C" int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda, int fmt_b, const uint8_t* B,
                               int ldb, int M, int N, int K, const float* scale_a_dev,
                               const float* scale_b_dev, int bias_dtype, const void* bias,
                               int c_dtype, void* C, int ldc, void* ws, size_t ws_bytes, void* stream) {
     clear_error();
-    DF_CHECK(M >= 0 && N >= 0 && K >= 0, DF_ERR_INVALID, "df_fp8_gemm_nt: negative size M=%d N=%d K=%d", M, N, K);
-    DF_CHECK((fmt_a == E4M3 || fmt_a == E5M2) && (fmt_b == E4M3 || fmt_b == E5M2), DF_ERR_UNSUPPORTED,
-             "df_fp8_gemm_nt: bad fp8 formats %d %d", fmt_a, fmt_b);
-    DF_CHECK(c_dtype == DF_DTYPE_FLOAT32 || c_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
-             "df_fp8_gemm_nt: output dtype %d not supported", c_dtype);
-    DF_CHECK(!bias || bias_dtype == DF_DTYPE_FLOAT32 || bias_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
-             "df_fp8_gemm_nt: bias dtype %d not supported", bias_dtype);
-    DF_CHECK(ldc >= N, DF_ERR_INVALID, "df_fp8_gemm_nt: ldc=%d < N=%d", ldc, N);
-    if (M == 0 || N == 0) return DF_OK;
-    DF_CHECK(A && B && C && scale_a_dev && scale_b_dev, DF_ERR_INVALID, "df_fp8_gemm_nt: NULL pointer");
-    DF_CHECK(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0, DF_ERR_ALIGN,
-             "df_fp8_gemm_nt: lda=%d ldb=%d must be multiples of 16 and >= K=%d", lda, ldb, K);
-    DF_CHECK(aligned16(A) && aligned16(B), DF_ERR_ALIGN, "df_fp8_gemm_nt: A and B must be 16-byte aligned");
-    DF_CHECK(!ws || aligned16(ws), DF_ERR_ALIGN, "df_fp8_gemm_nt: workspace must be 16-byte aligned");
-    // K is rounded up to the 16-byte granule: the operand rows are zero
-    // there (df_quantize_2d pads ld with zeros), so the products vanish.
-    GemmArgs g{A, lda, B, ldb, M, N, (K + 15) & ~15, scale_a_dev, scale_b_dev, bias, C, ldc,
-               static_cast<float*>(ws), ws ? ws_bytes : 0, as_stream(stream)};
+    GemmArgs g;
+    bool empty = false;
+    const int st = nt_args("df_fp8_gemm_nt", fmt_a, A, lda, fmt_b, B, ldb, M, N, K, scale_a_dev, scale_b_dev,
+                           bias_dtype, bias, c_dtype, C, ldc, ws, ws_bytes, stream, g, empty);
+    if (st != DF_OK || empty) return st;
     if (fmt_a == E4M3 && fmt_b == E4M3) dispatch_out<E4M3, E4M3>(g, bias_dtype, c_dtype);
     else if (fmt_a == E5M2 && fmt_b == E4M3) dispatch_out<E5M2, E4M3>(g, bias_dtype, c_dtype);
     else if (fmt_a == E4M3 && fmt_b == E5M2) dispatch_out<E4M3, E5M2>(g, bias_dtype, c_dtype);
@@ -1102,4 +1254,72 @@ extern "C" int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* 
     // dW[N,K] = sum_m dY[m,n] X[m,k]: NT with reduction M, A = dY^T [N, M], B = X^T [K, M]
     return df_fp8_gemm_nt(DF_FMT_E5M2, dYtq, ldyt, DF_FMT_E4M3, Xtq, ldxt, N, K, M, sdy_dev, sx_dev,
                           DF_DTYPE_FLOAT32, nullptr, dw_dtype, dW, lddw, ws, ws_bytes, stream);
+}
+
+// dW [N, K] in NT form: A = dY^T [N, M], B = X^T [K, M], reduction M;
+// dX [M, K]: A = dY [M, N], B = W^T [K, N], reduction N.
+static void bwd_shapes(int M, int N, int K, GemmArgs& dw, GemmArgs& dx) {
+    dw = GemmArgs{};
+    dx = GemmArgs{};
+    dw.M = N, dw.N = K, dw.K = (M + 15) & ~15;
+    dx.M = M, dx.N = K, dx.K = (N + 15) & ~15;
+}
+
+extern "C" size_t df_fp8_gemm_bwd_workspace_bytes(int M, int N, int K) {
+    size_t need = std::max(df_fp8_gemm_workspace_bytes(M, K, N), df_fp8_gemm_workspace_bytes(N, K, M));
+    const int cus = device_cu_count();
+    if (cus > 0 && M > 0 && N > 0 && K > 0) {
+        GemmArgs dw, dx;
+        bwd_shapes(M, N, K, dw, dx);
+        const GroupPlan gp = grouped_plan(dw, dx, SIZE_MAX, cus);
+        if (gp.grouped && gp.S > 1) need = std::max(need, (size_t)gp.S * (size_t)N * (size_t)K * sizeof(float));
+    }
+    return need;
+}
+
+extern "C" int df_fp8_gemm_bwd_plan(int M, int N, int K, size_t ws_bytes, int* grouped, int* dw_slices) {
+    clear_error();
+    DF_CHECK(grouped && dw_slices, DF_ERR_INVALID, "df_fp8_gemm_bwd_plan: NULL output");
+    *grouped = 0;
+    *dw_slices = 0;
+    const int cus = device_cu_count();
+    if (cus <= 0 || M <= 0 || N <= 0 || K <= 0) return DF_OK;
+    GemmArgs dw, dx;
+    bwd_shapes(M, N, K, dw, dx);
+    const GroupPlan gp = grouped_plan(dw, dx, ws_bytes, cus);
+    *grouped = gp.grouped ? 1 : 0;
+    *dw_slices = gp.grouped ? gp.S : 0;
+    return DF_OK;
+}
+
+extern "C" int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, const uint8_t* dYtq,
+                               int ldyt, const uint8_t* Xtq, int ldxt, int M, int N, int K, const float* sdy_dev,
+                               const float* sw_dev, const float* sx_dev, int dx_dtype, void* dX, int lddx,
+                               int dw_dtype, void* dW, int lddw, void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    GemmArgs dx, dw;
+    bool ex = false, ew = false;
+    int st = nt_args("df_fp8_gemm_bwd (dX)", DF_FMT_E5M2, dYq, lddy, DF_FMT_E4M3, Wtq, ldwt, M, K, N, sdy_dev,
+                     sw_dev, DF_DTYPE_FLOAT32, nullptr, dx_dtype, dX, lddx, ws, ws_bytes, stream, dx, ex);
+    if (st != DF_OK) return st;
+    st = nt_args("df_fp8_gemm_bwd (dW)", DF_FMT_E5M2, dYtq, ldyt, DF_FMT_E4M3, Xtq, ldxt, N, K, M, sdy_dev, sx_dev,
+                 DF_DTYPE_FLOAT32, nullptr, dw_dtype, dW, lddw, ws, ws_bytes, stream, dw, ew);
+    if (st != DF_OK) return st;
+    const int cus = device_cu_count();
+    GroupPlan gp{false, 1, 0};
+    if (!ex && !ew && M > 0 && N > 0 && cus > 0 && persistent_ok(dx) && persistent_ok(dw))
+        gp = grouped_plan(dw, dx, dw.ws ? dw.ws_bytes : 0, cus);
+    if (!gp.grouped) {
+        st = df_fp8_gemm_bwd_dx(dYq, lddy, Wtq, ldwt, M, N, K, sdy_dev, sw_dev, dx_dtype, dX, lddx, ws, ws_bytes,
+                                stream);
+        if (st != DF_OK) return st;
+        return df_fp8_gemm_bwd_dw(dYtq, ldyt, Xtq, ldxt, M, N, K, sdy_dev, sx_dev, dw_dtype, dW, lddw, ws, ws_bytes,
+                                  stream);
+    }
+    const bool dw32 = dw_dtype == DF_DTYPE_FLOAT32, dx32 = dx_dtype == DF_DTYPE_FLOAT32;
+    if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus);
+    else if (dw32) launch_grouped<float, uint16_t>(dw, dx, gp, cus);
+    else if (dx32) launch_grouped<uint16_t, float>(dw, dx, gp, cus);
+    else launch_grouped<uint16_t, uint16_t>(dw, dx, gp, cus);
+    return launch_status("df_fp8_gemm_bwd");
 }

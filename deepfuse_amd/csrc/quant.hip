@@ -125,13 +125,25 @@ __device__ __forceinline__ float scale_from_absmax(float am, int fmt) {
 }
 
 // Stage 2: one block folds the partials, writes absmax and (optionally) scale.
+// This thread's max over partial[threadIdx.x + k * kThreads]: eight
+// independent loads in flight per iteration (one iteration for 2048
+// partials), not one load-then-max chain per partial.
+__device__ __forceinline__ uint32_t fold_parts(const uint32_t* __restrict__ partial, int nparts) {
+    uint32_t m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = threadIdx.x;
+    for (; i + 7 * kThreads < nparts; i += 8 * kThreads) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) m[u] = max(m[u], partial[i + u * kThreads]);
+    }
+    for (; i < nparts; i += kThreads) m[0] = max(m[0], partial[i]);
+    return max(max(max(m[0], m[1]), max(m[2], m[3])), max(max(m[4], m[5]), max(m[6], m[7])));
+}
+
 __global__ __launch_bounds__(kThreads) void absmax_stage2(const uint32_t* __restrict__ partial,
                                                            int nparts, int fmt,
                                                            float* __restrict__ absmax_out,
                                                            float* __restrict__ scale_out) {
-    uint32_t m = 0;
-    for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
-    m = block_max_u32(m);
+    uint32_t m = block_max_u32(fold_parts(partial, nparts));
     if (threadIdx.x == 0) {
         const float am = __uint_as_float(m);
         if (absmax_out) absmax_out[0] = am;
@@ -566,9 +578,7 @@ __global__ __launch_bounds__(kThreads) void amax_history_kernel(const uint32_t* 
                                                                  int fmt, float* __restrict__ history, int len,
                                                                  float* __restrict__ scale_out) {
     __shared__ uint32_t cur;
-    uint32_t m = 0;
-    for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
-    m = block_max_u32(m);
+    const uint32_t m = block_max_u32(fold_parts(partial, nparts));
     if (threadIdx.x == 0) cur = m;
     constexpr int PER = kMaxHistory / kThreads;
     float old[PER];

@@ -280,14 +280,12 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
         quantize_operand(grad_output.data(), N, out_features_, DF_FMT_E5M2, sc + 2, dyq, Op, dyt, Np, db);
     }
     tensor<TT> grad_input({N, in_features_});
-    const size_t gb = std::max(df_fp8_gemm_workspace_bytes(N, in_features_, out_features_),
-                               df_fp8_gemm_workspace_bytes(out_features_, in_features_, N));
+    // dX (fc_backward_input) and dW (fc_backward_weights) in one launch
+    const size_t gb = df_fp8_gemm_bwd_workspace_bytes(N, out_features_, in_features_);
     uint8_t* gws = gemm_ws_.get(gb);
-    CHECK_DF_EX(df_fp8_gemm_bwd_dx(dyq, Op, wt, Op, N, out_features_, in_features_, sdy, sw, dt, grad_input.data(),
-                                   in_features_, gws, gb, st()));
-    CHECK_DF_EX(df_fp8_gemm_bwd_dw(dyt, Np, reinterpret_cast<const uint8_t*>(xt_cache_->data()), Np, N,
-                                   out_features_, in_features_, sdy, sx, dt, this->grad_weights_.data(), in_features_,
-                                   gws, gb, st()));
+    CHECK_DF_EX(df_fp8_gemm_bwd(dyq, Op, wt, Op, dyt, Np, reinterpret_cast<const uint8_t*>(xt_cache_->data()), Np, N,
+                                out_features_, in_features_, sdy, sw, sx, dt, grad_input.data(), in_features_, dt,
+                                this->grad_weights_.data(), in_features_, gws, gb, st()));
     CHECK_DF_EX(df_convert(DF_DTYPE_FLOAT32, db, dt, this->grad_bias_.data(), out_features_, st()));
     return grad_input;
 }

@@ -248,6 +248,32 @@ int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ld
                        int M, int N, int K, const float* sdy_dev, const float* sx_dev,
                        int dw_dtype, void* dW, int lddw,
                        void* ws, size_t ws_bytes, void* stream);
+/* dX and dW of one Linear in one launch: the arguments of df_fp8_gemm_bwd_dx
+ * and df_fp8_gemm_bwd_dw together (M tokens, N outputs, K inputs).  The dW
+ * GEMM has few output tiles (6400 x 1600: 175 of 256 x 256 for 256 CUs), so
+ * its launch alone leaves CUs idle; here one persistent grid takes dW's work
+ * units first and deals dX's tiles to the CUs as they free up (a static
+ * schedule, no atomics).  dX is bit-identical to df_fp8_gemm_bwd_dx; dW to
+ * df_fp8_gemm_bwd_dw whenever both split its K range alike (they may pick
+ * different slice counts, which changes dW's fp32 rounding, within the
+ * 1e-4 bar either way).  Falls back to the two calls where the grouped
+ * launch does not apply (degenerate sizes, operands beyond 2^31 bytes) or
+ * would not be faster.  ws: df_fp8_gemm_bwd_workspace_bytes(M, N, K) never
+ * limits the plan; smaller only narrows it.  Together these replace
+ * fc_backward_input and fc_backward_weights (fully_connected_layer.cu:43-89)
+ * as FullyConnectedLayer::backward launches them (:310-338). */
+size_t df_fp8_gemm_bwd_workspace_bytes(int M, int N, int K);
+/* The plan df_fp8_gemm_bwd takes for these sizes, a workspace of ws_bytes
+ * and operands with the smallest leading dimensions: *grouped = 1 for the
+ * one grouped launch (then *dw_slices = the K slices of dW, 1 = unsplit),
+ * 0 for the two separate calls (*dw_slices = 0). */
+int df_fp8_gemm_bwd_plan(int M, int N, int K, size_t ws_bytes, int* grouped, int* dw_slices);
+int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
+                    const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ldxt,
+                    int M, int N, int K, const float* sdy_dev, const float* sw_dev,
+                    const float* sx_dev, int dx_dtype, void* dX, int lddx,
+                    int dw_dtype, void* dW, int lddw,
+                    void* ws, size_t ws_bytes, void* stream);
 
 /* ---- layer weight streaming (new: the reference describes layer-serialized
  * execution, README.md:212-226, and has its host-side pieces in the NVMe

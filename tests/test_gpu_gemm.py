@@ -213,3 +213,66 @@ def test_split_k_matches_unsplit(dev, M, N, K):
     assert orc.rel_err(with_ws, no_ws) <= 1e-5
     if (M, N) in ((1600, 1600), (384, 200)):
         assert df.lib().df_fp8_gemm_workspace_bytes(M, N, K) > 0  # these two do take split-K
+
+
+def grouped_case(dev, M, K, N, seed, rows=None, wrows=None, wcols=None, out16=False):
+    """df_fp8_gemm_bwd against the two separate calls on the same codes:
+    dX bit-identical, dW within 1e-5 (the launches may cut dW's K range into
+    different slices) and both against the oracle at the 1e-4 bar."""
+    X = synth.normal((M, K), 1.0, seed=seed)
+    W = synth.normal((N, K), 0.02, seed=seed + 1)
+    dY = synth.normal((M, N), 1e-3, seed=seed + 2)
+    _, xt, sx, Xd = quant_operand(X, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    _, wt, sw, Wd = quant_operand(W, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    dyq, dyt, sdy, dYd = quant_operand(dY, Fmt.E5M2, dev, want_q=True, want_qt=True)
+    dX, dW = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx)
+    dX_sep = df.gemm_nt(dyq, Fmt.E5M2, wt, Fmt.E4M3, N, sdy, sw)
+    dW_sep = df.gemm_nt(dyt, Fmt.E5M2, xt, Fmt.E4M3, M, sdy, sx)
+    assert torch.equal(dX, dX_sep)
+    assert orc.rel_err(dW.cpu().numpy(), dW_sep.cpu().numpy()) <= 1e-5
+    idx = np.arange(M) if rows is None else np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+    assert orc.rel_err(dX.cpu().numpy()[idx], orc.fc_backward_input(dYd[idx], Wd)) <= TOL
+    o_idx = np.arange(N) if wrows is None else np.sort(np.random.default_rng(seed + 9).choice(N, wrows, replace=False))
+    i_idx = np.arange(K) if wcols is None else np.sort(np.random.default_rng(seed + 8).choice(K, wcols, replace=False))
+    refw = orc.fc_backward_weights(np.ascontiguousarray(dYd[:, o_idx]), np.ascontiguousarray(Xd[:, i_idx]))
+    assert orc.rel_err(dW.cpu().numpy()[np.ix_(o_idx, i_idx)], refw) <= TOL
+    if out16:
+        dX16, dW16 = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, dx_dtype=torch.bfloat16,
+                                 dw_dtype=torch.bfloat16)
+        check_bf16_image(dX, dX16)
+        check_bf16_image(dW, dW16)
+
+
+@pytest.mark.parametrize("K,N", GPT2_XL)
+def test_grouped_backward_config4(dev, K, N):
+    """Config 4 (M = 16384): every XL Linear takes the grouped launch, fc and
+    proj with dW unsplit, qkv and attn_proj as the plan decides."""
+    M = 16384
+    grouped, slices = df.gemm_bwd_plan(M, N, K)
+    assert grouped and slices >= 1
+    grouped_case(dev, M, K, N, seed=synth.SEED_BASE + 77 + K + N, rows=24, wrows=8, wcols=64, out16=(N == 1600))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4, 3), (64, 768, 3072), (129, 272, 257), (4096, 1600, 1600),
+                                   (2048, 6400, 1600), (8192, 768, 2304)])
+def test_grouped_backward_shapes(dev, M, K, N):
+    """Ragged and small shapes: grouped where the plan finds it faster,
+    the two separate calls otherwise; the results are the same either way."""
+    grouped_case(dev, M, K, N, seed=M + 3 * K + 7 * N, out16=True)
+
+
+def test_grouped_backward_without_workspace(dev):
+    """No workspace: dW cannot be sliced, the plan falls back or groups
+    unsplit, and the outputs still match."""
+    M, K, N = 16384, 1600, 1600
+    assert df.gemm_bwd_plan(M, N, K, 0)[1] in (0, 1)
+    X = synth.normal((M, K), 1.0, seed=31)
+    dY = synth.normal((M, N), 1e-3, seed=32)
+    W = synth.normal((N, K), 0.02, seed=33)
+    _, xt, sx, _ = quant_operand(X, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    _, wt, sw, _ = quant_operand(W, Fmt.E4M3, dev, want_q=False, want_qt=True)
+    dyq, dyt, sdy, _ = quant_operand(dY, Fmt.E5M2, dev, want_q=True, want_qt=True)
+    dX, dW = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, workspace=False)
+    dX2, dW2 = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx)
+    assert torch.equal(dX, dX2)
+    assert orc.rel_err(dW.cpu().numpy(), dW2.cpu().numpy()) <= 1e-5
