@@ -434,8 +434,8 @@ EXTRA_STATS = (
 # kernel's template arguments: <A format, B format, output, bias type, bias,
 # K-split>.
 TRAFFIC_FAMILIES = {
-    "gemm_fwd": ("gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true, false>",),
-    "gemm_dx": ("gemm_nt_persistent_kernel<1, 0, unsigned short, float, false, false>",),
+    "gemm_fwd": ("gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true, false, void>",),
+    "gemm_dx": ("gemm_nt_persistent_kernel<1, 0, unsigned short, float, false, false, void>",),
 }
 
 
@@ -467,8 +467,12 @@ def summarize_profiles():
         rows = list(csv.DictReader(fh))
     lines = ["# rocprofv3 kernel statistics -- bench.py, config 4 (GPT-2 XL Linears fwd+bwd, M=16384)", "",
              "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["stats"], "",
-             "23 steps: 3 warm-up + 20 HIP-graph replays (the timed region) + 20 eager steps with HIP events "
-             "(the per-kernel pass).  Durations in microseconds.", "",
+             "Steps, in order: 3 eager warm-up steps, the HIP-graph capture, 3 warm-up replays, 20 timed "
+             "replays (the timed region); then, for comparison, three alternations of 20 replays of the step with "
+             "separate dX and dW launches and 20 of the grouped step; then 20 eager steps with HIP events (the "
+             "per-kernel pass).  The grouped dX + dW launch is the persistent kernel whose last template argument "
+             "is the dX output type (`unsigned short`); `void` marks single-GEMM launches.  Durations in "
+             "microseconds.", "",
              "| kernel | calls | avg us | min us | max us | % time |", "|---|---|---|---|---|---|"]
     for r in rows:
         lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
