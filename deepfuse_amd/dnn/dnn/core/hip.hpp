@@ -57,7 +57,6 @@ public:
 
 private:
     int id_;
-    Hip* previous_;
 };
 
 class StreamGuard {

@@ -30,7 +30,7 @@ void Device::dump_info(std::ostream& os) const {
        << (total_memory_bytes() >> 20) << " MiB, " << clock_ghz() << " GHz";
 }
 
-Hip::Hip(int device_id) : id_(device_id), previous_(g_current) {
+Hip::Hip(int device_id) : id_(device_id) {
     CHECK_HIP_EX(hipSetDevice(id_));
     CHECK_HIP_EX(hipFree(nullptr));  // force context creation
     g_current = this;
