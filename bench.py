@@ -5,14 +5,16 @@ at GPT-2 XL shapes, as fractions of the fp8 MFMA and HBM rooflines.
 Workload ("config 4"): the four GPT-2 XL Linears
 (d = 1600: qkv 1600->4800, attn proj 1600->1600, fc 1600->6400, proj
 6400->1600) at M = 16384 tokens, forward and backward, on seeded synthetic
-bf16 tensors already resident in HBM.  One step, per Linear:
+bf16 tensors already resident in HBM.  One step: absmax + quantize of the
+four weights W -> e4m3 (both copies) in one df_quantize_2d_batch call
+(--per-linear-weights: per Linear, in its forward), then per Linear:
   forward : absmax + quantize X -> e4m3 (row copy and transposed copy),
-            absmax + quantize W -> e4m3 (both copies),
             Y = Xq . Wq^T * sx * sw + b            (bf16 out, fused bias)
   backward: absmax + quantize dY -> e5m2 (both copies) with db = column
             sums fused into the same pass,
             dX = dYq . W * sdy * sw                  (bf16 out)
             dW = dYq^T . X * sdy * sx                (fp32 out, overwrite)
+            in one grouped launch (--separate-backward: two launches)
 value = GEMM flops of the step (2*M*N*K per GEMM, 12 GEMMs) / step time.
 
 Also reported on the same JSON line:
@@ -36,6 +38,7 @@ HIP-event pair around the K steps.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -61,6 +64,8 @@ def parse():
     p.add_argument("--no-delayed", action="store_true", help="skip the delayed-scaling step leg")
     p.add_argument("--no-producer", action="store_true", help="skip the LayerNorm + quantize leg")
     p.add_argument("--no-config3", action="store_true", help="skip the GPT-2 small forward leg (config 3)")
+    p.add_argument("--per-linear-weights", action="store_true",
+                   help="quantize each weight in its own calls instead of one df_quantize_2d_batch per step")
     p.add_argument("--separate-backward", action="store_true",
                    help="time the backward as separate dX and dW launches instead of df_fp8_gemm_bwd")
     p.add_argument("--vendor-compare", action="store_true",
@@ -192,13 +197,30 @@ def main():
                    sc, q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), db.data_ptr(), cws.data_ptr(),
                    cws.numel(), cur())
 
+    # all four weights in one df_quantize_2d_batch call (three launches)
+    nl = len(layers)
+    w_am = torch.empty(nl, dtype=torch.float32, device=dev)
+    w_sc = torch.empty(nl, dtype=torch.float32, device=dev)
+    qb_ws = torch.empty(L.df_quantize_2d_batch_workspace_bytes(), dtype=torch.uint8, device=dev)
+    iarr = lambda vals: (ctypes.c_int * nl)(*vals)
+    parr = lambda ts: (ctypes.c_void_p * nl)(*[t.data_ptr() for t in ts])
+    qb_args = (parr([l["W"] for l in layers]), iarr([l["N"] for l in layers]), iarr([l["K"] for l in layers]),
+               E4, w_am.data_ptr(), w_sc.data_ptr(), parr([l["Wq"] for l in layers]),
+               iarr([l["Wq"].stride(0) for l in layers]), parr([l["Wt"] for l in layers]),
+               iarr([l["Wt"].stride(0) for l in layers]), qb_ws.data_ptr(), qb_ws.numel())
+
     def step(tm, grouped=not args.separate_backward):
-        for l in layers:
+        if not args.per_linear_weights:
+            tm.run("weights_batch", df.call, "df_quantize_2d_batch", BF, nl, *qb_args, cur())
+        for i, l in enumerate(layers):
             K, N = l["K"], l["N"]
             s = l["sc"].data_ptr()
             sx_am, sx, sw_am, sw, sdy_am, sdy = (s + 4 * j for j in range(6))
             quant(tm, l["X"], M, K, E4, sx_am, sx, l["Xq"], l["Xt"], "act")
-            quant(tm, l["W"], N, K, E4, sw_am, sw, l["Wq"], l["Wt"], "weight")
+            if args.per_linear_weights:
+                quant(tm, l["W"], N, K, E4, sw_am, sw, l["Wq"], l["Wt"], "weight")
+            else:
+                sw = w_sc.data_ptr() + 4 * i
             tm.run("gemm_fwd", df.call, "df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["Xq"].stride(0),
                    l["Wq"].data_ptr(), l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF,
                    l["Y"].data_ptr(), N, gws.data_ptr(), gws_bytes, cur())
@@ -226,6 +248,10 @@ def main():
         for k in gemm_flops:
             gemm_flops[k] += 2 * f if k == "gemm_bwd" else f
         for tag, r, c in (("act", M, K), ("weight", N, K), ("grad", M, N)):
+            if tag == "weight" and not args.per_linear_weights:
+                # absmax read + quantize read + both code layouts written
+                qbytes["weights_batch"] = qbytes.get("weights_batch", 0) + 2 * r * c + 2 * r * c + 2 * r * c
+                continue
             qbytes["absmax_" + tag] = qbytes.get("absmax_" + tag, 0) + 2 * r * c
             qbytes["quantize2d_" + tag] = qbytes.get("quantize2d_" + tag, 0) + 2 * r * c + 2 * r * c
 

@@ -79,6 +79,9 @@ _SIGS = {
     "df_quantize_2d_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
                                        _vp, _c_int, _vp, _vp, _c_sz, _vp]),
     "df_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_quantize_2d_batch_workspace_bytes": (_c_sz, []),
+    "df_quantize_2d_batch": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      _c_sz, _vp]),
     "df_fp8_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
     "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
@@ -310,6 +313,29 @@ def gemm_bwd(dy_q, wt_q, dyt_q, xt_q, M: int, N: int, K: int, sdy, sw, sx, dx_dt
          _ptr(xt_q), xt_q.stride(0), M, N, K, _ptr(sdy), _ptr(sw), _ptr(sx), dt(dx_dtype), _ptr(dX), K,
          dt(dw_dtype), _ptr(dW), K, _ptr(ws), ws.numel() if ws is not None else 0, _stream())
     return dX, dW
+
+
+def quantize_2d_batch(tensors, fmt: Fmt, want_q=True, want_qt=True):
+    """df_quantize_2d_batch over contiguous 2-D device tensors (fp32 or
+    bf16, one dtype): returns (absmax [count], scale [count], [q], [qt])
+    with q [R, ceil16(C)] and qt [C, ceil16(R)] (None where not wanted)."""
+    torch = _torch()
+    count = len(tensors)
+    dev = tensors[0].device
+    am = torch.empty(count, dtype=torch.float32, device=dev)
+    sc = torch.empty(count, dtype=torch.float32, device=dev)
+    qs = [torch.empty((t.shape[0], round16(t.shape[1])), dtype=torch.uint8, device=dev) if want_q else None
+          for t in tensors]
+    qts = [torch.empty((t.shape[1], round16(t.shape[0])), dtype=torch.uint8, device=dev) if want_qt else None
+           for t in tensors]
+    arr = lambda vals: (_c_int * count)(*vals)
+    ptrs = lambda ts: (_vp * count)(*[_ptr(t) for t in ts])
+    ws = _scratch(dev, int(lib().df_quantize_2d_batch_workspace_bytes()), "qbatch")
+    call("df_quantize_2d_batch", int(_in_dtype(tensors[0])), count, ptrs(tensors), arr([t.shape[0] for t in tensors]),
+         arr([t.shape[1] for t in tensors]), int(fmt), _ptr(am), _ptr(sc), ptrs(qs) if want_q else None,
+         arr([q.stride(0) for q in qs]) if want_q else None, ptrs(qts) if want_qt else None,
+         arr([q.stride(0) for q in qts]) if want_qt else None, _ptr(ws), ws.numel(), _stream())
+    return am, sc, qs, qts
 
 
 def gemm_bwd_plan(M: int, N: int, K: int, ws_bytes: int | None = None):

@@ -10,6 +10,9 @@
 // a type at dnn/core/tensor.cu:489-498).  Semantics: include/df_capi.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "df_common.hpp"
 
 namespace dfk {
@@ -56,14 +59,14 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t m) {
 constexpr int kU = 8;
 constexpr int64_t kChunkVec = (int64_t)kThreads * kU;
 
-// Stage 1, fp32: one partial maximum per block.
-__global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __restrict__ x,
-                                                               int64_t n,
-                                                               uint32_t* __restrict__ partial) {
+// Stage 1 bodies: the block's maximum over its chunks (block bi of nb
+// blocks walking the chunks with a stride of nb).  |x| bit patterns, NaN
+// and infinities skipped (fold_*).
+__device__ __forceinline__ uint32_t absmax_f32_block(const float* __restrict__ x, int64_t n, int bi, int nb) {
     uint32_t m = 0;
     const int64_t nvec = n >> 2;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+    for (int64_t base = (int64_t)bi * kChunkVec; base < nvec; base += (int64_t)nb * kChunkVec) {
         if (base + kChunkVec <= nvec) {
             u32x4 v[kU];
 #pragma unroll
@@ -79,20 +82,17 @@ __global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __res
             }
         }
     }
-    if (blockIdx.x == 0 && threadIdx.x < (n & 3))
+    if (bi == 0 && threadIdx.x < (n & 3))
         m = fold_f32(m, __float_as_uint(x[(nvec << 2) + threadIdx.x]));
-    m = block_max_u32(m);
-    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+    return block_max_u32(m);
 }
 
-// Stage 1, bf16: 16-byte loads hold 8 values.
-__global__ __launch_bounds__(kThreads) void absmax_bf16_stage1(const uint16_t* __restrict__ x,
-                                                                int64_t n,
-                                                                uint32_t* __restrict__ partial) {
+// bf16: 16-byte loads hold 8 values.
+__device__ __forceinline__ uint32_t absmax_bf16_block(const uint16_t* __restrict__ x, int64_t n, int bi, int nb) {
     uint32_t m = 0;
     const int64_t nvec = n >> 3;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+    for (int64_t base = (int64_t)bi * kChunkVec; base < nvec; base += (int64_t)nb * kChunkVec) {
         if (base + kChunkVec <= nvec) {
             u32x4 v[kU];
 #pragma unroll
@@ -109,9 +109,21 @@ __global__ __launch_bounds__(kThreads) void absmax_bf16_stage1(const uint16_t* _
             }
         }
     }
-    if (blockIdx.x == 0 && threadIdx.x < (n & 7))
+    if (bi == 0 && threadIdx.x < (n & 7))
         m = fold_f32(m, (uint32_t)x[(nvec << 3) + threadIdx.x] << 16);
-    m = block_max_u32(m);
+    return block_max_u32(m);
+}
+
+// Stage 1: one partial maximum per block.
+__global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __restrict__ x, int64_t n,
+                                                               uint32_t* __restrict__ partial) {
+    const uint32_t m = absmax_f32_block(x, n, blockIdx.x, gridDim.x);
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void absmax_bf16_stage1(const uint16_t* __restrict__ x, int64_t n,
+                                                                uint32_t* __restrict__ partial) {
+    const uint32_t m = absmax_bf16_block(x, n, blockIdx.x, gridDim.x);
     if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
@@ -430,13 +442,14 @@ template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bo
 __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, int cols, int ldx, bool vec_ok,
                                          const QDiv& d, uint8_t* __restrict__ q, int ldq, uint8_t* __restrict__ qt,
                                          int ldqt, float* __restrict__ colpart, uint32_t* __restrict__ amaxpart,
-                                         const LnArgs& ln, uint8_t* tile, float (*csum)[kT2]) {
+                                         const LnArgs& ln, uint8_t* tile, float (*csum)[kT2], int bx, int by,
+                                         int nbx) {
     constexpr int E = Ld<InT>::E;      // elements per 16-byte load
     constexpr int TPR = kT2 / E;       // threads per tile row
     constexpr int RG = kThreads / TPR; // row groups
     constexpr int RPT = kT2 / RG;      // rows per thread (8 for bf16, 16 for fp32)
     constexpr int TSTRIDE = kT2 + 16;  // LDS tile row (bytes), [column][row]
-    const int r0 = blockIdx.y * kT2, c0 = blockIdx.x * kT2;
+    const int r0 = by * kT2, c0 = bx * kT2;  // tile (bx, by) of a grid nbx tiles wide
     const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
     const int c = c0 + tc;
     const bool full = vec_ok && c + E <= cols;
@@ -561,11 +574,11 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
         float sum = 0.0f;
 #pragma unroll
         for (int g = 0; g < RG; ++g) sum += csum[g][threadIdx.x];
-        colpart[(int64_t)blockIdx.y * cols + c0 + threadIdx.x] = sum;
+        colpart[(int64_t)by * cols + c0 + threadIdx.x] = sum;
     }
     if (AMAX) {
         am = block_max_u32(am);
-        if (threadIdx.x == 0) amaxpart[blockIdx.y * gridDim.x + blockIdx.x] = am;
+        if (threadIdx.x == 0) amaxpart[by * nbx + bx] = am;
     }
 }
 
@@ -738,10 +751,88 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
     const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
     if (!CODES || d.fast)
         q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, true>(x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart,
-                                                          amaxpart, ln, tile, csum);
+                                                          amaxpart, ln, tile, csum, blockIdx.x, blockIdx.y, gridDim.x);
     else
         q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, false>(x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart,
-                                                           amaxpart, ln, tile, csum);
+                                                           amaxpart, ln, tile, csum, blockIdx.x, blockIdx.y,
+                                                           gridDim.x);
+}
+
+// ---- several 2-D tensors in three launches (every Linear's weights after
+// an optimizer step): per-tensor absmax partials, one fold block per
+// tensor, then every tensor's tiles.  Each tensor gets the same scale and
+// codes as df_absmax_scale_* followed by df_quantize_2d would give it.
+constexpr int kBatchMax = 32;  // tensors per launch
+
+struct BatchArgs {
+    int count;
+    const void* x[kBatchMax];  // contiguous [rows, cols]
+    int rows[kBatchMax], cols[kBatchMax];
+    uint8_t* q[kBatchMax];
+    uint8_t* qt[kBatchMax];
+    int ldq[kBatchMax], ldqt[kBatchMax];
+    int vec_ok[kBatchMax];
+    int blk_first[kBatchMax + 1];   // absmax blocks of tensor t: [blk_first[t], blk_first[t+1])
+    int tile_first[kBatchMax + 1];  // 2-D tiles of tensor t, row-major over tiles_x[t] columns
+    int tiles_x[kBatchMax];
+};
+
+// the tensor t with first[t] <= i < first[t+1]
+__device__ __forceinline__ int batch_owner(const int* first, int count, int i) {
+    int lo = 0, hi = count - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (first[mid] <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+template <typename InT>
+__global__ __launch_bounds__(kThreads) void absmax_batch_stage1(const BatchArgs B, uint32_t* __restrict__ partial) {
+    const int t = batch_owner(B.blk_first, B.count, blockIdx.x);
+    const int bi = blockIdx.x - B.blk_first[t], nb = B.blk_first[t + 1] - B.blk_first[t];
+    const int64_t n = (int64_t)B.rows[t] * B.cols[t];
+    uint32_t m;
+    if constexpr (std::is_same<InT, float>::value)
+        m = absmax_f32_block(static_cast<const float*>(B.x[t]), n, bi, nb);
+    else
+        m = absmax_bf16_block(static_cast<const uint16_t*>(B.x[t]), n, bi, nb);
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void absmax_batch_stage2(const BatchArgs B, const uint32_t* __restrict__ partial,
+                                                                 int fmt, float* __restrict__ absmax_out,
+                                                                 float* __restrict__ scale_out) {
+    const int t = blockIdx.x;
+    const uint32_t m = block_max_u32(fold_parts(partial + B.blk_first[t], B.blk_first[t + 1] - B.blk_first[t]));
+    if (threadIdx.x == 0) {
+        const float am = __uint_as_float(m);
+        if (absmax_out) absmax_out[t] = am;
+        scale_out[t] = scale_from_absmax(am, fmt);
+    }
+}
+
+template <typename InT, int FMT>
+__global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const BatchArgs B,
+                                                                      const float* __restrict__ scale) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2 + 16)];
+    __shared__ float csum[1][kT2];
+    const int t = batch_owner(B.tile_first, B.count, blockIdx.x);
+    const int lt = blockIdx.x - B.tile_first[t];
+    const int nbx = B.tiles_x[t], bx = lt % nbx, by = lt / nbx;
+    const InT* x = static_cast<const InT*>(B.x[t]);
+    const int rows = B.rows[t], cols = B.cols[t];
+    const bool vec_ok = B.vec_ok[t] != 0;
+    const QDiv d = make_qdiv(scale[t]);
+    if (d.fast)
+        q2d_tile<InT, FMT, false, true, false, false, true>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t], B.qt[t],
+                                                            B.ldqt[t], nullptr, nullptr, LnArgs(), tile, csum, bx, by,
+                                                            nbx);
+    else
+        q2d_tile<InT, FMT, false, true, false, false, false>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t],
+                                                             B.qt[t], B.ldqt[t], nullptr, nullptr, LnArgs(), tile,
+                                                             csum, bx, by, nbx);
 }
 
 // out[c] = sum over tile rows of colpart[t][c].  A block owns 64 columns;
@@ -1082,6 +1173,91 @@ extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ld
     DF_CHECK(out, DF_ERR_INVALID, "df_colsum: out is NULL");
     return quantize_2d_impl("df_colsum", in_dtype, x, rows, cols, ldx, E4M3, nullptr, nullptr, 0, nullptr, 0, out,
                             ws, ws_bytes, stream);
+}
+
+extern "C" size_t df_quantize_2d_batch_workspace_bytes(void) { return kMaxReduceBlocks * sizeof(uint32_t); }
+
+extern "C" int df_quantize_2d_batch(int in_dtype, int count, const void* const* x, const int* rows, const int* cols,
+                                    int fmt, float* absmax_dev, float* scale_dev, uint8_t* const* q, const int* ldq,
+                                    uint8_t* const* qt, const int* ldqt, void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    const char* name = "df_quantize_2d_batch";
+    DF_CHECK(count >= 0, DF_ERR_INVALID, "%s: count=%d", name, count);
+    if (count == 0) return DF_OK;
+    DF_CHECK(x && rows && cols && scale_dev, DF_ERR_INVALID, "%s: NULL argument", name);
+    DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad format %d", name, fmt);
+    DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
+             "%s: dtype %d not supported", name, in_dtype);
+    DF_CHECK(aligned4(scale_dev) && aligned4(absmax_dev), DF_ERR_ALIGN, "%s: absmax/scale misaligned", name);
+    DF_CHECK(ws && aligned4(ws) && ws_bytes >= df_quantize_2d_batch_workspace_bytes(), DF_ERR_WORKSPACE,
+             "%s: workspace %zu bytes < %zu", name, ws ? ws_bytes : (size_t)0, df_quantize_2d_batch_workspace_bytes());
+    const int esz = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 2;
+    for (int t = 0; t < count; ++t) {
+        uint8_t* qq = q ? q[t] : nullptr;
+        uint8_t* qqt = qt ? qt[t] : nullptr;
+        const bool empty = rows[t] == 0 || cols[t] == 0;
+        DF_CHECK(rows[t] >= 0 && cols[t] >= 0, DF_ERR_INVALID, "%s: tensor %d: bad shape %d x %d", name, t, rows[t],
+                 cols[t]);
+        DF_CHECK(qq || qqt || empty, DF_ERR_INVALID, "%s: tensor %d: no output", name, t);
+        DF_CHECK(x[t] || empty, DF_ERR_INVALID, "%s: tensor %d: x is NULL", name, t);
+        DF_CHECK(aligned16(x[t]), DF_ERR_ALIGN, "%s: tensor %d: x must be 16-byte aligned", name, t);
+        DF_CHECK(!qq || (ldq && ldq[t] >= cols[t] && ldq[t] % 16 == 0 && aligned16(qq)), DF_ERR_ALIGN,
+                 "%s: tensor %d: q needs ldq >= cols, a multiple of 16, and 16-byte alignment", name, t);
+        DF_CHECK(!qqt || (ldqt && ldqt[t] >= rows[t] && ldqt[t] % 16 == 0 && aligned16(qqt)), DF_ERR_ALIGN,
+                 "%s: tensor %d: qt needs ldqt >= rows, a multiple of 16, and 16-byte alignment", name, t);
+        DF_CHECK(q2d_grid(rows[t], cols[t], qq, qq ? ldq[t] : 0, qqt, qqt ? ldqt[t] : 0).y <= 65535, DF_ERR_INVALID,
+                 "%s: tensor %d: rows=%d too large", name, t, rows[t]);
+    }
+    hipStream_t st = as_stream(stream);
+    uint32_t* part = static_cast<uint32_t*>(ws);
+    for (int t0 = 0; t0 < count; t0 += kBatchMax) {
+        BatchArgs B{};
+        B.count = std::min(count - t0, kBatchMax);
+        // absmax blocks in proportion to the tensors' sizes, at least one
+        // each, at most kMaxReduceBlocks in all
+        int64_t total = 0;
+        for (int i = 0; i < B.count; ++i) total += (int64_t)rows[t0 + i] * cols[t0 + i];
+        const int64_t budget = kMaxReduceBlocks - B.count;
+        int bf = 0, tf = 0;
+        for (int i = 0; i < B.count; ++i) {
+            const int t = t0 + i;
+            const int64_t n = (int64_t)rows[t] * cols[t];
+            B.x[i] = x[t];
+            B.rows[i] = rows[t];
+            B.cols[i] = cols[t];
+            B.q[i] = q ? q[t] : nullptr;
+            B.qt[i] = qt ? qt[t] : nullptr;
+            B.ldq[i] = B.q[i] ? ldq[t] : 0;
+            B.ldqt[i] = B.qt[i] ? ldqt[t] : 0;
+            B.vec_ok[i] = ((int64_t)cols[t] * esz) % 16 == 0;
+            const int want = grid_for((n / (16 / esz) + kU - 1) / kU, kMaxReduceBlocks);
+            const int share = total > 0 ? (int)(budget * n / total) : 0;
+            B.blk_first[i] = bf;
+            bf += 1 + std::max(0, std::min(want - 1, share));
+            const dim3 g = q2d_grid(rows[t], cols[t], B.q[i], B.ldq[i], B.qt[i], B.ldqt[i]);
+            B.tile_first[i] = tf;
+            B.tiles_x[i] = g.x > 0 ? (int)g.x : 1;
+            tf += (int)(g.x * g.y);
+        }
+        B.blk_first[B.count] = bf;
+        B.tile_first[B.count] = tf;
+        float* am = absmax_dev ? absmax_dev + t0 : nullptr;
+        float* sc = scale_dev + t0;
+        if (in_dtype == DF_DTYPE_FLOAT32) absmax_batch_stage1<float><<<bf, kThreads, 0, st>>>(B, part);
+        else absmax_batch_stage1<uint16_t><<<bf, kThreads, 0, st>>>(B, part);
+        absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
+        if (tf > 0) {
+            if (in_dtype == DF_DTYPE_FLOAT32) {
+                if (fmt == E4M3) quantize_2d_batch_kernel<float, E4M3><<<tf, kThreads, 0, st>>>(B, sc);
+                else quantize_2d_batch_kernel<float, E5M2><<<tf, kThreads, 0, st>>>(B, sc);
+            } else {
+                if (fmt == E4M3) quantize_2d_batch_kernel<uint16_t, E4M3><<<tf, kThreads, 0, st>>>(B, sc);
+                else quantize_2d_batch_kernel<uint16_t, E5M2><<<tf, kThreads, 0, st>>>(B, sc);
+            }
+        }
+        if (int rc = launch_status(name)) return rc;
+    }
+    return DF_OK;
 }
 
 // ---------------------------------------------------------------- LayerNorm --

@@ -136,6 +136,23 @@ int df_quantize_2d_colsum(int in_dtype, const void* x, int rows, int cols, int l
 int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
               float* out, void* ws, size_t ws_bytes, void* stream);
 
+/* Several contiguous 2-D tensors x[t] [rows[t], cols[t]] (every Linear's
+ * weights after an optimizer step) in three launches instead of three per
+ * tensor: per-tensor absmax and scale into absmax_dev[t] (device array, or
+ * NULL) and scale_dev[t] (device array), then row codes q[t] [rows, ldq[t]]
+ * and transposed codes qt[t] [cols, ldqt[t]] (either pointer array, or any
+ * entry, may be NULL), zero-padded like df_quantize_2d.  Each tensor gets
+ * exactly the scale and codes df_absmax_scale_* followed by df_quantize_2d
+ * gives it.  x, rows, cols, q, ldq, qt and ldqt are HOST arrays of `count`
+ * entries holding device pointers and sizes; x[t] 16-byte aligned.  ws:
+ * df_quantize_2d_batch_workspace_bytes() bytes.  No reference counterpart:
+ * the reference quantizes nothing; per tensor this is a5 + a6. */
+size_t df_quantize_2d_batch_workspace_bytes(void);
+int df_quantize_2d_batch(int in_dtype, int count, const void* const* x, const int* rows,
+                         const int* cols, int fmt, float* absmax_dev, float* scale_dev,
+                         uint8_t* const* q, const int* ldq, uint8_t* const* qt,
+                         const int* ldqt, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- delayed scaling (new: the reference has no quantizer) ----
  * The scale of a tensor comes from an amax history of earlier passes instead
  * of an absmax pass over the current data.  history[0..len) (device, fp32,

@@ -244,3 +244,43 @@ def test_quantize_2d_layouts(dev, fmt):
         flatb = orc.quantize(xb, s, int(fmt))
         assert_bits_equal(qb.cpu().numpy()[:, :cols], flatb, "q bf16")
         assert_bits_equal(qtb.cpu().numpy()[:, :rows], np.ascontiguousarray(flatb.T), "qt bf16")
+
+
+BATCH_SHAPES = [(4800, 1600), (1600, 1600), (0, 5), (1, 1), (129, 257), (6400, 1600), (3, 40), (1600, 6400)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("fmt", [Fmt.E4M3, Fmt.E5M2])
+def test_quantize_2d_batch_matches_single_calls(dev, dtype, fmt):
+    """df_quantize_2d_batch gives every tensor the absmax, scale, row codes
+    and transposed codes that df_absmax_scale + df_quantize_2d give it alone
+    (ragged shapes, an empty tensor, a 1x1, the GPT-2 XL weights)."""
+    rng = np.random.default_rng(7)
+    ts = []
+    for i, (r, c) in enumerate(BATCH_SHAPES):
+        x = (rng.standard_normal((r, c)) * (0.02 * (i + 1))).astype(np.float32)
+        if x.size:
+            x.reshape(-1)[rng.integers(0, x.size)] = 50.0 * (i + 1)  # an outlier sets each tensor's scale
+        t = to_dev_f32(x, dev)
+        ts.append(t if dtype == "f32" else t.to(torch.bfloat16))
+    am, sc, qs, qts = df.quantize_2d_batch(ts, fmt)
+    for i, t in enumerate(ts):
+        a1, s1 = df.absmax_scale(t, fmt)
+        q1, qt1 = df.quantize_2d(t, s1, fmt, want_q=True, want_qt=True)
+        assert am[i].item() == a1.item() and sc[i].item() == s1.item(), f"tensor {i} {tuple(t.shape)}"
+        assert torch.equal(qs[i], q1), f"q of tensor {i} {tuple(t.shape)}"
+        assert torch.equal(qts[i], qt1), f"qt of tensor {i} {tuple(t.shape)}"
+
+
+def test_quantize_2d_batch_many_tensors(dev):
+    """More tensors than one launch holds (32); only row codes asked for."""
+    rng = np.random.default_rng(8)
+    ts = [to_dev_f32(rng.standard_normal((17 + 3 * i, 40 + 8 * i)).astype(np.float32), dev) for i in range(41)]
+    am, sc, qs, qts = df.quantize_2d_batch(ts, Fmt.E4M3, want_qt=False)
+    assert all(q is None for q in qts)
+    for i, t in enumerate(ts):
+        x = t.cpu().numpy()
+        s = orc.scale(orc.absmax(x), int(Fmt.E4M3))
+        assert sc[i].item() == np.float32(s)
+        assert np.array_equal(qs[i].cpu().numpy()[:, :x.shape[1]], orc.quantize(x, s, int(Fmt.E4M3)))
+        assert not qs[i].cpu().numpy()[:, x.shape[1]:].any()  # zero padding
