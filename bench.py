@@ -442,6 +442,9 @@ PROFILE_COMMANDS = {
     "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-producer --no-delayed --no-config3"),
+    "stats_streaming": ("rocprofv3 --kernel-trace --memory-copy-trace --stats --output-format csv "
+                        "-d gpurun_out/prof_streaming -o bench -- python3 bench.py --steps 2 --warmup 1 "
+                        "--no-cpu-baseline --no-conversion --no-optimizer --no-producer --no-delayed --no-config3"),
     "stats_producer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_producer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-optimizer --no-delayed --no-config3"),
@@ -571,7 +574,49 @@ def summarize_profiles():
         with open(os.path.join(prof, fname), "w") as fh:
             fh.write("\n".join(lines) + "\n")
         extra.append(fname)
+    if streaming_summary(out_dir, prof):
+        extra.append("streaming_h2d_copies_config5.md")
     print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)}, extra {extra})")
+
+
+def streaming_summary(out_dir, prof):
+    """profiles/streaming_h2d_copies_config5.md from the stats_streaming run:
+    the weight copies of config 5 (the host-to-device stream that carries
+    2 x layers copies per step, all the same size) and their rate, with the
+    copy size taken from the same run's bench line."""
+    import csv
+    path = os.path.join(out_dir, "prof_streaming", "bench_memory_copy_trace.csv")
+    log = os.path.join(out_dir, "prof_streaming.log")
+    if not (os.path.exists(path) and os.path.exists(log)):
+        return False
+    line = [l for l in open(log) if l.startswith('{"metric"')]
+    if not line:
+        return False
+    st = json.loads(line[-1])["streaming"]
+    with open(path) as fh:
+        rows = [r for r in csv.DictReader(fh) if r["Direction"] == "MEMORY_COPY_HOST_TO_DEVICE"]
+    by_stream = {}
+    for r in rows:
+        by_stream.setdefault(r["Stream_Id"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    sid, durs = max(by_stream.items(), key=lambda kv: len(kv[1]))
+    nbytes = st["copy_bytes"]
+    durs.sort()
+    med = durs[len(durs) // 2]
+    lines = ["# rocprofv3 memory-copy trace -- config 5 weight streaming (48-layer GPT-2 XL Linear stack, 8192 tokens)",
+             "", "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["stats_streaming"],
+             "", f"The streamer's copy stream (stream id {sid}) carries {len(durs)} host-to-device copies of "
+             f"{nbytes / 1e6:.2f} MB (one layer's e4m3 weight codes, W for the forward sweep, W^T for the backward): "
+             "warm-up, the timed steps, and the copies-alone pass.", "",
+             "| quantity | value |", "|---|---|",
+             f"| copies | {len(durs)} |",
+             f"| median / min / max copy | {med:.1f} / {durs[0]:.1f} / {durs[-1]:.1f} us |",
+             f"| rate at the median copy | {nbytes / (med * 1e-6) / 1e9:.1f} GB/s |",
+             f"| same run, bench line: streamed step / compute alone / copies alone | {st['ms_per_step']} / "
+             f"{st['compute_alone_ms']} / {st['h2d_alone_ms']} ms (overlap {st['overlap']}) |",
+             f"| same run, bench line: copies alone rate | {st['h2d_gbs']} GB/s |"]
+    with open(os.path.join(prof, "streaming_h2d_copies_config5.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return True
 
 
 def conversion_bench(torch, df, synth, dev, stream, reps=10):
@@ -1190,7 +1235,7 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
             "compute_alone_tflops": round(step_flops / (compute_ms * 1e-3) / 1e12, 2),
             "compute_alone_graph_ms": round(compute_graph_ms, 3),
             "h2d_alone_ms": round(h2d_ms, 3), "h2d_gbs": round(h2d_bytes / (h2d_ms * 1e-3) / 1e9, 2),
-            "h2d_bytes_per_step": h2d_bytes,
+            "h2d_bytes_per_step": h2d_bytes, "copy_bytes": blob, "copies_per_step": 2 * layers,
             "bound": "pcie" if h2d_ms > compute_ms else "compute",
             "overlap": round(max(h2d_ms, compute_ms) / stream_ms, 4),
             "steps": steps,
