@@ -1036,7 +1036,54 @@ def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
         res[name] = {"ms": round(ms, 3), "bytes_per_param": bpe, "gbs": round(gbs, 1),
                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
     res["fused_saving"] = round(1 - res["fused_clip_adam"]["ms"] / res["clip_then_adam"]["ms"], 3)
-    del P, G, M, V
+
+    # The optimizer step followed by the e4m3 codes of every weight (row and
+    # transposed, for the next step's GEMMs): Adam, then the batched
+    # quantize with its own absmax pass, against Adam measuring the weights'
+    # absmax as it writes them and the batched quantize taking it.  The list
+    # puts the weights first so their absmax values are contiguous.
+    W = P[0::2]
+    order = lambda ts: ts[0::2] + ts[1::2]
+    pp2, gp2, mp2, vp2 = arr(order(P)), arr(order(G)), arr(order(M)), arr(order(V))
+    sizes2 = (ctypes.c_int64 * cnt)(*[t.numel() for t in order(P)])
+    nw = len(W)
+    qw = [torch.empty((t.shape[0], df.round16(t.shape[1])), dtype=torch.uint8, device=dev) for t in W]
+    qtw = [torch.empty((t.shape[1], df.round16(t.shape[0])), dtype=torch.uint8, device=dev) for t in W]
+    am = torch.empty(cnt, dtype=torch.float32, device=dev)
+    wsc = torch.empty(nw, dtype=torch.float32, device=dev)
+    qws = torch.empty(df.lib().df_quantize_2d_batch_workspace_bytes(), dtype=torch.uint8, device=dev)
+    iarr = lambda vals: (ctypes.c_int * nw)(*vals)
+    warr = lambda ts: (ctypes.c_void_p * nw)(*[t.data_ptr() for t in ts])
+    wargs = (warr(W), iarr([t.shape[0] for t in W]), iarr([t.shape[1] for t in W]), 0)
+    codes = (warr(qw), iarr([q.stride(0) for q in qw]), warr(qtw), iarr([q.stride(0) for q in qtw]))
+
+    def adam2(absmax=None):
+        step[0] += 1
+        a = (pp2, gp2, mp2, vp2, sizes2, cnt, 1e-4, 0.9, 0.999, 1e-8, 0.0, step[0], None, 1.0)
+        if absmax is None:
+            df.call("df_adam_update_f32", *a, stream)
+        else:
+            df.call("df_adam_update_absmax_f32", *a, absmax, stream)
+
+    def requant_unfused():
+        adam2()
+        df.call("df_quantize_2d_batch", int(df.DType.FLOAT32), nw, *wargs, None, wsc.data_ptr(), *codes,
+                qws.data_ptr(), qws.numel(), stream)
+
+    def requant_fused():
+        adam2(am.data_ptr())
+        df.call("df_quantize_2d_batch_absmax", int(df.DType.FLOAT32), nw, *wargs, am.data_ptr(), wsc.data_ptr(),
+                *codes, stream)
+
+    nwp = sum(t.numel() for t in W)
+    for name, fn, wbytes in (("adam_then_weight_codes", requant_unfused, 4 + 4 + 2),
+                             ("adam_absmax_then_weight_codes", requant_fused, 4 + 2)):
+        ms = timed(fn)
+        byts = n * 28 + nwp * wbytes
+        res[name] = {"ms": round(ms, 3), "bytes": byts, "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}
+    res["weight_codes_saving"] = round(1 - res["adam_absmax_then_weight_codes"]["ms"]
+                                       / res["adam_then_weight_codes"]["ms"], 3)
+    del P, G, M, V, W, qw, qtw
     torch.cuda.empty_cache()
     return res
 

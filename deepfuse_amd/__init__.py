@@ -82,6 +82,8 @@ _SIGS = {
     "df_quantize_2d_batch_workspace_bytes": (_c_sz, []),
     "df_quantize_2d_batch": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                       _c_sz, _vp]),
+    "df_quantize_2d_batch_absmax": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _vp]),
     "df_fp8_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
     "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
@@ -125,6 +127,8 @@ _SIGS = {
     "df_clip_grad_norm_f32": (_c_int, [_vp, _vp, _c_int, _c_f, _vp, _vp, _c_sz, _vp]),
     "df_adam_update_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_f, _c_f, _c_f, _c_f, _c_f,
                                     _c_int, _vp, _c_f, _vp]),
+    "df_adam_update_absmax_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_f, _c_f, _c_f, _c_f, _c_f,
+                                           _c_int, _vp, _c_f, _vp, _vp]),
 }
 
 _lib = None
@@ -315,14 +319,16 @@ def gemm_bwd(dy_q, wt_q, dyt_q, xt_q, M: int, N: int, K: int, sdy, sw, sx, dx_dt
     return dX, dW
 
 
-def quantize_2d_batch(tensors, fmt: Fmt, want_q=True, want_qt=True):
+def quantize_2d_batch(tensors, fmt: Fmt, want_q=True, want_qt=True, absmax=None):
     """df_quantize_2d_batch over contiguous 2-D device tensors (fp32 or
     bf16, one dtype): returns (absmax [count], scale [count], [q], [qt])
-    with q [R, ceil16(C)] and qt [C, ceil16(R)] (None where not wanted)."""
+    with q [R, ceil16(C)] and qt [C, ceil16(R)] (None where not wanted).
+    With ``absmax`` given (device fp32 [count]) the absmax pass is skipped
+    (df_quantize_2d_batch_absmax) and that tensor is returned."""
     torch = _torch()
     count = len(tensors)
     dev = tensors[0].device
-    am = torch.empty(count, dtype=torch.float32, device=dev)
+    am = torch.empty(count, dtype=torch.float32, device=dev) if absmax is None else absmax
     sc = torch.empty(count, dtype=torch.float32, device=dev)
     qs = [torch.empty((t.shape[0], round16(t.shape[1])), dtype=torch.uint8, device=dev) if want_q else None
           for t in tensors]
@@ -330,11 +336,15 @@ def quantize_2d_batch(tensors, fmt: Fmt, want_q=True, want_qt=True):
            for t in tensors]
     arr = lambda vals: (_c_int * count)(*vals)
     ptrs = lambda ts: (_vp * count)(*[_ptr(t) for t in ts])
-    ws = _scratch(dev, int(lib().df_quantize_2d_batch_workspace_bytes()), "qbatch")
-    call("df_quantize_2d_batch", int(_in_dtype(tensors[0])), count, ptrs(tensors), arr([t.shape[0] for t in tensors]),
-         arr([t.shape[1] for t in tensors]), int(fmt), _ptr(am), _ptr(sc), ptrs(qs) if want_q else None,
-         arr([q.stride(0) for q in qs]) if want_q else None, ptrs(qts) if want_qt else None,
-         arr([q.stride(0) for q in qts]) if want_qt else None, _ptr(ws), ws.numel(), _stream())
+    head = (int(_in_dtype(tensors[0])), count, ptrs(tensors), arr([t.shape[0] for t in tensors]),
+            arr([t.shape[1] for t in tensors]), int(fmt), _ptr(am), _ptr(sc))
+    tail = (ptrs(qs) if want_q else None, arr([q.stride(0) for q in qs]) if want_q else None,
+            ptrs(qts) if want_qt else None, arr([q.stride(0) for q in qts]) if want_qt else None)
+    if absmax is None:
+        ws = _scratch(dev, int(lib().df_quantize_2d_batch_workspace_bytes()), "qbatch")
+        call("df_quantize_2d_batch", *head, *tail, _ptr(ws), ws.numel(), _stream())
+    else:
+        call("df_quantize_2d_batch_absmax", *head, *tail, _stream())
     return am, sc, qs, qts
 
 
@@ -430,15 +440,21 @@ def grad_norm(grads, clip: float | None = None):
 
 
 def adam_update(params, grads, ms, vs, timestep: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
-                weight_decay=0.0, clip_norm=None, max_norm=0.0):
+                weight_decay=0.0, clip_norm=None, max_norm=0.0, absmax=None):
     """One Adam step (AdamOptimizer<float>::step) over fp32 device tensors,
     in place on params, ms and vs; ``clip_norm`` (a device norm from
-    :func:`grad_norm`) applies max_norm / norm to the gradients on the fly."""
+    :func:`grad_norm`) applies max_norm / norm to the gradients on the fly.
+    ``absmax`` (an fp32 device tensor of len(params)) also receives max |p|
+    of each updated tensor (df_adam_update_absmax_f32)."""
     n = len(params)
     assert len(grads) == n and len(ms) == n and len(vs) == n
-    call("df_adam_update_f32", _ptrs(params), _ptrs(grads), _ptrs(ms), _ptrs(vs), _sizes(params), n,
-         float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(timestep),
-         _ptr(clip_norm), float(max_norm), _stream())
+    args = (_ptrs(params), _ptrs(grads), _ptrs(ms), _ptrs(vs), _sizes(params), n, float(lr), float(beta1),
+            float(beta2), float(eps), float(weight_decay), int(timestep), _ptr(clip_norm), float(max_norm))
+    if absmax is None:
+        call("df_adam_update_f32", *args, _stream())
+    else:
+        assert absmax.numel() >= n and absmax.dtype == _torch().float32
+        call("df_adam_update_absmax_f32", *args, _ptr(absmax), _stream())
 
 
 # ----------------------------------------------------------------------------

@@ -40,6 +40,15 @@ template <> struct Fp8<E5M2> {
     static constexpr float fmax = 57344.0f;
 };
 
+// ------------------------------------------------------------ absmax fold --
+// |x| over finite values as an unsigned max of the sign-cleared bit patterns
+// (monotone for non-negative binary32); inf/NaN patterns (>= 0x7F800000)
+// contribute 0.
+__device__ __forceinline__ uint32_t fold_f32(uint32_t m, uint32_t bits) {
+    const uint32_t a = bits & 0x7FFFFFFFu;
+    return max(m, a < 0x7F800000u ? a : 0u);
+}
+
 // ----------------------------------------------------------------- encode --
 // binary32 -> fp8 code in the low byte.  |v| >= max (inf included) saturates,
 // NaN gives sign|0x7F.  Normal targets round the re-biased significand in

@@ -57,6 +57,7 @@ struct AdamList {
     float* v[kAdamList];
     int64_t n[kAdamList];
     int first[kAdamList + 1];
+    int idx[kAdamList];  // position in the caller's list (for the absmax output)
     int count;
 };
 
@@ -186,8 +187,14 @@ static __device__ __forceinline__ void adam1(float& p, float gr, float& m, float
     p = p - h.lr * mh / (__builtin_sqrtf(vh) + h.eps);
 }
 
+// AMAX: also fold max |p| of the updated parameters into absmax[idx] (the
+// binary32 bit patterns of non-negative values order like unsigned integers,
+// so a global unsigned atomic max gives the exact maximum in any order).
+template <bool AMAX>
 __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const AdamHyper h,
-                                                         const float* __restrict__ norm) {
+                                                         const float* __restrict__ norm,
+                                                         uint32_t* __restrict__ absmax) {
+    uint32_t am = 0;
     float f = 1.0f;
     if (norm) {
         const float nv = norm[0];
@@ -228,6 +235,7 @@ __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const
                     rp[k][e] = pp;
                     rm[k][e] = mm;
                     rv[k][e] = ve;
+                    if (AMAX) am = fold_f32(am, __float_as_uint(pp));
                 }
                 __builtin_nontemporal_store(rp[k], pv + i);
                 __builtin_nontemporal_store(rm[k], mv + i);
@@ -241,6 +249,19 @@ __global__ __launch_bounds__(kOThreads) void adam_kernel(const AdamList L, const
             p[i] = pp;
             m[i] = mm;
             v[i] = vv;
+            if (AMAX) am = fold_f32(am, __float_as_uint(pp));
+        }
+    }
+    if (AMAX) {
+        __shared__ uint32_t red[kOThreads / 64];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) am = max(am, (uint32_t)__shfl_xor((int)am, off, 64));
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int w = 1; w < kOThreads / 64; ++w) am = max(am, red[w]);
+            atomicMax(absmax + L.idx[t], am);
         }
     }
 }
@@ -367,17 +388,17 @@ static float bias_correction(float beta, int t) {
     return 1.0f - (float)pow((double)beta, (double)t);
 }
 
-extern "C" int df_adam_update_f32(float* const* params, const float* const* grads, float* const* m,
-                                  float* const* v, const int64_t* sizes, int count, float lr, float beta1,
-                                  float beta2, float eps, float weight_decay, int timestep,
-                                  const float* clip_norm_dev, float max_norm, void* stream) {
+static int adam_impl(const char* fn, float* const* params, const float* const* grads, float* const* m,
+                     float* const* v, const int64_t* sizes, int count, float lr, float beta1, float beta2, float eps,
+                     float weight_decay, int timestep, const float* clip_norm_dev, float max_norm, float* absmax_dev,
+                     void* stream) {
     clear_error();
-    const char* fn = "df_adam_update_f32";
     DF_CHECK(count >= 0, DF_ERR_INVALID, "%s: count = %d is negative", fn, count);
     DF_CHECK(count == 0 || (params && grads && m && v && sizes), DF_ERR_INVALID,
              "%s: a pointer array is NULL", fn);
     DF_CHECK(timestep >= 1, DF_ERR_INVALID, "%s: timestep = %d (the first step is 1)", fn, timestep);
     DF_CHECK(!clip_norm_dev || aligned4(clip_norm_dev), DF_ERR_ALIGN, "%s: clip_norm_dev misaligned", fn);
+    DF_CHECK(aligned4(absmax_dev), DF_ERR_ALIGN, "%s: absmax_dev misaligned", fn);
     if (int rc = check_list(fn, reinterpret_cast<const void* const*>(params), sizes, count, "params")) return rc;
     if (int rc = check_list(fn, reinterpret_cast<const void* const*>(grads), sizes, count, "grads")) return rc;
     if (int rc = check_list(fn, reinterpret_cast<const void* const*>(m), sizes, count, "m")) return rc;
@@ -395,6 +416,11 @@ extern "C" int df_adam_update_f32(float* const* params, const float* const* grad
     h.bc2 = bias_correction(beta2, timestep);
     h.max_norm = max_norm;
     hipStream_t st = as_stream(stream);
+    uint32_t* am = reinterpret_cast<uint32_t*>(absmax_dev);
+    if (am && count > 0) {
+        const uint32_t zero = 0;
+        if (int rc = df_fill(am, count, 4, &zero, stream)) return rc;  // empty tensors stay at 0
+    }
     for (int i0 = 0; i0 < count;) {
         AdamList L{};
         int blocks = 0, c = 0;
@@ -406,13 +432,33 @@ extern "C" int df_adam_update_f32(float* const* params, const float* const* grad
             L.v[c] = v[i0];
             L.n[c] = sizes[i0];
             L.first[c] = blocks;
+            L.idx[c] = i0;
             blocks += (int)chunks(sizes[i0]);
             ++c;
         }
         if (c == 0) break;
         L.first[c] = blocks;
         L.count = c;
-        adam_kernel<<<blocks, kOThreads, 0, st>>>(L, h, clip_norm_dev);
+        if (am) adam_kernel<true><<<blocks, kOThreads, 0, st>>>(L, h, clip_norm_dev, am);
+        else adam_kernel<false><<<blocks, kOThreads, 0, st>>>(L, h, clip_norm_dev, nullptr);
     }
     return launch_status("adam_kernel");
+}
+
+extern "C" int df_adam_update_f32(float* const* params, const float* const* grads, float* const* m,
+                                  float* const* v, const int64_t* sizes, int count, float lr, float beta1,
+                                  float beta2, float eps, float weight_decay, int timestep,
+                                  const float* clip_norm_dev, float max_norm, void* stream) {
+    return adam_impl("df_adam_update_f32", params, grads, m, v, sizes, count, lr, beta1, beta2, eps, weight_decay,
+                     timestep, clip_norm_dev, max_norm, nullptr, stream);
+}
+
+extern "C" int df_adam_update_absmax_f32(float* const* params, const float* const* grads, float* const* m,
+                                         float* const* v, const int64_t* sizes, int count, float lr, float beta1,
+                                         float beta2, float eps, float weight_decay, int timestep,
+                                         const float* clip_norm_dev, float max_norm, float* absmax_dev,
+                                         void* stream) {
+    DF_CHECK(absmax_dev || count == 0, DF_ERR_INVALID, "df_adam_update_absmax_f32: absmax_dev is NULL");
+    return adam_impl("df_adam_update_absmax_f32", params, grads, m, v, sizes, count, lr, beta1, beta2, eps,
+                     weight_decay, timestep, clip_norm_dev, max_norm, absmax_dev, stream);
 }

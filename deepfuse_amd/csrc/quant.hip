@@ -21,13 +21,7 @@ constexpr int kThreads = 256;
 constexpr int kMaxReduceBlocks = 2048;  // partials in the absmax workspace
 
 // ------------------------------------------------------------------ absmax --
-// |x| over finite values as an unsigned max of the sign-cleared bit patterns
-// (monotone for non-negative binary32); inf/NaN patterns (>= 0x7F800000)
-// contribute 0.
-__device__ __forceinline__ uint32_t fold_f32(uint32_t m, uint32_t bits) {
-    const uint32_t a = bits & 0x7FFFFFFFu;
-    return max(m, a < 0x7F800000u ? a : 0u);
-}
+// (fold_f32, the binary32 fold, is in df_common.hpp)
 // two bf16 in one dword: widen each to its binary32 pattern
 __device__ __forceinline__ uint32_t fold_bf16x2(uint32_t m, uint32_t w) {
     const uint32_t hi = w & 0x7FFF0000u;
@@ -813,6 +807,12 @@ __global__ __launch_bounds__(kThreads) void absmax_batch_stage2(const BatchArgs 
     }
 }
 
+// scales from absmax values the caller supplies (df_quantize_2d_batch_absmax)
+__global__ __launch_bounds__(kThreads) void scale_batch_kernel(const float* __restrict__ absmax, int count, int fmt,
+                                                                float* __restrict__ scale_out) {
+    for (int t = threadIdx.x; t < count; t += kThreads) scale_out[t] = scale_from_absmax(absmax[t], fmt);
+}
+
 template <typename InT, int FMT>
 __global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const BatchArgs B,
                                                                       const float* __restrict__ scale) {
@@ -1177,20 +1177,24 @@ extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ld
 
 extern "C" size_t df_quantize_2d_batch_workspace_bytes(void) { return kMaxReduceBlocks * sizeof(uint32_t); }
 
-extern "C" int df_quantize_2d_batch(int in_dtype, int count, const void* const* x, const int* rows, const int* cols,
-                                    int fmt, float* absmax_dev, float* scale_dev, uint8_t* const* q, const int* ldq,
-                                    uint8_t* const* qt, const int* ldqt, void* ws, size_t ws_bytes, void* stream) {
+// absmax_in non-NULL: the per-tensor absmax comes from the caller (no
+// absmax pass, no workspace); else it is measured into absmax_dev.
+static int batch_impl(const char* name, int in_dtype, int count, const void* const* x, const int* rows,
+                      const int* cols, int fmt, const float* absmax_in, float* absmax_dev, float* scale_dev,
+                      uint8_t* const* q, const int* ldq, uint8_t* const* qt, const int* ldqt, void* ws,
+                      size_t ws_bytes, void* stream) {
     clear_error();
-    const char* name = "df_quantize_2d_batch";
     DF_CHECK(count >= 0, DF_ERR_INVALID, "%s: count=%d", name, count);
     if (count == 0) return DF_OK;
     DF_CHECK(x && rows && cols && scale_dev, DF_ERR_INVALID, "%s: NULL argument", name);
     DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad format %d", name, fmt);
     DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
              "%s: dtype %d not supported", name, in_dtype);
-    DF_CHECK(aligned4(scale_dev) && aligned4(absmax_dev), DF_ERR_ALIGN, "%s: absmax/scale misaligned", name);
-    DF_CHECK(ws && aligned4(ws) && ws_bytes >= df_quantize_2d_batch_workspace_bytes(), DF_ERR_WORKSPACE,
-             "%s: workspace %zu bytes < %zu", name, ws ? ws_bytes : (size_t)0, df_quantize_2d_batch_workspace_bytes());
+    DF_CHECK(aligned4(scale_dev) && aligned4(absmax_dev) && aligned4(absmax_in), DF_ERR_ALIGN,
+             "%s: absmax/scale misaligned", name);
+    DF_CHECK(absmax_in || (ws && aligned4(ws) && ws_bytes >= df_quantize_2d_batch_workspace_bytes()),
+             DF_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu", name, ws ? ws_bytes : (size_t)0,
+             df_quantize_2d_batch_workspace_bytes());
     const int esz = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 2;
     for (int t = 0; t < count; ++t) {
         uint8_t* qq = q ? q[t] : nullptr;
@@ -1243,9 +1247,13 @@ extern "C" int df_quantize_2d_batch(int in_dtype, int count, const void* const* 
         B.tile_first[B.count] = tf;
         float* am = absmax_dev ? absmax_dev + t0 : nullptr;
         float* sc = scale_dev + t0;
-        if (in_dtype == DF_DTYPE_FLOAT32) absmax_batch_stage1<float><<<bf, kThreads, 0, st>>>(B, part);
-        else absmax_batch_stage1<uint16_t><<<bf, kThreads, 0, st>>>(B, part);
-        absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
+        if (absmax_in) {
+            scale_batch_kernel<<<1, kThreads, 0, st>>>(absmax_in + t0, B.count, fmt, sc);
+        } else {
+            if (in_dtype == DF_DTYPE_FLOAT32) absmax_batch_stage1<float><<<bf, kThreads, 0, st>>>(B, part);
+            else absmax_batch_stage1<uint16_t><<<bf, kThreads, 0, st>>>(B, part);
+            absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
+        }
         if (tf > 0) {
             if (in_dtype == DF_DTYPE_FLOAT32) {
                 if (fmt == E4M3) quantize_2d_batch_kernel<float, E4M3><<<tf, kThreads, 0, st>>>(B, sc);
@@ -1258,6 +1266,22 @@ extern "C" int df_quantize_2d_batch(int in_dtype, int count, const void* const* 
         if (int rc = launch_status(name)) return rc;
     }
     return DF_OK;
+}
+
+extern "C" int df_quantize_2d_batch(int in_dtype, int count, const void* const* x, const int* rows, const int* cols,
+                                    int fmt, float* absmax_dev, float* scale_dev, uint8_t* const* q, const int* ldq,
+                                    uint8_t* const* qt, const int* ldqt, void* ws, size_t ws_bytes, void* stream) {
+    return batch_impl("df_quantize_2d_batch", in_dtype, count, x, rows, cols, fmt, nullptr, absmax_dev, scale_dev, q,
+                      ldq, qt, ldqt, ws, ws_bytes, stream);
+}
+
+extern "C" int df_quantize_2d_batch_absmax(int in_dtype, int count, const void* const* x, const int* rows,
+                                           const int* cols, int fmt, const float* absmax_dev, float* scale_dev,
+                                           uint8_t* const* q, const int* ldq, uint8_t* const* qt, const int* ldqt,
+                                           void* stream) {
+    DF_CHECK(absmax_dev || count == 0, DF_ERR_INVALID, "df_quantize_2d_batch_absmax: absmax_dev is NULL");
+    return batch_impl("df_quantize_2d_batch_absmax", in_dtype, count, x, rows, cols, fmt, absmax_dev, nullptr,
+                      scale_dev, q, ldq, qt, ldqt, nullptr, 0, stream);
 }
 
 // ---------------------------------------------------------------- LayerNorm --

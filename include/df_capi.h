@@ -152,6 +152,13 @@ int df_quantize_2d_batch(int in_dtype, int count, const void* const* x, const in
                          const int* cols, int fmt, float* absmax_dev, float* scale_dev,
                          uint8_t* const* q, const int* ldq, uint8_t* const* qt,
                          const int* ldqt, void* ws, size_t ws_bytes, void* stream);
+/* The same with the per-tensor absmax given (absmax_dev[t], device array),
+ * e.g. from df_adam_update_absmax_f32: no absmax pass, no workspace; the
+ * scales are formed from it by the D1/D2 rule, as df_compute_scale does. */
+int df_quantize_2d_batch_absmax(int in_dtype, int count, const void* const* x, const int* rows,
+                                const int* cols, int fmt, const float* absmax_dev, float* scale_dev,
+                                uint8_t* const* q, const int* ldq, uint8_t* const* qt,
+                                const int* ldqt, void* stream);
 
 /* ---- delayed scaling (new: the reference has no quantizer) ----
  * The scale of a tensor comes from an amax history of earlier passes instead
@@ -361,6 +368,19 @@ int df_adam_update_f32(float* const* params, const float* const* grads, float* c
                        float beta1, float beta2, float eps, float weight_decay,
                        int timestep, const float* clip_norm_dev, float max_norm,
                        void* stream);
+/* df_adam_update_f32 that also writes absmax_dev[i] (device array of
+ * `count` floats) = max |p| over the finite values of the updated
+ * parameters of tensor i (0 for an empty one): the absmax the next step's
+ * quantization of the weights needs, measured while the update already
+ * holds them in registers instead of in a pass of its own over every
+ * parameter.  The parameters, m and v are bit-identical to
+ * df_adam_update_f32's.  No reference counterpart (the reference has no fp8
+ * weights); pair it with df_quantize_2d_batch_absmax. */
+int df_adam_update_absmax_f32(float* const* params, const float* const* grads, float* const* m,
+                              float* const* v, const int64_t* sizes, int count, float lr,
+                              float beta1, float beta2, float eps, float weight_decay,
+                              int timestep, const float* clip_norm_dev, float max_norm,
+                              float* absmax_dev, void* stream);
 
 /* ---- tensor utilities behind dnn::tensor (dnn/core/tensor.cu:18-52) ---- */
 /* fill_kernel (tensor.cu:19): n elements of elem_bytes (1, 2 or 4) = *value */

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import deepfuse_amd as df
+from deepfuse_amd import Fmt
 from oracle import pyoracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -155,3 +156,47 @@ def test_argument_errors(dev):
     with pytest.raises(df.DFError) as ei:
         df.call("df_grad_norm_f32", df._ptrs([x]), df._sizes([x]), 1, x.data_ptr(), x.data_ptr(), 0, None)
     assert ei.value.status == -5
+
+
+def test_adam_absmax_output(dev):
+    """df_adam_update_absmax_f32: the same parameters, m and v as
+    df_adam_update_f32, plus max |p| of every updated tensor (exact; empty
+    tensors 0); more tensors than one launch holds."""
+    sizes = RAGGED + [7, 4096] * 25
+    rng = np.random.default_rng(31)
+    p0 = [rng.standard_normal(n).astype(np.float32) for n in sizes]
+    g0 = [(rng.standard_normal(n) * 0.5).astype(np.float32) for n in sizes]
+    outs = []
+    for with_absmax in (False, True):
+        p, g = to_dev(p0, dev), to_dev(g0, dev)
+        m = [torch.zeros_like(x) for x in p]
+        v = [torch.zeros_like(x) for x in p]
+        am = torch.full((len(sizes),), -1.0, dtype=torch.float32, device=dev) if with_absmax else None
+        df.adam_update(p, g, m, v, 1, weight_decay=0.01, absmax=am)
+        torch.cuda.synchronize()
+        outs.append((p, m, v, am))
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    am = outs[1][3].cpu().numpy()
+    for i, x in enumerate(outs[1][0]):
+        exp = np.abs(x.cpu().numpy()).max() if x.numel() else 0.0
+        assert am[i] == exp, f"tensor {i} (size {sizes[i]})"
+
+
+def test_adam_absmax_then_batch_quantize(dev):
+    """The optimizer step's absmax feeds df_quantize_2d_batch_absmax: the
+    scales and codes equal df_quantize_2d_batch's own absmax pass."""
+    shapes = [(480, 160), (160, 160), (640, 160), (160, 640)]
+    rng = np.random.default_rng(32)
+    p = [torch.from_numpy(rng.standard_normal(s).astype(np.float32) * 0.02).to(dev) for s in shapes]
+    g = [torch.from_numpy(rng.standard_normal(s).astype(np.float32) * 1e-3).to(dev) for s in shapes]
+    m = [torch.zeros_like(x) for x in p]
+    v = [torch.zeros_like(x) for x in p]
+    am = torch.empty(len(p), dtype=torch.float32, device=dev)
+    df.adam_update(p, g, m, v, 1, absmax=am)
+    a1, s1, q1, qt1 = df.quantize_2d_batch(p, Fmt.E4M3, absmax=am)
+    a2, s2, q2, qt2 = df.quantize_2d_batch(p, Fmt.E4M3)
+    assert torch.equal(a1, a2) and torch.equal(s1, s2)
+    for i in range(len(p)):
+        assert torch.equal(q1[i], q2[i]) and torch.equal(qt1[i], qt2[i])
