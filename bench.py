@@ -365,8 +365,10 @@ def main():
         else:
             d["gbs"] = round(qbytes[k] / (t / args.steps * 1e-3) / 1e9, 1)
         kernels[k] = d
+    weights_batch = None if args.per_linear_weights else (
+        lambda: df.call("df_quantize_2d_batch", BF, nl, *qb_args, cur()))
     delayed = None if args.no_delayed else delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes,
-                                                                    ms_per_step, step_flops)
+                                                                    ms_per_step, step_flops, weights_batch, w_sc)
     qt_ms = sum(per[k][0] for k in qbytes) / args.steps
     q_gbs = sum(qbytes.values()) / (qt_ms * 1e-3) / 1e9
     gemm_ms = sum(per[k][0] for k in gemm_flops) / args.steps
@@ -666,13 +668,17 @@ def conversion_bench(torch, df, synth, dev, stream, reps=10):
     return res
 
 
-def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit_ms, step_flops):
-    """The config-4 step with delayed scaling: every operand (X, W, dY of each
-    Linear) is quantized at the scale of its amax history and measures its
-    own absmax in the same pass (df_quantize_2d_delayed), so the separate
-    absmax passes disappear.  Histories are seeded from the operands' own
-    absmax first.  Two steps are captured per graph (the two scale slots of
-    each operand alternate), replayed args.steps // 2 + 1 times."""
+def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit_ms, step_flops,
+                        weights_batch=None, w_sc=None):
+    """The config-4 step with delayed scaling: every activation and gradient
+    (X, dY of each Linear) is quantized at the scale of its amax history and
+    measures its own absmax in the same pass (df_quantize_2d_delayed), so
+    their separate absmax passes disappear.  The weights are quantized as in
+    the just-in-time step: in one df_quantize_2d_batch call (weights_batch,
+    scales in w_sc), or with --per-linear-weights delayed like the others.
+    Histories are seeded from the operands' own absmax first.  Two steps are
+    captured per graph (the two scale slots of each operand alternate),
+    replayed args.steps // 2 + 1 times."""
     from deepfuse_amd import DType, Fmt
     BF, F32 = int(DType.BFLOAT16), int(DType.FLOAT32)
     E4, E5 = int(Fmt.E4M3), int(Fmt.E5M2)
@@ -708,10 +714,12 @@ def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit
         return used
 
     def step(parity):
-        for l, r in zip(layers, roles):
+        if weights_batch is not None:
+            weights_batch()
+        for i, (l, r) in enumerate(zip(layers, roles)):
             K, N = l["K"], l["N"]
             sx = quant(r["x"], parity)
-            sw = quant(r["w"], parity)
+            sw = quant(r["w"], parity) if weights_batch is None else w_sc.data_ptr() + 4 * i
             df.call("df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["Xq"].stride(0), l["Wq"].data_ptr(),
                     l["Wq"].stride(0), M, N, K, sx, sw, BF, l["b"].data_ptr(), BF, l["Y"].data_ptr(), N,
                     gws.data_ptr(), gws_bytes, cur())
@@ -748,7 +756,8 @@ def delayed_scaling_leg(torch, df, layers, M, args, cur, ws, gws, gws_bytes, jit
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / (2 * reps)
     del graph
-    return {"history": H, "steps": 2 * reps, "ms_per_step": round(ms, 4),
+    return {"history": H, "weights": "per Linear, delayed" if weights_batch is None else "batched, just-in-time",
+            "steps": 2 * reps, "ms_per_step": round(ms, 4),
             "tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
             "speedup_vs_just_in_time": round(jit_ms / ms, 4)}
 
