@@ -829,7 +829,8 @@ def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20):
     Per Linear: absmax + e4m3 codes of X [M, K] and W [N, K] (bf16), then
     the fp8 GEMM with the fused scale, bf16 bias and bf16 output.  Reported:
     each GEMM alone (average launch), the four GEMMs, and the whole forward
-    with its quantization, against the per-shape attainable bound
+    with its quantization (weights per Linear, and all four in one
+    df_quantize_2d_batch call), against the per-shape attainable bound
     min(5.0 PF, AI x 8 TB/s) (AI: fp8 A and B read once, bf16 C written
     once)."""
     import numpy as np
@@ -895,6 +896,32 @@ def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20):
 
     ms = timed(forward)
     res["forward_with_quantize"] = {"ms": round(ms, 4), "tflops": round(tot_flops / (ms * 1e-3) / 1e12, 1)}
+
+    # the same forward with the four weights' codes from one df_quantize_2d_batch call
+    import ctypes
+    nl = len(lin)
+    wsc = torch.empty(nl, dtype=torch.float32, device=dev)
+    qws = torch.empty(df.lib().df_quantize_2d_batch_workspace_bytes(), dtype=torch.uint8, device=dev)
+    iarr = lambda vals: (ctypes.c_int * nl)(*vals)
+    parr = lambda ts: (ctypes.c_void_p * nl)(*[t.data_ptr() for t in ts])
+    wargs = (parr([l["W"] for l in lin]), iarr([l["N"] for l in lin]), iarr([l["K"] for l in lin]), E4, None,
+             wsc.data_ptr(), parr([l["Wq"] for l in lin]), iarr([l["K"] for l in lin]), None, None,
+             qws.data_ptr(), qws.numel())
+
+    def forward_batched():
+        df.call("df_quantize_2d_batch", BF, nl, *wargs, stream)
+        for i, l in enumerate(lin):
+            s = l["sc"].data_ptr()
+            df.call("df_absmax_scale_bf16", l["X"].data_ptr(), l["X"].numel(), E4, s, s + 4, aws.data_ptr(),
+                    aws.numel(), stream)
+            df.call("df_quantize_bf16_e4m3", l["X"].data_ptr(), l["X"].numel(), s + 4, l["Xq"].data_ptr(), stream)
+            df.call("df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["K"], l["Wq"].data_ptr(), l["K"], M, l["N"], l["K"],
+                    s + 4, wsc.data_ptr() + 4 * i, BF, l["b"].data_ptr(), BF, l["Y"].data_ptr(), l["N"],
+                    gws.data_ptr(), gws.numel(), stream)
+
+    ms = timed(forward_batched)
+    res["forward_with_quantize_weights_batched"] = {"ms": round(ms, 4),
+                                                    "tflops": round(tot_flops / (ms * 1e-3) / 1e12, 1)}
     return res
 
 
