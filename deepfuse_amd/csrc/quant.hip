@@ -1235,7 +1235,7 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
             B.ldqt[i] = B.qt[i] ? ldqt[t] : 0;
             B.vec_ok[i] = ((int64_t)cols[t] * esz) % 16 == 0;
             const int want = grid_for((n / (16 / esz) + kU - 1) / kU, kMaxReduceBlocks);
-            const int share = total > 0 ? (int)(budget * n / total) : 0;
+            const int share = total > 0 ? (int)((double)budget * (double)n / (double)total) : 0;
             B.blk_first[i] = bf;
             bf += 1 + std::max(0, std::min(want - 1, share));
             const dim3 g = q2d_grid(rows[t], cols[t], B.q[i], B.ldq[i], B.qt[i], B.ldqt[i]);

@@ -108,3 +108,47 @@ def test_enums_mirror_reference():
     assert [DType.FLOAT32, DType.HALF, DType.INT8, DType.UINT8, DType.BFLOAT16] == [0, 1, 2, 3, 4]
     assert (DType.FP8E4M3, DType.FP8E5M2) == (5, 6)
     assert (Fmt.E4M3, Fmt.E5M2) == (0, 1)
+
+
+def test_grouped_backward_and_batch_argument_errors():
+    F32, BF16 = int(DType.FLOAT32), int(DType.BFLOAT16)
+    # df_fp8_gemm_bwd checks both problems before planning: misaligned dY codes, bad ld, bad dtype
+    args = [FAKE, 32, FAKE, 32, FAKE, 64, FAKE, 64, 64, 32, 32, FAKE, FAKE, FAKE, F32, FAKE, 32, F32, FAKE, 32,
+            None, 0, None]
+    bad = list(args)
+    bad[0] = FAKE + 4
+    assert status("df_fp8_gemm_bwd", *bad) == -4 and "(dX)" in err()
+    bad = list(args)
+    bad[5] = 24  # ldyt not a multiple of 16
+    assert status("df_fp8_gemm_bwd", *bad) == -4 and "(dW)" in err()
+    bad = list(args)
+    bad[17] = int(DType.HALF)  # dW dtype
+    assert status("df_fp8_gemm_bwd", *bad) == -2
+    g, sl = ctypes.c_int(7), ctypes.c_int(7)
+    assert status("df_fp8_gemm_bwd_plan", 0, 10, 10, 0, ctypes.byref(g), ctypes.byref(sl)) == 0
+    assert (g.value, sl.value) == (0, 0)
+    assert status("df_fp8_gemm_bwd_plan", 1, 1, 1, 0, None, None) == -1
+    # df_quantize_2d_batch
+    one_p = (ctypes.c_void_p * 1)(FAKE)
+    one_i = (ctypes.c_int * 1)(16)
+    ws_b = df.lib().df_quantize_2d_batch_workspace_bytes()
+    assert status("df_quantize_2d_batch", BF16, 0, None, None, None, 0, None, None, None, None, None, None, None, 0,
+                  None) == 0  # nothing to do
+    assert status("df_quantize_2d_batch", BF16, -1, None, None, None, 0, None, None, None, None, None, None, None,
+                  0, None) == -1
+    assert status("df_quantize_2d_batch", BF16, 1, one_p, one_i, one_i, 0, None, None, one_p, one_i, None, None,
+                  FAKE, ws_b, None) == -1  # no scale output
+    assert status("df_quantize_2d_batch", BF16, 1, one_p, one_i, one_i, 0, None, FAKE, one_p, one_i, None, None,
+                  None, 0, None) == -5  # no workspace
+    assert status("df_quantize_2d_batch", int(DType.HALF), 1, one_p, one_i, one_i, 0, None, FAKE, one_p, one_i,
+                  None, None, FAKE, ws_b, None) == -2
+    mis = (ctypes.c_void_p * 1)(FAKE + 2)
+    assert status("df_quantize_2d_batch", BF16, 1, mis, one_i, one_i, 0, None, FAKE, one_p, one_i, None, None,
+                  FAKE, ws_b, None) == -4 and "tensor 0" in err()
+    assert status("df_quantize_2d_batch_absmax", BF16, 1, one_p, one_i, one_i, 0, None, FAKE, one_p, one_i, None,
+                  None, None) == -1  # absmax input missing
+    # Adam with absmax: the absmax array is required
+    one_f = (ctypes.c_void_p * 1)(FAKE)
+    one_n = (ctypes.c_int64 * 1)(64)
+    assert status("df_adam_update_absmax_f32", one_f, one_f, one_f, one_f, one_n, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0,
+                  1, None, 0.0, None, None) == -1
