@@ -724,8 +724,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     // Stores one finished tile: scale, bias, conversion to T, the slab pass
     // and the 16-byte row-segment stores (tile: this block's unit index, for
     // the bias slot).
+    // always inlined: when both problems store the same type this lambda is
+    // called from two places, and an outlined copy would take acc by
+    // reference, i.e. through scratch memory
     auto store_tile = [&](auto tag, auto with_bias, typename decltype(tag)::type* const Cu, int Mo, int No,
-                          int ldco, int veco, float sabo, int tile, int tm0, int tn0) {
+                          int ldco, int veco, float sabo, int tile, int tm0,
+                          int tn0) __attribute__((always_inline)) {
         using T = typename decltype(tag)::type;
         constexpr bool BIAS = decltype(with_bias)::value;
         constexpr int ES = (int)sizeof(T);
@@ -774,9 +778,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const bool col_full = veco && scol + 16 / ES <= No;
         const int my_sr = fr % SR, my_pass = fr / SR;
         typedef typename std::conditional<ES == 2, u32x2, f32x4>::type Pk;
-        Pk pk[FM][FN][4];
+        // LDS operations of one wave execute in order, so a pass's reads see
+        // its writes and precede the next pass's writes; the empty asm
+        // statements keep the compiler from reordering them.
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i) {
+            Pk pk[FN][4];
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -785,15 +792,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                     const float v0 = a[4 * g] * sabo + bv[j][g][0], v1 = a[4 * g + 1] * sabo + bv[j][g][1];
                     const float v2 = a[4 * g + 2] * sabo + bv[j][g][2], v3 = a[4 * g + 3] * sabo + bv[j][g][3];
                     if constexpr (ES == 2)
-                        pk[i][j][g] = u32x2{pack_bf16_rne(v0, v1), pack_bf16_rne(v2, v3)};
+                        pk[j][g] = u32x2{pack_bf16_rne(v0, v1), pack_bf16_rne(v2, v3)};
                     else
-                        pk[i][j][g] = f32x4{v0, v1, v2, v3};
+                        pk[j][g] = f32x4{v0, v1, v2, v3};
                 }
-        // LDS operations of one wave execute in order, so a pass's reads see
-        // its writes and precede the next pass's writes; the empty asm
-        // statements keep the compiler from reordering them.
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int p = 0; p < NPASS; ++p) {
                 if (my_pass == p) {
@@ -801,7 +803,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                     for (int j = 0; j < FN; ++j)
 #pragma unroll
                         for (int g = 0; g < 4; ++g)
-                            *reinterpret_cast<Pk*>(slab + my_sr * SROW + (j * 32 + 8 * g + h4) * ES) = pk[i][j][g];
+                            *reinterpret_cast<Pk*>(slab + my_sr * SROW + (j * 32 + 8 * g + h4) * ES) = pk[j][g];
                 }
                 asm volatile("" ::: "memory");
 #pragma unroll
@@ -823,6 +825,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 }
                 asm volatile("" ::: "memory");
             }
+        }
     };
 
     auto epilogue = [&](int tile) {
