@@ -343,8 +343,9 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
 // LDS tile [column][row] that is then stored to qt as 128-byte row segments.
 // Elements outside [rows) x [cols) encode as 0, so the padding of q (columns
 // up to ldq) and of qt (columns up to ldqt) is written in the same pass.
-// With AMAX and without LN (delayed scaling: no absmax or statistics pass
-// has just read x) the loads of x and the stores of q / qt are non-temporal.  On the 16384 x {1600, 4800,
+// NT (default: AMAX without LN, i.e. delayed scaling, where no absmax or
+// statistics pass has just read x) makes the loads of x and the stores of
+// q / qt non-temporal.  On the 16384 x {1600, 4800,
 // 6400} bf16 operands of GPT-2 XL that made the delayed-scaling step 3.5%
 // faster; after an absmax pass the cached re-read of x hits the Infinity
 // Cache and plain accesses are faster.
@@ -449,7 +450,7 @@ template <bool NT, typename T> __device__ __forceinline__ void st_nt(T* p, const
 // absmax see.
 // The tile pass proper, instantiated for both division forms (FAST: see
 // qdiv_t); the kernel below owns the LDS and picks the form once per block.
-template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bool FAST>
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bool FAST, bool NT = AMAX && !LN>
 __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, int cols, int ldx, bool vec_ok,
                                          const QDiv& d, uint8_t* __restrict__ q, int ldq, uint8_t* __restrict__ qt,
                                          int ldqt, float* __restrict__ colpart, uint32_t* __restrict__ amaxpart,
@@ -464,7 +465,6 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
     const int c = c0 + tc;
     const bool full = vec_ok && c + E <= cols;
-    constexpr bool NT = AMAX && !LN;  // x is cold: see above
     uint32_t codes[RPT][E / 4];
     float cs[E];
     uint32_t am = 0;
@@ -832,7 +832,7 @@ __global__ __launch_bounds__(kThreads) void scale_batch_kernel(const float* __re
     for (int t = threadIdx.x; t < count; t += kThreads) scale_out[t] = scale_from_absmax(absmax[t], fmt);
 }
 
-template <typename InT, int FMT>
+template <typename InT, int FMT, bool NT>
 __global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const BatchArgs B,
                                                                       const float* __restrict__ scale) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2 + 16)];
@@ -845,11 +845,11 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const Batch
     const bool vec_ok = B.vec_ok[t] != 0;
     const QDiv d = make_qdiv(scale[t]);
     if (d.fast)
-        q2d_tile<InT, FMT, false, true, false, false, true>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t], B.qt[t],
+        q2d_tile<InT, FMT, false, true, false, false, true, NT>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t], B.qt[t],
                                                             B.ldqt[t], nullptr, nullptr, LnArgs(), tile, csum, bx, by,
                                                             nbx);
     else
-        q2d_tile<InT, FMT, false, true, false, false, false>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t],
+        q2d_tile<InT, FMT, false, true, false, false, false, NT>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t],
                                                              B.qt[t], B.ldqt[t], nullptr, nullptr, LnArgs(), tile,
                                                              csum, bx, by, nbx);
 }
@@ -1273,14 +1273,20 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
             else absmax_batch_stage1<uint16_t><<<bf, kThreads, 0, st>>>(B, part);
             absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
         }
-        if (tf > 0) {
+        // with the caller's absmax no pass has just read x: non-temporal tiles
+        auto tiles = [&](auto nt) {
+            constexpr bool NT = decltype(nt)::value;
             if (in_dtype == DF_DTYPE_FLOAT32) {
-                if (fmt == E4M3) quantize_2d_batch_kernel<float, E4M3><<<tf, kThreads, 0, st>>>(B, sc);
-                else quantize_2d_batch_kernel<float, E5M2><<<tf, kThreads, 0, st>>>(B, sc);
+                if (fmt == E4M3) quantize_2d_batch_kernel<float, E4M3, NT><<<tf, kThreads, 0, st>>>(B, sc);
+                else quantize_2d_batch_kernel<float, E5M2, NT><<<tf, kThreads, 0, st>>>(B, sc);
             } else {
-                if (fmt == E4M3) quantize_2d_batch_kernel<uint16_t, E4M3><<<tf, kThreads, 0, st>>>(B, sc);
-                else quantize_2d_batch_kernel<uint16_t, E5M2><<<tf, kThreads, 0, st>>>(B, sc);
+                if (fmt == E4M3) quantize_2d_batch_kernel<uint16_t, E4M3, NT><<<tf, kThreads, 0, st>>>(B, sc);
+                else quantize_2d_batch_kernel<uint16_t, E5M2, NT><<<tf, kThreads, 0, st>>>(B, sc);
             }
+        };
+        if (tf > 0) {
+            if (absmax_in) tiles(std::true_type());
+            else tiles(std::false_type());
         }
         if (int rc = launch_status(name)) return rc;
     }
