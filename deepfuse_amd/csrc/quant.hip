@@ -776,6 +776,10 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
 // tensor, then every tensor's tiles.  Each tensor gets the same scale and
 // codes as df_absmax_scale_* followed by df_quantize_2d would give it.
 constexpr int kBatchMax = 32;  // tensors per launch
+// Input bytes of one launch beyond which its absmax pass has pushed the
+// first tensors out of the 256 MB Infinity Cache before the tile pass
+// re-reads them: the tile pass then streams (non-temporal accesses).
+constexpr int64_t kBatchColdBytes = (int64_t)256 << 20;
 
 struct BatchArgs {
     int count;
@@ -1273,7 +1277,8 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
             else absmax_batch_stage1<uint16_t><<<bf, kThreads, 0, st>>>(B, part);
             absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
         }
-        // with the caller's absmax no pass has just read x: non-temporal tiles
+        // non-temporal tiles where x is not in cache: no pass has just read it
+        // (the caller's absmax), or the absmax pass read more than it holds
         auto tiles = [&](auto nt) {
             constexpr bool NT = decltype(nt)::value;
             if (in_dtype == DF_DTYPE_FLOAT32) {
@@ -1285,7 +1290,7 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
             }
         };
         if (tf > 0) {
-            if (absmax_in) tiles(std::true_type());
+            if (absmax_in || total * esz > kBatchColdBytes) tiles(std::true_type());
             else tiles(std::false_type());
         }
         if (int rc = launch_status(name)) return rc;
