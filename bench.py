@@ -1130,7 +1130,8 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
     codes in pinned host memory: the forward sweep streams W [N, K] per layer,
     the backward sweep (layers in reverse) streams W^T [K, N] for dX, through
     a ring of `slots` device slots filled on the streamer's copy stream while
-    earlier layers compute (df_streamer_*).  Per layer and Linear the step
+    earlier layers compute (deepfuse_amd.stack.StreamedStack, the same code
+    tests/test_gpu_stream.py checks).  Per layer and Linear the step
     quantizes the activation (e4m3, row copy + the transposed copy cached for
     dW) and the upstream gradient (e5m2, both copies, db fused), and runs the
     forward, dX and dW GEMMs; dW is kept per layer (fp32).
@@ -1138,126 +1139,10 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
     Also timed: the same step with all weights resident in HBM (compute
     alone) and the 2*layers weight copies alone on the copy stream (PCIe
     alone); overlap = max(compute, copies) / streamed."""
-    import ctypes
+    from deepfuse_amd.stack import StreamedStack
 
-    import numpy as np
-
-    from deepfuse_amd import DType, Fmt
-
-    M = tokens
-    r16 = df.round16
-    fwd_off, bwd_off, o1, o2 = [], [], 0, 0
-    for _, K, N in XL_LINEARS:
-        fwd_off.append(o1)
-        o1 += N * r16(K)
-        bwd_off.append(o2)
-        o2 += K * r16(N)
-    blob = max(o1, o2)
-    total_host = 2 * layers * blob
-    hp = ctypes.c_void_p()
-    df.call("df_host_alloc", total_host, ctypes.byref(hp))
-    host = torch.frombuffer((ctypes.c_uint8 * total_host).from_address(hp.value), dtype=torch.uint8)
-    cur = lambda: torch.cuda.current_stream().cuda_stream
+    stack = StreamedStack(torch, dev, layers=layers, tokens=tokens)
     try:
-        # weights: generated on the device (seeded), quantized with the
-        # library's own kernels, then stored as codes in pinned host memory
-        sw = torch.empty((layers, len(XL_LINEARS)), dtype=torch.float32, device=dev)
-        am = torch.empty(1, dtype=torch.float32, device=dev)
-        ws = torch.empty(df.lib().df_absmax_workspace_bytes(), dtype=torch.uint8, device=dev)
-        gen = torch.Generator(device=dev)
-        for l in range(layers):
-            for i, (_, K, N) in enumerate(XL_LINEARS):
-                gen.manual_seed(synth.SEED_BASE + 5000 + 10 * l + i)
-                W = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
-                s_ptr = sw.data_ptr() + 4 * (l * len(XL_LINEARS) + i)
-                df.call("df_absmax_scale_bf16", W.data_ptr(), W.numel(), int(Fmt.E4M3), am.data_ptr(), s_ptr,
-                        ws.data_ptr(), ws.numel(), cur())
-                wq = torch.empty((N, r16(K)), dtype=torch.uint8, device=dev)
-                wt = torch.empty((K, r16(N)), dtype=torch.uint8, device=dev)
-                df.call("df_quantize_2d", int(DType.BFLOAT16), W.data_ptr(), N, K, K, int(Fmt.E4M3), s_ptr,
-                        wq.data_ptr(), wq.stride(0), wt.data_ptr(), wt.stride(0), cur())
-                fb = (2 * l) * blob + fwd_off[i]
-                bb = (2 * l + 1) * blob + bwd_off[i]
-                host[fb:fb + wq.numel()].copy_(wq.reshape(-1).cpu())
-                host[bb:bb + wt.numel()].copy_(wt.reshape(-1).cpu())
-        torch.cuda.synchronize()
-
-        def to_bf16(a):
-            return torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
-
-        acts, grads, bias = [], [], []
-        for i, (_, K, N) in enumerate(XL_LINEARS):
-            seed = synth.SEED_BASE + 5 + 10 * i
-            acts.append(to_bf16(synth.normal((M, K), 1.0, seed=seed)))
-            grads.append(to_bf16(synth.normal((M, N), 1e-3, seed=seed + 3)))
-            bias.append(to_bf16(synth.normal((N,), 0.02, seed=seed + 2)))
-        Mp = r16(M)
-        xq = [torch.empty((M, r16(K)), dtype=torch.uint8, device=dev) for _, K, N in XL_LINEARS]
-        xt = [[torch.empty((K, Mp), dtype=torch.uint8, device=dev) for _, K, N in XL_LINEARS]
-              for _ in range(layers)]
-        dyq = [torch.empty((M, r16(N)), dtype=torch.uint8, device=dev) for _, K, N in XL_LINEARS]
-        dyt = [torch.empty((N, Mp), dtype=torch.uint8, device=dev) for _, K, N in XL_LINEARS]
-        Y = [torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _, K, N in XL_LINEARS]
-        dX = [torch.empty((M, K), dtype=torch.bfloat16, device=dev) for _, K, N in XL_LINEARS]
-        dW = [[torch.empty((N, K), dtype=torch.float32, device=dev) for _, K, N in XL_LINEARS]
-              for _ in range(layers)]
-        db = [torch.empty((N,), dtype=torch.float32, device=dev) for _, K, N in XL_LINEARS]
-        sc = torch.empty((len(XL_LINEARS), 4), dtype=torch.float32, device=dev)
-        cws = torch.empty(max(df.lib().df_quantize_2d_workspace_bytes(M, N) for _, _, N in XL_LINEARS),
-                          dtype=torch.uint8, device=dev)
-        gws_b = max(max(df.lib().df_fp8_gemm_workspace_bytes(M, n, k), df.lib().df_fp8_gemm_bwd_workspace_bytes(M, n, k))
-                    for _, k, n in XL_LINEARS)
-        gws = torch.empty(max(gws_b, 16), dtype=torch.uint8, device=dev)
-        BF, F32, E4, E5 = int(DType.BFLOAT16), int(DType.FLOAT32), int(Fmt.E4M3), int(Fmt.E5M2)
-
-        def fwd_layer(l, base):
-            for i, (_, K, N) in enumerate(XL_LINEARS):
-                s = sc[i].data_ptr()
-                x = acts[i]
-                df.call("df_absmax_scale_bf16", x.data_ptr(), x.numel(), E4, s, s + 4, ws.data_ptr(), ws.numel(),
-                        cur())
-                df.call("df_quantize_2d", BF, x.data_ptr(), M, K, K, E4, s + 4, xq[i].data_ptr(), xq[i].stride(0),
-                        xt[l][i].data_ptr(), Mp, cur())
-                swp = sw.data_ptr() + 4 * (l * len(XL_LINEARS) + i)
-                df.call("df_fp8_gemm_fwd", xq[i].data_ptr(), xq[i].stride(0), base + fwd_off[i], r16(K), M, N, K,
-                        s + 4, swp, BF, bias[i].data_ptr(), BF, Y[i].data_ptr(), N, gws.data_ptr(), gws.numel(),
-                        cur())
-
-        def bwd_layer(l, base):
-            for i, (_, K, N) in enumerate(XL_LINEARS):
-                s = sc[i].data_ptr()
-                g = grads[i]
-                df.call("df_absmax_scale_bf16", g.data_ptr(), g.numel(), E5, s + 8, s + 12, ws.data_ptr(),
-                        ws.numel(), cur())
-                df.call("df_quantize_2d_colsum", BF, g.data_ptr(), M, N, N, E5, s + 12, dyq[i].data_ptr(),
-                        dyq[i].stride(0), dyt[i].data_ptr(), Mp, db[i].data_ptr(), cws.data_ptr(), cws.numel(),
-                        cur())
-                swp = sw.data_ptr() + 4 * (l * len(XL_LINEARS) + i)
-                # dX and dW in one launch; the activation scale of layer l's
-                # forward is the one cached with xt[l]; every layer sees the
-                # same activations here, so sc[i][1] still holds it
-                df.call("df_fp8_gemm_bwd", dyq[i].data_ptr(), dyq[i].stride(0), base + bwd_off[i], r16(N),
-                        dyt[i].data_ptr(), Mp, xt[l][i].data_ptr(), Mp, M, N, K, s + 12, swp, s + 4, BF,
-                        dX[i].data_ptr(), K, F32, dW[l][i].data_ptr(), K, gws.data_ptr(), gws.numel(), cur())
-
-        seq = [(0, l) for l in range(layers)] + [(1, l) for l in reversed(range(layers))]
-        step_flops = 3 * 2 * M * sum(K * N for _, K, N in XL_LINEARS) * layers
-
-        def streamed_step(st):
-            # load idx + slots - 2 right after layer idx's launches: the load
-            # blocks until layer idx - 2 is done, layers idx - 1 and idx stay
-            # queued on the compute stream
-            ahead = slots - 2
-            pending = [st.load(hp.value + (2 * ll + dd) * blob, blob) for dd, ll in seq[:ahead]]
-            for idx, (d, l) in enumerate(seq):
-                slot, base = pending.pop(0)
-                st.wait(slot)
-                (fwd_layer if d == 0 else bwd_layer)(l, base)
-                st.release(slot)
-                if idx + ahead < len(seq):
-                    dd, ll = seq[idx + ahead]
-                    pending.append(st.load(hp.value + (2 * ll + dd) * blob, blob))
-
         def timed(fn, reps):
             torch.cuda.synchronize()
             e0 = torch.cuda.Event(enable_timing=True)
@@ -1270,16 +1155,16 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) / reps, (time.perf_counter() - t0) * 1e3 / reps
 
-        streamer = df.WeightStreamer(slots, blob)
-        streamed_step(streamer)  # warm-up
-        stream_ms, stream_wall = timed(lambda: streamed_step(streamer), steps)
+        streamer = df.WeightStreamer(slots, stack.blob)
+        stack.streamed_step(streamer)  # warm-up
+        stream_ms, stream_wall = timed(lambda: stack.streamed_step(streamer), steps)
 
         # PCIe alone: the same 2*layers copies back to back on the copy stream
         cs = torch.cuda.ExternalStream(streamer.copy_stream())
 
         def copies_only():
-            for d, l in seq:
-                slot, _ = streamer.load(hp.value + (2 * l + d) * blob, blob)
+            for d, l in stack.seq:
+                slot, _ = streamer.load(stack.host_ptr + stack.host_offset(l, d), stack.blob)
                 streamer.release(slot, cs.cuda_stream)
 
         torch.cuda.synchronize()
@@ -1293,26 +1178,20 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
         streamer.close()
 
         # compute alone: weights resident in HBM (one device copy of the blobs)
-        dev_w = torch.empty(2 * layers * blob, dtype=torch.uint8, device=dev)
-        dev_w.copy_(host)
-
-        def resident_step():
-            for d, l in seq:
-                base = dev_w.data_ptr() + (2 * l + d) * blob
-                (fwd_layer if d == 0 else bwd_layer)(l, base)
-
-        resident_step()
-        compute_ms, compute_wall = timed(resident_step, steps)
+        dev_w = stack.resident_weights()
+        stack.resident_step(dev_w)
+        compute_ms, compute_wall = timed(lambda: stack.resident_step(dev_w), steps)
         # the same resident step replayed from a HIP graph: no host launch gaps
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            resident_step()
+            stack.resident_step(dev_w)
         graph.replay()
         compute_graph_ms, _ = timed(graph.replay, steps)
         del graph, dev_w
-        h2d_bytes = 2 * layers * blob
+        h2d_bytes = 2 * layers * stack.blob
+        step_flops = stack.step_flops
         return {
-            "workload": f"config 5: {layers}-layer GPT-2 XL Linear stack, {M} tokens, fwd+bwd, e4m3 weights "
+            "workload": f"config 5: {layers}-layer GPT-2 XL Linear stack, {tokens} tokens, fwd+bwd, e4m3 weights "
                         f"streamed from pinned host memory through {slots} device slots",
             "value": round(step_flops / (stream_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "ms_per_step": round(stream_ms, 3), "host_ms_per_step": round(stream_wall, 3),
@@ -1321,14 +1200,13 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
             "compute_alone_tflops": round(step_flops / (compute_ms * 1e-3) / 1e12, 2),
             "compute_alone_graph_ms": round(compute_graph_ms, 3),
             "h2d_alone_ms": round(h2d_ms, 3), "h2d_gbs": round(h2d_bytes / (h2d_ms * 1e-3) / 1e9, 2),
-            "h2d_bytes_per_step": h2d_bytes, "copy_bytes": blob, "copies_per_step": 2 * layers,
+            "h2d_bytes_per_step": h2d_bytes, "copy_bytes": stack.blob, "copies_per_step": 2 * layers,
             "bound": "pcie" if h2d_ms > compute_ms else "compute",
             "overlap": round(max(h2d_ms, compute_ms) / stream_ms, 4),
             "steps": steps,
         }
     finally:
-        torch.cuda.synchronize()
-        df.call("df_host_free", hp.value)
+        stack.close()
 
 
 def cpu_baseline(tokens):

@@ -87,6 +87,7 @@ _SIGS = {
     "df_fp8_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
     "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+    "df_fp8_gemm_nt_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_sz, _vp, _vp]),
     "df_fp8_gemm_fwd": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                  _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_bwd_dx": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
@@ -296,6 +297,23 @@ def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dty
          M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _ptr(ws),
          ws.numel() if ws is not None else 0, _stream())
     return c
+
+
+class GemmKernel(enum.IntEnum):
+    """DF_GEMM_KERNEL_* of include/df_capi.h."""
+    PERSISTENT = 0
+    TILED_DMA_256 = 1
+    TILED_DMA_128 = 2
+    TILED_REG_256 = 3
+    TILED_REG_128 = 4
+
+
+def gemm_plan(M: int, N: int, K: int, lda: int, ldb: int, bias=None, ws_bytes: int = 0):
+    """(GemmKernel, K slices) that df_fp8_gemm_nt takes for these arguments;
+    ``bias`` is the bias tensor the call would pass (its alignment counts)."""
+    k, s = _c_int(), _c_int()
+    call("df_fp8_gemm_nt_plan", M, N, K, lda, ldb, _ptr(bias), ws_bytes, ctypes.byref(k), ctypes.byref(s))
+    return GemmKernel(k.value), s.value
 
 
 def gemm_bwd(dy_q, wt_q, dyt_q, xt_q, M: int, N: int, K: int, sdy, sw, sx, dx_dtype=None, dw_dtype=None,

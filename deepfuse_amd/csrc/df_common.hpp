@@ -183,6 +183,24 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// --------------------------------------------------------------- binary16 --
+// binary32 -> IEEE binary16 with the hardware convert (v_cvt_f16_f32: round
+// to nearest even under the default mode, binary16 subnormals kept, |x| >=
+// 65520 -> inf); NaN gives the quiet NaN sign|0x7E00, the policy of the
+// bf16 rounding above.
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
+    return (u & 0x7FFFFFFFu) > 0x7F800000u ? (((u >> 16) & 0x8000u) | 0x7E00u) : h;
+}
+// binary16 -> binary32, exact; a NaN keeps its sign and payload bits (the
+// hardware convert would set the quiet bit of a signalling NaN).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    const bool nan = (h & 0x7C00u) == 0x7C00u && (h & 0x03FFu) != 0u;
+    return nan ? __uint_as_float(((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x03FFu) << 13)) : v;
+}
+
 // ------------------------------------------------------------- host side --
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();

@@ -1053,32 +1053,61 @@ static void launch_persistent(const GemmArgs& g, int grid) {
             g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, static_cast<OutT*>(g.C), g.ldc, vec_out);
 }
 
-template <int FA, int FB, typename OutT, typename BiasT>
-static void launch_shape(const GemmArgs& g) {
+// The kernel one NT GEMM call runs (df_fp8_gemm_nt_plan reports it): the
+// persistent kernel when its offsets fit (split into K-slice units when the
+// output has fewer tiles than CUs and a workspace allows it), otherwise the
+// tiled kernels -- LDS-DMA when both operands fit a 32-bit buffer range,
+// register-staged beyond -- with 256x256 or 128x128 blocks and split-K from
+// plan_gemm.  Every launch below follows this plan.
+struct NtPlan {
+    int kind;   // DF_GEMM_KERNEL_*
+    int split;  // K slices (1 = unsplit)
+    int L;      // persistent split: DMA steps per slice
+    int grid;   // persistent: blocks
+};
+
+static NtPlan nt_plan(const GemmArgs& g) {
     const int cus = device_cu_count();
+    const size_t ws = g.ws ? g.ws_bytes : 0;
     if (cus > 0 && persistent_ok(g)) {
         const int64_t tiles = (int64_t)((g.M + kPBM - 1) / kPBM) * ((g.N + kPBN - 1) / kPBN);
-        if (tiles >= cus) {
-            launch_persistent<FA, FB, OutT, BiasT>(g, cus);
+        if (tiles >= cus) return NtPlan{DF_GEMM_KERNEL_PERSISTENT, 1, 0, cus};
+        const PSplit ps = persistent_split_plan(g.M, g.N, g.K, ws, cus);
+        if (ps.S == 1) return NtPlan{DF_GEMM_KERNEL_PERSISTENT, 1, 0, (int)tiles};
+        return NtPlan{DF_GEMM_KERNEL_PERSISTENT, ps.S, ps.L, (int)std::min<int64_t>(tiles * ps.S, cus)};
+    }
+    const GemmPlan gp = plan_gemm(g.M, g.N, g.K, ws);
+    const bool dma_ok = (int64_t)g.M * g.lda < (1ll << 31) && (int64_t)g.N * g.ldb < (1ll << 31);
+    const int kind = dma_ok ? (gp.big ? DF_GEMM_KERNEL_TILED_DMA_256 : DF_GEMM_KERNEL_TILED_DMA_128)
+                            : (gp.big ? DF_GEMM_KERNEL_TILED_REG_256 : DF_GEMM_KERNEL_TILED_REG_128);
+    int split = gp.split;
+    if (split > 1) {  // the slice count the launch really makes
+        const int nk = (g.K + kBK - 1) / kBK;
+        const int kps = ((nk + split - 1) / split) * kBK;
+        split = (g.K + kps - 1) / kps;
+    }
+    return NtPlan{kind, split, 0, 0};
+}
+
+template <int FA, int FB, typename OutT, typename BiasT>
+static void launch_shape(const GemmArgs& g) {
+    const NtPlan p = nt_plan(g);
+    if (p.kind == DF_GEMM_KERNEL_PERSISTENT) {
+        if (p.split == 1) {
+            launch_persistent<FA, FB, OutT, BiasT>(g, p.grid);
             return;
         }
-        const PSplit ps = persistent_split_plan(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0, cus);
-        if (ps.S == 1) {
-            launch_persistent<FA, FB, OutT, BiasT>(g, (int)tiles);
-            return;
-        }
-        const int grid = (int)std::min<int64_t>(tiles * ps.S, cus);
-        gemm_nt_persistent_kernel<FA, FB, float, BiasT, false, true><<<grid, 512, 0, g.st>>>(
-            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, g.ws, g.N, g.N % 4 == 0, ps.L, ps.S);
+        gemm_nt_persistent_kernel<FA, FB, float, BiasT, false, true><<<p.grid, 512, 0, g.st>>>(
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, g.ws, g.N, g.N % 4 == 0, p.L, p.split);
         const int64_t total = (int64_t)g.M * g.N;
         const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
         const bool vec_red = (g.N % 4 == 0) && ((int64_t)g.ldc * (int64_t)sizeof(OutT)) % 16 == 0 && aligned16(g.C);
-        splitk_reduce_kernel<OutT, BiasT><<<blocks, 256, 0, g.st>>>(g.ws, ps.S, g.M, g.N, g.sa, g.sb,
+        splitk_reduce_kernel<OutT, BiasT><<<blocks, 256, 0, g.st>>>(g.ws, p.split, g.M, g.N, g.sa, g.sb,
                                                                     static_cast<const BiasT*>(g.bias),
                                                                     static_cast<OutT*>(g.C), g.ldc, vec_red);
         return;
     }
-    if (plan_gemm(g.M, g.N, g.K, g.ws ? g.ws_bytes : 0).big)
+    if (p.kind == DF_GEMM_KERNEL_TILED_DMA_256 || p.kind == DF_GEMM_KERNEL_TILED_REG_256)
         launch_cfg<256, 256, 2, 4, FA, FB, OutT, BiasT>(g);
     else
         launch_cfg<128, 128, 2, 2, FA, FB, OutT, BiasT>(g);
@@ -1231,6 +1260,23 @@ extern "C" int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda, int fmt_b, c
     else if (fmt_a == E4M3 && fmt_b == E5M2) dispatch_out<E4M3, E5M2>(g, bias_dtype, c_dtype);
     else dispatch_out<E5M2, E5M2>(g, bias_dtype, c_dtype);
     return launch_status("df_fp8_gemm_nt");
+}
+
+extern "C" int df_fp8_gemm_nt_plan(int M, int N, int K, int lda, int ldb, const void* bias, size_t ws_bytes,
+                                   int* kernel, int* split) {
+    clear_error();
+    DF_CHECK(kernel && split, DF_ERR_INVALID, "df_fp8_gemm_nt_plan: NULL output");
+    DF_CHECK(M > 0 && N > 0 && K > 0, DF_ERR_INVALID, "df_fp8_gemm_nt_plan: sizes must be positive (M=%d N=%d K=%d)",
+             M, N, K);
+    DF_CHECK(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0, DF_ERR_ALIGN,
+             "df_fp8_gemm_nt_plan: lda=%d ldb=%d must be multiples of 16 and >= K=%d", lda, ldb, K);
+    // the pointers only matter through their alignment (bias) and presence (ws)
+    GemmArgs g{nullptr, lda, nullptr, ldb, M, N, (K + 15) & ~15, nullptr, nullptr, bias, nullptr, N,
+               ws_bytes ? reinterpret_cast<float*>(uintptr_t{16}) : nullptr, ws_bytes, nullptr};
+    const NtPlan p = nt_plan(g);
+    *kernel = p.kind;
+    *split = p.split;
+    return DF_OK;
 }
 
 extern "C" int df_fp8_gemm_fwd(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw, int M, int N,

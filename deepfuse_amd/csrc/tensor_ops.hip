@@ -4,7 +4,6 @@
 // fp8 hot path; they exist so the C++ drop-in tensor does its device work
 // through the C ABI like everything else.
 #include <hip/hip_runtime.h>
-#include <hip/hip_fp16.h>
 
 #include <cstdarg>
 #include <cstdio>
@@ -74,8 +73,12 @@ template <> struct Elem<DF_DTYPE_FLOAT32> {
 };
 template <> struct Elem<DF_DTYPE_HALF> {
     using T = uint16_t;
-    static __device__ float ld(T v) { return __half2float(__ushort_as_half(v)); }
-    static __device__ T st(float f) { return __half_as_ushort(__float2half(f)); }
+    static __device__ float ld(T v) { return f16_to_f32(v); }
+    static __device__ T st(float f) { return (T)f32_to_f16_rne(f); }
+};
+template <> struct Elem<DF_DTYPE_INT8> {  // input side only (exact widening)
+    using T = int8_t;
+    static __device__ float ld(T v) { return (float)v; }
 };
 template <> struct Elem<DF_DTYPE_BFLOAT16> {
     using T = uint16_t;
@@ -186,7 +189,10 @@ extern "C" int df_convert(int in_dtype, const void* in, int out_dtype, void* out
     DF_CVT(DF_DTYPE_FLOAT32, DF_DTYPE_BFLOAT16)
     DF_CVT(DF_DTYPE_FLOAT32, DF_DTYPE_HALF)
     DF_CVT(DF_DTYPE_BFLOAT16, DF_DTYPE_FLOAT32)
+    DF_CVT(DF_DTYPE_BFLOAT16, DF_DTYPE_HALF)
     DF_CVT(DF_DTYPE_HALF, DF_DTYPE_FLOAT32)
+    DF_CVT(DF_DTYPE_INT8, DF_DTYPE_FLOAT32)
+    DF_CVT(DF_DTYPE_INT8, DF_DTYPE_HALF)
 #undef DF_CVT
     DF_CHECK(false, DF_ERR_UNSUPPORTED, "df_convert: %d -> %d not supported", in_dtype, out_dtype);
 }

@@ -252,6 +252,26 @@ int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda,
                    int c_dtype, void* C, int ldc,
                    void* ws, size_t ws_bytes, void* stream);
 
+/* The kernel df_fp8_gemm_nt runs for these arguments (bias: the bias
+ * pointer the call would pass, or NULL -- only its alignment matters;
+ * ws_bytes: the workspace size, 0 for none): *kernel one of
+ * DF_GEMM_KERNEL_*, *split the K slices (1 = unsplit).  The persistent
+ * kernel takes every call whose operands fit its 32-bit buffer offsets
+ * (M*lda and N*ldb below 2^31, lda and ldb below 2^23) and whose bias is
+ * 4-byte aligned; the tiled kernels take the rest, with LDS-DMA operand
+ * loads while M*lda and N*ldb stay below 2^31 and register-staged loads
+ * beyond.  Same plan as the reference-facing calls below; no reference
+ * counterpart (the reference has one kernel per GEMM). */
+enum {
+    DF_GEMM_KERNEL_PERSISTENT = 0,
+    DF_GEMM_KERNEL_TILED_DMA_256 = 1,
+    DF_GEMM_KERNEL_TILED_DMA_128 = 2,
+    DF_GEMM_KERNEL_TILED_REG_256 = 3,
+    DF_GEMM_KERNEL_TILED_REG_128 = 4
+};
+int df_fp8_gemm_nt_plan(int M, int N, int K, int lda, int ldb, const void* bias, size_t ws_bytes,
+                        int* kernel, int* split);
+
 /* Forward: Y[M,N] = X_q[M,K] . W_q[N,K]^T * sx * sw + b  (e4m3 x e4m3).
  * Replaces fully_connected_forward_kernel (fully_connected_layer.cu:14-41). */
 int df_fp8_gemm_fwd(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw,
@@ -390,8 +410,13 @@ int df_add(int dtype, const void* a, const void* b, void* out, int64_t n, void* 
 /* equal_kernel (tensor.cu:39): mask[i] = bitwise a[i] == b[i] (per element) */
 int df_equal_mask(int dtype, const void* a, const void* b, uint8_t* mask, int64_t n,
                   void* stream);
-/* elementwise cast (RNE), fp32 <-> bf16 and fp32 <-> f16; the reference's
- * utils::to_float / to_half (dnn/utils/convert.cu:6-27) as a tensor op */
+/* elementwise cast, the reference's utils::to_float / to_half
+ * (dnn/utils/convert.cu:6-27) as a tensor op: fp32 -> bf16, fp32 -> f16,
+ * bf16 -> f16 (round to nearest even once, from the exact binary32 value;
+ * f16 subnormals kept, |x| >= 65520 -> inf; NaN -> sign|0x7FC0 (bf16) or
+ * sign|0x7E00 (f16)); bf16, f16, int8 -> fp32 and int8 -> f16 (exact; a
+ * NaN keeps its payload); fp32 -> fp32 (a copy).  Other pairs:
+ * DF_ERR_UNSUPPORTED. */
 int df_convert(int in_dtype, const void* in, int out_dtype, void* out, int64_t n, void* stream);
 /* approx_equal_kernel (tensor.cu:46): mask[i] = |a[i]-b[i]| <= atol, in fp32 */
 int df_approx_equal_mask(int dtype, const void* a, const void* b, uint8_t* mask,

@@ -88,6 +88,41 @@ uint16_t dfo_f32_to_bf16(float v) {
 
 float dfo_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 
+/* binary32 -> IEEE binary16 (1 sign, 5 exponent bits of bias 15, 10 fraction
+ * bits), round to nearest even.  |v| >= 65520 (the midpoint between the
+ * largest finite 65504 and 2^16, which ties to the even 2^16) overflows to
+ * inf; binary16 subnormals (|v| < 2^-14, unit 2^-24) are honoured; NaN gives
+ * the quiet NaN sign|0x7E00 (the same policy as the bf16 rounding). */
+uint16_t dfo_f32_to_f16(float v) {
+    uint32_t u = f2u(v);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(sign | 0x7E00u);
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (a >= 0x38800000u) { /* 2^-14 and up: a normal binary16 */
+        uint32_t r = a - ((uint32_t)(127 - 15) << 23);
+        r = (r + 0x0FFFu + ((r >> 13) & 1u)) >> 13;
+        return (uint16_t)(sign | r);
+    }
+    /* subnormal or zero: the value in units of 2^-24, rounded to an integer
+     * (the scaling by a power of two is exact; 1024 is the smallest normal) */
+    return (uint16_t)(sign | (uint16_t)rintf(u2f(a) * 0x1p24f));
+}
+
+/* IEEE binary16 -> binary32, exact; a NaN keeps its sign and payload (the
+ * fraction shifted into the top of the binary32 fraction), like the bf16
+ * widening. */
+float dfo_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 31) return u2f(sign | 0x7F800000u | (m << 13));
+    if (e == 0) {
+        float v = (float)m * 0x1p-24f; /* exact: m < 2^10 */
+        return u2f(sign | f2u(v));
+    }
+    return u2f(sign | ((e - 15 + 127) << 23) | (m << 13));
+}
+
 /* ------------------------------------------------------------------------ */
 /* Tensor operations                                                        */
 /* ------------------------------------------------------------------------ */
@@ -187,6 +222,50 @@ static void enc_range(int64_t lo, int64_t hi, void* p, int tid) {
 void dfo_encode_bits_range(uint32_t first, int64_t count, int fmt, uint8_t* out, int nthreads) {
     enc_ctx c = {first, fmt, out};
     parallel_range(count, nthreads, enc_range, &c);
+}
+
+/* Elementwise conversion between the DType values 0 (binary32), 1
+ * (binary16), 2 (int8) and 4 (bf16): widen to binary32 exactly, then round
+ * once to the output type.  Returns 0, or -1 for a pair it does not
+ * convert (the product's df_convert refuses the same pairs). */
+static float widen(int dt, const void* in, int64_t i) {
+    switch (dt) {
+        case 0: return ((const float*)in)[i];
+        case 1: return dfo_f16_to_f32(((const uint16_t*)in)[i]);
+        case 2: return (float)((const int8_t*)in)[i];
+        default: return dfo_bf16_to_f32(((const uint16_t*)in)[i]);
+    }
+}
+
+int dfo_convert(int in_dtype, const void* in, int out_dtype, void* out, int64_t n) {
+    const int in_ok = in_dtype == 0 || in_dtype == 1 || in_dtype == 2 || in_dtype == 4;
+    const int out_ok = out_dtype == 0 || out_dtype == 1 || out_dtype == 4;
+    if (!in_ok || !out_ok) return -1;
+    for (int64_t i = 0; i < n; ++i) {
+        float v = widen(in_dtype, in, i);
+        if (out_dtype == 0) ((float*)out)[i] = v;
+        else if (out_dtype == 1) ((uint16_t*)out)[i] = dfo_f32_to_f16(v);
+        else ((uint16_t*)out)[i] = dfo_f32_to_bf16(v);
+    }
+    return 0;
+}
+
+/* Narrowing of every fp32 bit pattern in [first, first+count): bf16 (RNE) or
+ * binary16 (RNE), the exhaustive-sweep helper of the conversion tests. */
+typedef struct { uint32_t first; int to_f16; uint16_t* out; } narrow_ctx;
+
+static void narrow_range(int64_t lo, int64_t hi, void* p, int tid) {
+    (void)tid;
+    narrow_ctx* c = (narrow_ctx*)p;
+    if (c->to_f16)
+        for (int64_t i = lo; i < hi; ++i) c->out[i] = dfo_f32_to_f16(u2f(c->first + (uint32_t)i));
+    else
+        for (int64_t i = lo; i < hi; ++i) c->out[i] = dfo_f32_to_bf16(u2f(c->first + (uint32_t)i));
+}
+
+void dfo_narrow_bits_range(uint32_t first, int64_t count, int to_f16, uint16_t* out, int nthreads) {
+    narrow_ctx c = {first, to_f16, out};
+    parallel_range(count, nthreads, narrow_range, &c);
 }
 
 /* Sorted values of the non-negative finite codes 0..max_code, built from the

@@ -71,6 +71,15 @@ float dfo_decode(uint8_t q, int fmt);          /* exact; NaN code -> canonical q
 float dfo_fmax(int fmt);                       /* 448 or 57344 */
 uint16_t dfo_f32_to_bf16(float v);             /* RNE; NaN -> sign|0x7FC0 */
 float dfo_bf16_to_f32(uint16_t h);             /* exact widening */
+/* binary32 <-> IEEE binary16, the reference's utils::to_half / to_float
+ * (dnn/utils/convert.cu:6-27): RNE narrowing with subnormals, |v| >= 65520
+ * -> inf, NaN -> sign|0x7E00; exact widening, NaN payload kept. */
+uint16_t dfo_f32_to_f16(float v);
+float dfo_f16_to_f32(uint16_t h);
+/* Arrays of DType 0 (binary32), 1 (binary16), 2 (int8, input only) or 4
+ * (bf16): exact widening to binary32, then one rounding to the output type;
+ * -1 for an unsupported pair. */
+int dfo_convert(int in_dtype, const void* in, int out_dtype, void* out, int64_t n);
 
 /* ---- tensor ops ---- */
 float dfo_absmax_f32(const float* x, int64_t n);           /* D2 */
@@ -84,6 +93,11 @@ void dfo_dequantize_bf16(const uint8_t* q, int64_t n, float s, int fmt, uint16_t
 /* Encode of every fp32 bit pattern in [first, first+count) at s = 1:
  * the exhaustive sweep helper (nthreads <= 0 -> one thread). */
 void dfo_encode_bits_range(uint32_t first, int64_t count, int fmt, uint8_t* out,
+                           int nthreads);
+
+/* bf16 (to_f16 == 0) or binary16 (to_f16 != 0) narrowing of every fp32 bit
+ * pattern in [first, first+count) (exhaustive conversion sweeps). */
+void dfo_narrow_bits_range(uint32_t first, int64_t count, int to_f16, uint16_t* out,
                            int nthreads);
 
 /* Independent encoder for the exhaustive pin: binary search of the sorted

@@ -25,6 +25,10 @@ _SIGS = {
     "dfo_fmax": (_f, [_i]),
     "dfo_f32_to_bf16": (ctypes.c_uint16, [_f]),
     "dfo_bf16_to_f32": (_f, [ctypes.c_uint16]),
+    "dfo_f32_to_f16": (ctypes.c_uint16, [_f]),
+    "dfo_f16_to_f32": (_f, [ctypes.c_uint16]),
+    "dfo_narrow_bits_range": (None, [_u32, _i64, _i, _vp, _i]),
+    "dfo_convert": (_i, [_i, _vp, _i, _vp, _i64]),
     "dfo_absmax_f32": (_f, [_vp, _i64]),
     "dfo_absmax_bf16": (_f, [_vp, _i64]),
     "dfo_scale": (_f, [_f, _i]),
@@ -148,6 +152,25 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     r[nan] = ((u[nan] >> 16) & 0x8000 | 0x7FC0).astype(np.uint16)
     return r
+
+
+_CVT_NP = {0: np.float32, 1: np.uint16, 2: np.int8, 4: np.uint16}
+
+
+def convert(x: np.ndarray, in_dtype: int, out_dtype: int) -> np.ndarray:
+    """dfo_convert: DType 0 (f32), 1 (f16 bits), 2 (int8), 4 (bf16 bits)."""
+    x = np.ascontiguousarray(x, _CVT_NP[in_dtype])
+    out = np.empty(x.shape, _CVT_NP[out_dtype])
+    if lib().dfo_convert(in_dtype, _p(x), out_dtype, _p(out), x.size) != 0:
+        raise ValueError(f"unsupported conversion {in_dtype} -> {out_dtype}")
+    return out
+
+
+def narrow_bits_range(first: int, count: int, to_f16: bool, threads: int | None = None) -> np.ndarray:
+    """bf16 (or binary16) bit patterns of every fp32 pattern in [first, first+count)."""
+    out = np.empty(count, np.uint16)
+    lib().dfo_narrow_bits_range(first, count, 1 if to_f16 else 0, _p(out), threads or nthreads())
+    return out
 
 
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:

@@ -6,7 +6,11 @@ fp32-accumulated product of the same dequantized operands, computed by the
 oracle's restatement of dnn/layers/fully_connected_layer.cu:14-106.  Codes
 feeding the GEMM are first checked bit-exact.  bf16 outputs are checked to
 be the round-to-nearest-even image of the fp32 result of the same kernel.
-At full configuration sizes the oracle runs on a seeded sample of rows.
+At full configuration sizes the oracle runs on sampled rows chosen so that
+every 256-row band of the output (one band of the persistent kernel's
+256x256 tiles) is checked at its first and last row and at two seeded rows
+between; dW samples hit every 256 x 256 tile.  A sampled output row spans
+every column tile, so every output tile is compared with the oracle.
 """
 import numpy as np
 import pytest
@@ -44,6 +48,28 @@ def quant_operand(x, fmt, dev, want_q=True, want_qt=False):
     return q, qt, sc, deq
 
 
+def band_rows(M, seed, band=256, extra=2):
+    """First and last row of every `band`-row band of an M-row output plus
+    `extra` seeded rows inside each band (sorted, unique)."""
+    rng = np.random.default_rng(seed)
+    rows = set()
+    for b0 in range(0, M, band):
+        b1 = min(b0 + band, M) - 1
+        rows.update((b0, b1))
+        rows.update(int(r) for r in rng.integers(b0, b1 + 1, size=extra))
+    return np.array(sorted(rows), dtype=np.int64)
+
+
+def pick_rows(M, rows, seed):
+    """None: every row; "bands": band_rows; an int: that many seeded rows."""
+    if rows is None:
+        return np.arange(M)
+    if isinstance(rows, str):
+        assert rows == "bands"
+        return band_rows(M, seed)
+    return np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+
+
 def check_bf16_image(c32, c16):
     exp = synth.f32_to_bf16_bits(c32.cpu().numpy())
     got = c16.view(torch.int16).cpu().numpy().view(np.uint16)
@@ -59,7 +85,7 @@ def forward_case(dev, M, K, N, seed, bias=True, rows=None):
     bd = dev_f32(b, dev) if bias else None
     Y = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd)
     Yh = Y.cpu().numpy()
-    idx = np.arange(M) if rows is None else np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+    idx = pick_rows(M, rows, seed)
     ref = orc.fc_forward(Xd[idx], Wd, b)
     err = orc.rel_err(Yh[idx], ref)
     assert err <= TOL, f"forward M={M} K={K} N={N}: rel err {err:.3e}"
@@ -103,14 +129,14 @@ def backward_case(dev, M, K, N, seed, rows=None, wrows=None, wcols=None):
     dyq, dyt, sdy, dYd = quant_operand(dY, Fmt.E5M2, dev, want_q=True, want_qt=True)
     # dX[M,K]: A = dY [M, N], B = W^T [K, N]
     dX = df.gemm_nt(dyq, Fmt.E5M2, wt, Fmt.E4M3, N, sdy, sw).cpu().numpy()
-    idx = np.arange(M) if rows is None else np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+    idx = pick_rows(M, rows, seed)
     ref = orc.fc_backward_input(dYd[idx], Wd)
     err = orc.rel_err(dX[idx], ref)
     assert err <= TOL, f"dX M={M} K={K} N={N}: {err:.3e}"
     # dW[N,K]: A = dY^T [N, M], B = X^T [K, M]
     dW = df.gemm_nt(dyt, Fmt.E5M2, xt, Fmt.E4M3, M, sdy, sx).cpu().numpy()
-    o_idx = np.arange(N) if wrows is None else np.sort(np.random.default_rng(seed + 9).choice(N, wrows, replace=False))
-    i_idx = np.arange(K) if wcols is None else np.sort(np.random.default_rng(seed + 8).choice(K, wcols, replace=False))
+    o_idx = pick_rows(N, wrows, seed + 9)
+    i_idx = pick_rows(K, wcols, seed + 8)
     refw = orc.fc_backward_weights(np.ascontiguousarray(dYd[:, o_idx]), np.ascontiguousarray(Xd[:, i_idx]))
     errw = orc.rel_err(dW[np.ix_(o_idx, i_idx)], refw)
     assert errw <= TOL, f"dW M={M} K={K} N={N}: {errw:.3e}"
@@ -158,7 +184,8 @@ GPT2_XL = [(1600, 4800), (1600, 1600), (1600, 6400), (6400, 1600)]
 @pytest.mark.parametrize("K,N", GPT2_SMALL)
 def test_config3_forward_bf16(dev, K, N):
     """Config 3: M = 8192 tokens, bf16 activations and weights quantized to
-    e4m3, bf16 output with fused bias; oracle on 48 sampled rows."""
+    e4m3, bf16 output with fused bias; oracle on the band rows (every
+    256-row band's first, last and two seeded rows)."""
     M = 8192
     seed = synth.SEED_BASE + 3 + K + N
     Xb = synth.f32_to_bf16_bits(synth.normal((M, K), 1.0, seed=seed))
@@ -176,7 +203,7 @@ def test_config3_forward_bf16(dev, K, N):
     s_x = orc.scale(orc.absmax(Xb), 0)
     s_w = orc.scale(orc.absmax(Wb), 0)
     assert sx.item() == np.float32(s_x) and sw.item() == np.float32(s_w)
-    idx = np.sort(np.random.default_rng(seed).choice(M, 48, replace=False))
+    idx = band_rows(M, seed)
     cx = orc.quantize(Xb[idx], s_x, 0)
     assert np.array_equal(xq.cpu().numpy()[idx][:, :K], cx)
     cw = orc.quantize(Wb, s_w, 0)
@@ -189,10 +216,11 @@ def test_config3_forward_bf16(dev, K, N):
 @pytest.mark.parametrize("K,N", GPT2_XL)
 def test_config4_forward_backward(dev, K, N):
     """Config 4: M = 16384 tokens, forward e4m3 x e4m3, backward dY ~
-    N(0, 1e-3) as e5m2; oracle on sampled rows of Y / dX and of dW."""
+    N(0, 1e-3) as e5m2; oracle on the band rows of Y and dX (every 256-row
+    band) and on dW rows x columns hitting every 256 x 256 tile."""
     M = 16384
-    backward_case(dev, M, K, N, seed=synth.SEED_BASE + 4 + K + N, rows=24, wrows=8, wcols=64)
-    forward_case(dev, M, K, N, seed=synth.SEED_BASE + 40 + K + N, rows=24)
+    backward_case(dev, M, K, N, seed=synth.SEED_BASE + 4 + K + N, rows="bands", wrows="bands", wcols="bands")
+    forward_case(dev, M, K, N, seed=synth.SEED_BASE + 40 + K + N, rows="bands")
 
 
 @pytest.mark.parametrize("M,N,K", [(1600, 1600, 16384), (384, 200, 8192), (4800, 1600, 16384)])
@@ -230,10 +258,10 @@ def grouped_case(dev, M, K, N, seed, rows=None, wrows=None, wcols=None, out16=Fa
     dW_sep = df.gemm_nt(dyt, Fmt.E5M2, xt, Fmt.E4M3, M, sdy, sx)
     assert torch.equal(dX, dX_sep)
     assert orc.rel_err(dW.cpu().numpy(), dW_sep.cpu().numpy()) <= 1e-5
-    idx = np.arange(M) if rows is None else np.sort(np.random.default_rng(seed).choice(M, rows, replace=False))
+    idx = pick_rows(M, rows, seed)
     assert orc.rel_err(dX.cpu().numpy()[idx], orc.fc_backward_input(dYd[idx], Wd)) <= TOL
-    o_idx = np.arange(N) if wrows is None else np.sort(np.random.default_rng(seed + 9).choice(N, wrows, replace=False))
-    i_idx = np.arange(K) if wcols is None else np.sort(np.random.default_rng(seed + 8).choice(K, wcols, replace=False))
+    o_idx = pick_rows(N, wrows, seed + 9)
+    i_idx = pick_rows(K, wcols, seed + 8)
     refw = orc.fc_backward_weights(np.ascontiguousarray(dYd[:, o_idx]), np.ascontiguousarray(Xd[:, i_idx]))
     assert orc.rel_err(dW.cpu().numpy()[np.ix_(o_idx, i_idx)], refw) <= TOL
     if out16:
@@ -250,7 +278,8 @@ def test_grouped_backward_config4(dev, K, N):
     M = 16384
     grouped, slices = df.gemm_bwd_plan(M, N, K)
     assert grouped and slices >= 1
-    grouped_case(dev, M, K, N, seed=synth.SEED_BASE + 77 + K + N, rows=24, wrows=8, wcols=64, out16=(N == 1600))
+    grouped_case(dev, M, K, N, seed=synth.SEED_BASE + 77 + K + N, rows="bands", wrows="bands", wcols="bands",
+                 out16=(N == 1600))
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4, 3), (64, 768, 3072), (129, 272, 257), (4096, 1600, 1600),
@@ -276,3 +305,99 @@ def test_grouped_backward_without_workspace(dev):
     dX2, dW2 = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx)
     assert torch.equal(dX, dX2)
     assert orc.rel_err(dW.cpu().numpy(), dW2.cpu().numpy()) <= 1e-5
+
+
+def bf16_operands(dev, M, K, N, seed):
+    """bf16 X [M, K] ~ N(0, 1), W [N, K] ~ N(0, 0.02), bias [N] ~ N(0, 0.1)
+    (host bf16 bits and device tensors), as the bench generates them."""
+    Xb = synth.f32_to_bf16_bits(synth.normal((M, K), 1.0, seed=seed))
+    Wb = synth.f32_to_bf16_bits(synth.normal((N, K), 0.02, seed=seed + 1))
+    bb = synth.f32_to_bf16_bits(synth.normal((N,), 0.1, seed=seed + 2))
+    tob = lambda a: torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
+    return Xb, Wb, bb, tob(Xb), tob(Wb), tob(bb)
+
+
+@pytest.mark.parametrize("K,N", GPT2_XL)
+def test_config4_forward_bf16_bias_and_output(dev, K, N):
+    """Config 4 forward as the bench runs it (df_fp8_gemm_fwd with bf16
+    bias and bf16 output, the persistent kernel's multi-tile walk over 16384
+    rows): the bf16 Y is the RNE image of the fp32 Y of the same call with
+    fp32 output, which is within 1e-4 of the oracle on every 256-row band."""
+    M = 16384
+    seed = synth.SEED_BASE + 44 + K + N
+    Xb, Wb, bb, Xd, Wd, bd = bf16_operands(dev, M, K, N, seed)
+    _, sx = df.absmax_scale(Xd, Fmt.E4M3)
+    _, sw = df.absmax_scale(Wd, Fmt.E4M3)
+    xq, _ = df.quantize_2d(Xd, sx, Fmt.E4M3)
+    wq, _ = df.quantize_2d(Wd, sw, Fmt.E4M3)
+    assert df.gemm_plan(M, N, K, xq.stride(0), wq.stride(0), bd, 1 << 30)[0] == df.GemmKernel.PERSISTENT
+    Y16 = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ws = df.gemm_workspace(M, N, K, dev)
+    df.call("df_fp8_gemm_fwd", xq.data_ptr(), xq.stride(0), wq.data_ptr(), wq.stride(0), M, N, K, sx.data_ptr(),
+            sw.data_ptr(), int(df.DType.BFLOAT16), bd.data_ptr(), int(df.DType.BFLOAT16), Y16.data_ptr(), N,
+            ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    Y32 = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd)
+    check_bf16_image(Y32, Y16)
+    s_x = orc.scale(orc.absmax(Xb), 0)
+    s_w = orc.scale(orc.absmax(Wb), 0)
+    assert sx.item() == np.float32(s_x) and sw.item() == np.float32(s_w)
+    idx = band_rows(M, seed)
+    cx = orc.quantize(Xb[idx], s_x, 0)
+    assert np.array_equal(xq.cpu().numpy()[idx][:, :K], cx)
+    cw = orc.quantize(Wb, s_w, 0)
+    assert np.array_equal(wq.cpu().numpy()[:, :K], cw)
+    ref = orc.fc_forward(orc.dequantize(cx, s_x, 0), orc.dequantize(cw, s_w, 0), orc.bf16_to_f32(bb))
+    err = orc.rel_err(Y32.cpu().numpy()[idx], ref)
+    assert err <= TOL, f"config4 bf16 {K}->{N}: {err:.3e}"
+
+
+# Calls the persistent kernel does not take (a bias that is not 4-byte
+# aligned; lda of 2^23 or more; an operand of 2 GiB or more) run the tiled
+# kernels: LDS-DMA operand loads while M*lda and N*ldb stay below 2^31,
+# register-staged loads beyond.  Each case states the kernel and split the
+# plan must pick, then checks the product against the oracle.
+#   (name, M, N, K, lda, bias_offset_elems, workspace, kernel, split>1)
+FALLBACK_CASES = [
+    ("dma256_bias_offset", 4096, 4096, 512, None, 1, False, "TILED_DMA_256", False),
+    ("dma128_bias_offset", 384, 384, 640, None, 1, False, "TILED_DMA_128", False),
+    ("dma128_splitk_bias_offset", 256, 256, 8192, None, 1, True, "TILED_DMA_128", True),
+    ("dma_lda_2p23", 128, 320, 512, 1 << 23, 0, False, "TILED_DMA_128", False),
+    ("reg256_2gib_operand", 32768, 384, 256, 1 << 16, 1, False, "TILED_REG_256", False),
+    ("reg128_2gib_operand", 256, 256, 512, 1 << 23, 0, False, "TILED_REG_128", False),
+    ("reg128_splitk_2gib_operand", 256, 320, 8192, 1 << 23, 1, True, "TILED_REG_128", True),
+]
+
+
+@pytest.mark.parametrize("name,M,N,K,lda,boff,use_ws,kernel,split", FALLBACK_CASES,
+                         ids=[c[0] for c in FALLBACK_CASES])
+def test_fallback_kernels_match_oracle(dev, name, M, N, K, lda, boff, use_ws, kernel, split):
+    seed = synth.SEED_BASE + 900 + M + N + K
+    A = synth.normal((M, K), 1.0, seed=seed)
+    B = synth.normal((N, K), 0.02, seed=seed + 1)
+    bias = synth.normal((N,), 0.1, seed=seed + 2)
+    bb = synth.f32_to_bf16_bits(bias)
+    aq, _, sa, Ad = quant_operand(A, Fmt.E4M3, dev)
+    bq, _, sb, Bd = quant_operand(B, Fmt.E4M3, dev)
+    big = None
+    if lda is not None:  # the same codes at a wide leading dimension
+        big = torch.zeros((M, lda), dtype=torch.uint8, device=dev)
+        big[:, :aq.shape[1]].copy_(aq)
+        aq = big[:, :aq.shape[1]]
+        assert aq.stride(0) == lda
+    # bf16 bias, `boff` elements into its buffer (2 bytes: not 4-byte aligned)
+    bstore = torch.zeros(N + 2, dtype=torch.int16, device=dev)
+    bstore[boff:boff + N].copy_(torch.from_numpy(bb.view(np.int16)))
+    bd = bstore[boff:boff + N].view(torch.bfloat16)
+    ws_bytes = int(df.lib().df_fp8_gemm_workspace_bytes(M, N, K)) if use_ws else 0
+    got_kernel, got_split = df.gemm_plan(M, N, K, aq.stride(0), bq.stride(0), bd, ws_bytes)
+    assert got_kernel == df.GemmKernel[kernel], f"{name}: plan {got_kernel!r}"
+    assert (got_split > 1) == split, f"{name}: split {got_split}"
+    Y = df.gemm_nt(aq, Fmt.E4M3, bq, Fmt.E4M3, K, sa, sb, bias=bd, split_k=use_ws)
+    Y16 = df.gemm_nt(aq, Fmt.E4M3, bq, Fmt.E4M3, K, sa, sb, bias=bd, out_dtype=torch.bfloat16, split_k=use_ws)
+    check_bf16_image(Y, Y16)
+    idx = band_rows(M, seed) if M > 1024 else np.arange(M)
+    ref = orc.fc_forward(Ad[idx], Bd, orc.bf16_to_f32(bb))
+    err = orc.rel_err(Y.cpu().numpy()[idx], ref)
+    assert err <= TOL, f"{name}: rel err {err:.3e}"
+    del big, aq, Y, Y16
+    torch.cuda.empty_cache()

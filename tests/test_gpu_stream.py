@@ -130,3 +130,132 @@ def test_streamer_refuses_unreleased_slot(dev):
         torch.cuda.synchronize()
     finally:
         df.call("df_host_free", host_ptr)
+
+
+# ---------------------------------------------------------------------------
+# Config 5 as the bench runs it: the 48-layer GPT-2 XL Linear stack
+# (deepfuse_amd.stack.StreamedStack, four Linears per layer), 8192 tokens,
+# forward then backward with the W^T codes streamed in reverse, 6 slots and
+# loads issued slots - 2 entries ahead -- the README's layer-serialized
+# execution (README.md:212-226) with the NVMe loader's pinned buffers and
+# async copies (apps/host-multi/NVMeLoader_Linux.hpp:22,69,124).
+from deepfuse_amd.stack import StreamedStack  # noqa: E402
+from oracle import pyoracle as orc  # noqa: E402
+
+C5_LAYERS, C5_TOKENS, C5_SLOTS = 48, 8192, 6
+
+
+@pytest.fixture(scope="module")
+def config5(dev):
+    """One streamed step and one resident step of the config-5 stack, every
+    layer's Y, dX (bf16, as the bench) and dW (fp32) kept from each."""
+    stack = StreamedStack(torch, dev, layers=C5_LAYERS, tokens=C5_TOKENS, keep_outputs=True)
+    try:
+        streamer = df.WeightStreamer(C5_SLOTS, stack.blob)
+        stack.streamed_step(streamer)
+        torch.cuda.synchronize()
+        streamer.close()
+        streamed = stack.new_outputs()
+        dev_w = stack.resident_weights()
+        stack.resident_step(dev_w)
+        torch.cuda.synchronize()
+        yield stack, streamed, dev_w
+    finally:
+        stack.close()
+
+
+def test_config5_streamed_equals_resident(config5):
+    """Every Y, dX and dW of all 48 layers is bit-identical between the
+    streamed step and the step reading resident weights."""
+    stack, (Ys, dXs, dWs), _ = config5
+    for l in range(C5_LAYERS):
+        for i, (name, K, N) in enumerate(stack.linears):
+            assert torch.equal(Ys[l][i], stack.Y[l][i]), f"Y layer {l} {name}"
+            assert torch.equal(dXs[l][i], stack.dX[l][i]), f"dX layer {l} {name}"
+            assert torch.equal(dWs[l][i], stack.dW[l][i]), f"dW layer {l} {name}"
+    # dW = dY^T . X does not involve W, and every layer reads the same
+    # activations and gradients: equal across layers
+    for l in range(1, C5_LAYERS):
+        for i in range(len(stack.linears)):
+            assert torch.equal(dWs[l][i], dWs[0][i]), f"dW layer {l} differs from layer 0"
+
+
+def _bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _band_rows(M, seed, band=256):
+    rng = np.random.default_rng(seed)
+    rows = set()
+    for b0 in range(0, M, band):
+        b1 = min(b0 + band, M) - 1
+        rows.update((b0, b1))
+        rows.update(int(r) for r in rng.integers(b0, b1 + 1, size=2))
+    return np.array(sorted(rows))
+
+
+@pytest.mark.parametrize("layer", [C5_LAYERS - 1, 0])
+def test_config5_layer_matches_oracle(config5, layer):
+    """The streamed Y, dX and dW of one layer's four Linears against the
+    oracle (dnn/layers/fully_connected_layer.cu:29-35,54-59,78-83 on the
+    dequantized codes): codes bit-exact; fp32 dW and the fp32 Y / dX of the
+    same GEMMs (same codes, fp32 output) within 1e-4 on every 256-row band;
+    the streamed bf16 Y and dX are the RNE image of those fp32 outputs."""
+    stack, (Ys, dXs, dWs), dev_w = config5
+    dev = stack.dev
+    M = stack.M
+    st = torch.cuda.current_stream().cuda_stream
+    sc = stack.sc.cpu().numpy()
+    sw = stack.sw.cpu().numpy()
+    for i, (name, K, N) in enumerate(stack.linears):
+        seed = stack.input_seed(i)
+        xb = synth.f32_to_bf16_bits(synth.normal((M, K), 1.0, seed=seed))
+        gb = synth.f32_to_bf16_bits(synth.normal((M, N), 1e-3, seed=seed + 3))
+        bb = synth.f32_to_bf16_bits(synth.normal((N,), 0.02, seed=seed + 2))
+        wb = _bits(stack.weight_bf16(layer, i))
+        s_x, s_dy, s_w = (orc.scale(orc.absmax(xb), orc.E4M3), orc.scale(orc.absmax(gb), orc.E5M2),
+                          orc.scale(orc.absmax(wb), orc.E4M3))
+        assert (sc[i, 1], sc[i, 3], sw[layer, i]) == (np.float32(s_x), np.float32(s_dy), np.float32(s_w)), name
+        cx, cdy, cw = orc.quantize(xb, s_x, orc.E4M3), orc.quantize(gb, s_dy, orc.E5M2), orc.quantize(wb, s_w, orc.E4M3)
+        r16 = df.round16
+        assert np.array_equal(stack.xq[i].cpu().numpy()[:, :K], cx), f"X codes {name}"
+        assert np.array_equal(stack.xt[layer][i].cpu().numpy()[:, :M], np.ascontiguousarray(cx.T)), f"X^T {name}"
+        assert np.array_equal(stack.dyq[i].cpu().numpy()[:, :N], cdy), f"dY codes {name}"
+        assert np.array_equal(stack.dyt[i].cpu().numpy()[:, :M], np.ascontiguousarray(cdy.T)), f"dY^T {name}"
+        host = stack.host.numpy()
+        fo = stack.host_offset(layer, 0) + stack.fwd_off[i]
+        bo = stack.host_offset(layer, 1) + stack.bwd_off[i]
+        assert np.array_equal(host[fo:fo + N * r16(K)].reshape(N, r16(K))[:, :K], cw), f"W codes {name}"
+        assert np.array_equal(host[bo:bo + K * r16(N)].reshape(K, r16(N))[:, :N], np.ascontiguousarray(cw.T)), \
+            f"W^T codes {name}"
+        Xd = orc.dequantize(cx, s_x, orc.E4M3, "f32")
+        dYd = orc.dequantize(cdy, s_dy, orc.E5M2, "f32")
+        Wd = orc.dequantize(cw, s_w, orc.E4M3, "f32")
+        idx = _band_rows(M, seed)
+        # Y: fp32 output of the same forward GEMM on the same codes
+        Y32 = torch.empty((M, N), dtype=torch.float32, device=dev)
+        df.call("df_fp8_gemm_fwd", stack.xq[i].data_ptr(), stack.xq[i].stride(0),
+                dev_w.data_ptr() + fo, r16(K), M, N, K, stack.sc[i].data_ptr() + 4, stack.sw_ptr(layer, i),
+                int(df.DType.BFLOAT16), stack.bias[i].data_ptr(), int(df.DType.FLOAT32), Y32.data_ptr(), N,
+                stack.gws.data_ptr(), stack.gws.numel(), st)
+        assert np.array_equal(_bits(Ys[layer][i]), synth.f32_to_bf16_bits(Y32.cpu().numpy())), f"Y bf16 {name}"
+        ref = orc.fc_forward(Xd[idx], Wd, orc.bf16_to_f32(bb))
+        err = orc.rel_err(Y32.cpu().numpy()[idx], ref)
+        assert err <= 1e-4, f"layer {layer} {name} Y: {err:.3e}"
+        # dX: fp32 output of the dX GEMM (the grouped launch's dX is the
+        # separate call's, bit for bit)
+        dX32 = torch.empty((M, K), dtype=torch.float32, device=dev)
+        df.call("df_fp8_gemm_bwd_dx", stack.dyq[i].data_ptr(), stack.dyq[i].stride(0), dev_w.data_ptr() + bo,
+                r16(N), M, N, K, stack.sc[i].data_ptr() + 12, stack.sw_ptr(layer, i), int(df.DType.FLOAT32),
+                dX32.data_ptr(), K, stack.gws.data_ptr(), stack.gws.numel(), st)
+        assert np.array_equal(_bits(dXs[layer][i]), synth.f32_to_bf16_bits(dX32.cpu().numpy())), f"dX bf16 {name}"
+        ref = orc.fc_backward_input(dYd[idx], Wd)
+        err = orc.rel_err(dX32.cpu().numpy()[idx], ref)
+        assert err <= 1e-4, f"layer {layer} {name} dX: {err:.3e}"
+        # dW: rows and columns hitting every 256 x 256 tile
+        o_idx, i_idx = _band_rows(N, seed + 9), _band_rows(K, seed + 8)
+        refw = orc.fc_backward_weights(np.ascontiguousarray(dYd[:, o_idx]), np.ascontiguousarray(Xd[:, i_idx]))
+        err = orc.rel_err(dWs[layer][i].cpu().numpy()[np.ix_(o_idx, i_idx)], refw)
+        assert err <= 1e-4, f"layer {layer} {name} dW: {err:.3e}"
+        # db from the same pass as the dY codes (fc_backward_bias, :91-106)
+        assert orc.rel_err(stack.db[i].cpu().numpy(), orc.fc_backward_bias(orc.bf16_to_f32(gb))) <= 1e-4
