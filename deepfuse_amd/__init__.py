@@ -116,6 +116,8 @@ _SIGS = {
     "df_quantize_2d_delayed_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "df_quantize_2d_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp,
                                         _c_int, _vp, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_quantize_2d_delayed_noalloc": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
+                                                _c_int, _vp, _c_int, _vp, _c_int, _vp, _vp]),
     "df_layernorm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
     "df_layernorm": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_layernorm_quantize": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_f, _vp, _c_int, _c_int,

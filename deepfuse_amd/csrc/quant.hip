@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "df_common.hpp"
@@ -1172,6 +1173,61 @@ extern "C" int df_quantize_2d_delayed(int in_dtype, const void* x, int rows, int
     DF_CHECK(history && scale_dev && next_scale_dev, DF_ERR_INVALID, "df_quantize_2d_delayed: NULL pointer");
     return quantize_2d_impl("df_quantize_2d_delayed", in_dtype, x, rows, cols, ldx, fmt, scale_dev, q, ldq, qt,
                             ldqt, colsum, ws, ws_bytes, stream, history, len, next_scale_dev);
+}
+
+// ---- allocation-free delayed-scaling quantize -----------------------------
+// The workspace of df_quantize_2d_delayed (column-sum partials, then one
+// tile maximum per block) lives in this file-scope device array instead of a
+// caller's buffer.  Every block overwrites its own entries before the fold
+// kernels read them, so nothing in it has to start at zero.  Each GPU holds
+// its own copy at its own address; host code uses only the address that
+// hipGetSymbolAddress returns for the current device (the array's name on
+// the host is a stand-in, not a device address).
+constexpr size_t kNoAllocScratchBytes = DF_QUANTIZE_2D_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device; nullptr (and the error message set) on failure.
+static void* scratch_for_current_device(const char* name) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("%s: no current device (or device index %d beyond %d)", name, dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error("%s: hipGetSymbolAddress(scratch) on device %d: %s", name, dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" int df_quantize_2d_delayed_noalloc(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                                              const float* scale_dev, float* next_scale_dev, float* history, int len,
+                                              uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum,
+                                              void* stream) {
+    clear_error();
+    static const char* name = "df_quantize_2d_delayed_noalloc";
+    DF_CHECK(history && scale_dev && next_scale_dev, DF_ERR_INVALID, "%s: NULL pointer", name);
+    DF_CHECK(rows >= 0 && cols >= 0, DF_ERR_INVALID, "%s: bad shape rows=%d cols=%d", name, rows, cols);
+    const size_t need = delayed_ws_layout(rows, cols, q ? ldq : 0, qt ? ldqt : 0, colsum != nullptr, nullptr);
+    DF_CHECK(need <= kNoAllocScratchBytes, DF_ERR_WORKSPACE,
+             "%s: rows=%d cols=%d need %zu bytes of scratch, above this entry point's fixed %zu bytes "
+             "(use df_quantize_2d_delayed with a workspace)",
+             name, rows, cols, need, kNoAllocScratchBytes);
+    void* ws = scratch_for_current_device(name);
+    if (!ws) return DF_ERR_HIP;
+    return quantize_2d_impl(name, in_dtype, x, rows, cols, ldx, fmt, scale_dev, q, ldq, qt, ldqt, colsum, ws,
+                            kNoAllocScratchBytes, stream, history, len, next_scale_dev);
 }
 
 extern "C" int df_quantize_2d(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,

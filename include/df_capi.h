@@ -191,6 +191,24 @@ int df_quantize_2d_delayed(int in_dtype, const void* x, int rows, int cols, int 
                            uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum, void* ws,
                            size_t ws_bytes, void* stream);
 
+/* df_quantize_2d_delayed without a workspace argument: the allocation-free
+ * variant, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference (which quantizes nothing).  Its workspace is
+ * a fixed array of DF_QUANTIZE_2D_NOALLOC_SCRATCH_BYTES inside the library,
+ * one per GPU, held until the process ends; the call allocates nothing
+ * (no hipMalloc, hipFree or allocating library routine).  A shape whose
+ * workspace (df_quantize_2d_delayed_workspace_bytes) exceeds that size is
+ * refused with DF_ERR_WORKSPACE before anything is launched.  Results are
+ * bit-identical to df_quantize_2d_delayed's.  Every call on one GPU uses
+ * that GPU's one array: calls that may overlap on one GPU (different
+ * streams, different threads) race and must be serialised by the caller. */
+#define DF_QUANTIZE_2D_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int df_quantize_2d_delayed_noalloc(int in_dtype, const void* x, int rows, int cols, int ldx, int fmt,
+                                   const float* scale_dev, float* next_scale_dev, float* history,
+                                   int len, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
+                                   float* colsum, void* stream);
+
 /* ---- LayerNorm with the quantize of its output fused in (producer side of
  * the qkv / fc1 Linears; layer_norm_forward_kernel,
  * dnn/layers/layer_norm_layer.cu:26-63) ----
