@@ -630,6 +630,29 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                                                           w * 256),
                 4, obias, 0, 0, 0);
     };
+    // instruction k (0..8) of dissue(): A rows (4), B rows (4), bias
+    auto dissue_one = [&](int k) __attribute__((always_inline)) {
+        uint8_t* base = lds + ((uint32_t)d_g & 1u) * kPStage;
+        const bool q1 = GROUPED && d_p;
+        if (k < 4) {
+            const uint32_t a16 = 16u * (uint32_t)(q1 ? p1.lda : lda);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                q1 ? rA1 : rA, (__attribute__((address_space(3))) void*)(base + (w * 4 + k) * 1024), 16,
+                ((k & 1) ? oa1 : oa0) + (uint32_t)(k >> 1) * a16, 0, 0, 0);
+        } else if (k < 8) {
+            const int d = k - 4;
+            const uint32_t b16 = 16u * (uint32_t)(q1 ? p1.ldb : ldb);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                q1 ? rB1 : rB, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
+                ((d & 1) ? ob1 : ob0) + (uint32_t)(d >> 1) * b16, 0, 0, 0);
+        } else if (HAS_BIAS) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rBias,
+                (__attribute__((address_space(3))) void*)(lbias + ((uint32_t)d_tile % kPBiasSlots) * kPBiasSlot +
+                                                          w * 256),
+                4, obias, 0, 0, 0);
+        }
+    };
     auto dadvance = [&]() {
         if (d_g < S && ++d_k == d_nku) {
             d_k = 0;
@@ -672,7 +695,18 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     // (na, nb).  Odd half-steps first wait for the DMA step that half-step
     // c_h+1 reads (after an epilogue its stores are still counted), then
     // synchronise the block and issue the DMA two steps ahead.
+    //
+    // Issue order, frozen by scheduling barriers: MFMA x (row block x/2,
+    // column block x%2), then, for x < 4, three of the twelve fragment
+    // reads, then (odd half-steps) this MFMA's share of the nine DMA
+    // instructions -- two after MFMA 0, one after each later one.  The reads
+    // all sit under the first four MFMAs, so they have landed by the end of
+    // the half-step and the wait before the next barrier costs nothing; the
+    // DMA is spread over the whole half-step instead of leaving as one burst
+    // (with the compiler's own order, driven by scheduling hints only, the
+    // reads and the DMA bunched up: the grouped backward ran 6% slower).
     auto half = [&](auto zero, auto odd, v8i* fa, v8i* fb, v8i* na, v8i* nb) {
+        __builtin_amdgcn_sched_barrier(0);
         if (decltype(odd)::value) {
             if (after_epi)
                 __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(W_AFTER));
@@ -685,37 +719,42 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const uint8_t* sA = lds + (((uint32_t)nxt >> 1) & 1u) * kPStage;
         const uint8_t* sB = sA + kPBM * kPKB;
         const int e = nxt & 1;
-        if (decltype(odd)::value) dissue();
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if (decltype(zero)::value) {
-                    const v16f z = {};
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], z, FB, FA, 0, 0, 0, 0);
-                } else {
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], FB, FA, 0,
-                                                                                0, 0, 0);
-                }
-            }
-#pragma unroll
-        for (int i = 0; i < FM; ++i) na[i] = rd(sA + (wm * 128 + i * 32) * kPKB, e);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) nb[j] = rd(sB + (wn * 64 + j * 32) * kPKB, e);
-        // interleave: one MFMA, then its share of the LDS reads and DMAs
+        u32x4 part[12];  // read r: fragment r/2 (A0-A3, B0, B1), 16-byte half r%2
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (x < 4)
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            else
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            if (decltype(odd)::value) {
-                if (x == 0)
-                    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-                else
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            const int i = x >> 1, j = x & 1;
+            if (decltype(zero)::value) {
+                const v16f z = {};
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], z, FB, FA, 0, 0, 0, 0);
+            } else {
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], FB, FA, 0, 0,
+                                                                            0, 0);
             }
+            if (x < 4) {
+#pragma unroll
+                for (int r = 3 * x; r < 3 * x + 3; ++r) {
+                    const int f = r >> 1, h = r & 1;
+                    const uint8_t* p = f < 4 ? sA + (wm * 128 + f * 32) * kPKB : sB + (wn * 64 + (f - 4) * 32) * kPKB;
+                    part[r] = *reinterpret_cast<const u32x4*>(p + foff[e][h]);
+                }
+            }
+            if (decltype(odd)::value) {
+                if (x == 0) {
+                    dissue_one(0);
+                    dissue_one(1);
+                } else {
+                    dissue_one(x + 1);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int f = 0; f < 6; ++f) {
+            const u32x4 lo = part[2 * f], hi = part[2 * f + 1];
+            v8i r;
+            r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+            r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+            if (f < 4) na[f] = r; else nb[f - 4] = r;
         }
         ++c_h;
         if (decltype(odd)::value) dadvance();
@@ -739,12 +778,18 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const int colw = tn0 + wn * 64;
         const int h4 = (lane >> 5) * 4;
         const uint8_t* bsl = lbias + ((uint32_t)tile % kPBiasSlots) * kPBiasSlot;
-        // bias of the lane's columns colw + 32j + 8g + h4 + (0..3).  A bf16
-        // bias of odd length: its last element shares a dword with the end
-        // of the buffer, which the dword DMA returned as zero.
+        // bias of the lane's columns colw + 32j + 8g + h4 + (0..3): fp32 as
+        // values (bv), bf16 as the raw pairs (braw: 16 registers instead of
+        // 32, widened where they are added, which keeps the forward's
+        // epilogue within the register budget next to the next tile's
+        // fragments).  A bf16 bias of odd length: its last element shares a
+        // dword with the end of the buffer, which the dword DMA returned as
+        // zero, so it is patched in from global memory.
+        constexpr bool PACKB = BIAS && sizeof(BiasT) == 2;
         float bv[FN][4][4];
-        float btail = 0.f;
-        if (BIAS && sizeof(BiasT) == 2 && (No & 1) && colw + 64 >= No) btail = bias_ld(bias, No - 1);
+        uint32_t braw[FN][4][2];
+        uint32_t tbits = 0;
+        if (PACKB && (No & 1) && colw + 64 >= No) tbits = reinterpret_cast<const uint16_t*>(bias)[No - 1];
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -752,23 +797,23 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 const int lc = wn * 64 + j * 32 + 8 * g + h4;
                 const int col = tn0 + lc;
                 float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-                if (BIAS) {
-                    if (sizeof(BiasT) == 4) {
-                        const f32x4 v = *reinterpret_cast<const f32x4*>(bsl + lc * 4);
-                        b0 = v.x; b1 = v.y; b2 = v.z; b3 = v.w;
-                    } else {
-                        const u32x2 v = *reinterpret_cast<const u32x2*>(bsl + lc * 2);
-                        b0 = bf16_to_f32(v.x & 0xFFFFu); b1 = bf16_to_f32(v.x >> 16);
-                        b2 = bf16_to_f32(v.y & 0xFFFFu); b3 = bf16_to_f32(v.y >> 16);
-                        if (No & 1) {
-                            b0 = col == No - 1 ? btail : b0;
-                            b1 = col + 1 == No - 1 ? btail : b1;
-                            b2 = col + 2 == No - 1 ? btail : b2;
-                            b3 = col + 3 == No - 1 ? btail : b3;
-                        }
+                uint32_t x0 = 0, x1 = 0;
+                if (PACKB) {
+                    const u32x2 v = *reinterpret_cast<const u32x2*>(bsl + lc * 2);
+                    x0 = v.x;
+                    x1 = v.y;
+                    if (No & 1) {
+                        x0 = col == No - 1 ? (x0 & 0xFFFF0000u) | tbits : x0;
+                        x0 = col + 1 == No - 1 ? (x0 & 0xFFFFu) | (tbits << 16) : x0;
+                        x1 = col + 2 == No - 1 ? (x1 & 0xFFFF0000u) | tbits : x1;
+                        x1 = col + 3 == No - 1 ? (x1 & 0xFFFFu) | (tbits << 16) : x1;
                     }
+                } else if (BIAS) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(bsl + lc * 4);
+                    b0 = v.x; b1 = v.y; b2 = v.z; b3 = v.w;
                 }
                 bv[j][g][0] = b0; bv[j][g][1] = b1; bv[j][g][2] = b2; bv[j][g][3] = b3;
+                braw[j][g][0] = x0; braw[j][g][1] = x1;
             }
         // slab read-back geometry: lane -> (row, 16-byte chunk)
         constexpr int CPR = 64 * ES / 16;
@@ -789,8 +834,15 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const v16f& a = acc[i][j];
-                    const float v0 = a[4 * g] * sabo + bv[j][g][0], v1 = a[4 * g + 1] * sabo + bv[j][g][1];
-                    const float v2 = a[4 * g + 2] * sabo + bv[j][g][2], v3 = a[4 * g + 3] * sabo + bv[j][g][3];
+                    float c0 = bv[j][g][0], c1 = bv[j][g][1], c2 = bv[j][g][2], c3 = bv[j][g][3];
+                    if (PACKB) {
+                        c0 = __uint_as_float(braw[j][g][0] << 16);
+                        c1 = __uint_as_float(braw[j][g][0] & 0xFFFF0000u);
+                        c2 = __uint_as_float(braw[j][g][1] << 16);
+                        c3 = __uint_as_float(braw[j][g][1] & 0xFFFF0000u);
+                    }
+                    const float v0 = a[4 * g] * sabo + c0, v1 = a[4 * g + 1] * sabo + c1;
+                    const float v2 = a[4 * g + 2] * sabo + c2, v3 = a[4 * g + 3] * sabo + c3;
                     if constexpr (ES == 2)
                         pk[j][g] = u32x2{pack_bf16_rne(v0, v1), pack_bf16_rne(v2, v3)};
                     else
