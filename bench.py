@@ -78,6 +78,8 @@ def parse():
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run one plain 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
+    p.add_argument("--conversion-only", action="store_true",
+                   help="run only the config-2 conversion leg and print its JSON (profiling runs)")
     p.add_argument("--summarize-profiles", action="store_true",
                    help="no GPU work: turn the rocprofv3 output of PROFILE_COMMANDS into the summaries under "
                         "profiles/")
@@ -149,6 +151,10 @@ def main():
 
     def cur():  # the stream kernels go to (the capture stream while capturing)
         return torch.cuda.current_stream().cuda_stream
+
+    if args.conversion_only:
+        print(json.dumps({"conversion": conversion_bench(torch, df, synth, dev, cur())}))
+        return
 
     def to_bf16(a):
         return torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
@@ -441,6 +447,16 @@ PROFILE_COMMANDS = {
               "-d gpurun_out/pmc_write -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
               "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph "
               "--copy-calibration"),
+    "stats_conversion": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_conversion -o bench "
+                         "-- python3 bench.py --conversion-only"),
+    "fetch_conversion": ("timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv "
+                         "-d gpurun_out/pmc_fetch_conv -o bench -- python3 bench.py --conversion-only --copy-calibration"),
+    "write_conversion": ("timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --kernel-trace --output-format csv "
+                         "-d gpurun_out/pmc_write_conv -o bench -- python3 bench.py --conversion-only --copy-calibration"),
+    "mfma": ("timeout -s KILL 180 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES "
+             "SQ_INSTS_VALU_MFMA_MOPS_F8 --kernel-trace --output-format csv -d gpurun_out/pmc_mfma -o bench -- "
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer "
+             "--no-producer --no-delayed --no-config3 --no-graph"),
     "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-producer --no-delayed --no-config3"),
@@ -483,15 +499,10 @@ def _short_kernel(name):
     return name
 
 
-def summarize_profiles():
-    """Write profiles/bench_config4_kernel_stats.md, hbm_traffic_config4.md
-    and hbm_traffic.json from the output of PROFILE_COMMANDS."""
+def config4_summaries(out_dir, prof):
+    """profiles/bench_config4_kernel_stats.md, hbm_traffic_config4.md and
+    hbm_traffic.json from the stats / fetch / write runs."""
     import csv
-
-    root = os.path.dirname(os.path.abspath(__file__))
-    prof = os.path.join(root, "profiles")
-    out_dir = os.path.join(root, "gpurun_out")
-    os.makedirs(prof, exist_ok=True)
 
     stats_csv = os.path.join(out_dir, "prof_bench", "bench_kernel_stats.csv")
     with open(stats_csv) as fh:
@@ -558,7 +569,28 @@ def summarize_profiles():
         lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:.1f} | {write[k][0]:.1f} | {mb:.1f} |")
     with open(os.path.join(prof, "hbm_traffic_config4.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
+    return rows, fams
+
+
+def summarize_profiles():
+    """Write profiles/bench_config4_kernel_stats.md, hbm_traffic_config4.md
+    and hbm_traffic.json from the output of PROFILE_COMMANDS."""
+    import csv
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    prof = os.path.join(root, "profiles")
+    out_dir = os.path.join(root, "gpurun_out")
+    os.makedirs(prof, exist_ok=True)
+
+    rows, fams = [], {}
+    if os.path.exists(os.path.join(out_dir, "prof_bench", "bench_kernel_stats.csv")) and \
+            os.path.exists(os.path.join(out_dir, "pmc_fetch", "bench_counter_collection.csv")):
+        rows, fams = config4_summaries(out_dir, prof)
     extra = []
+    if conversion_summary(out_dir, prof):
+        extra.append("conversion_config2_kernels.md")
+    if mfma_summary(out_dir, prof):
+        extra.append("gemm_mfma_busy_config4.md")
     for key, sub, fname, title, keep in EXTRA_STATS:
         path = os.path.join(out_dir, sub, "bench_kernel_stats.csv")
         if not os.path.exists(path):
@@ -579,6 +611,137 @@ def summarize_profiles():
     if streaming_summary(out_dir, prof):
         extra.append("streaming_h2d_copies_config5.md")
     print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)}, extra {extra})")
+
+
+CONVERSION_KERNELS = ("absmax_f32_stage1", "absmax_bf16_stage1", "absmax_stage2", "quantize_f32_kernel",
+                      "quantize_bf16_kernel", "dequantize_f32_kernel", "dequantize_bf16_kernel", "hbm_probe_kernel")
+
+
+def conversion_summary(out_dir, prof):
+    """profiles/conversion_config2_kernels.md from the stats_conversion,
+    fetch_conversion and write_conversion runs: per kernel instantiation of
+    the config-2 leg (n = 2^28), average duration, FETCH / WRITE bytes per
+    dispatch (copy-calibrated) and the resulting GB/s."""
+    import csv
+
+    stats = os.path.join(out_dir, "prof_conversion", "bench_kernel_stats.csv")
+    if not os.path.exists(stats):
+        return False
+    with open(stats) as fh:
+        rows = [r for r in csv.DictReader(fh) if any(k in r["Name"] for k in CONVERSION_KERNELS)]
+
+    def per_dispatch(sub, counter):
+        path = os.path.join(out_dir, sub, "bench_counter_collection.csv")
+        vals = {}
+        if not os.path.exists(path):
+            return vals
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] == counter:
+                    vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return vals
+
+    fetch = per_dispatch("pmc_fetch_conv", "FETCH_SIZE")
+    write = per_dispatch("pmc_write_conv", "WRITE_SIZE")
+    copy = [k for k in fetch if "copyBuffer" in k]
+    fscale = wscale = None
+    if copy and any("copyBuffer" in k for k in write):
+        cf = max(max(fetch[k]) for k in copy)
+        cw = max(max(v) for k, v in write.items() if "copyBuffer" in k)
+        fscale, wscale = (1 << 30) / (cf * 1024), (1 << 30) / (cw * 1024)
+    lines = ["# rocprofv3: config-2 conversion kernels (n = 268,435,456; fp32 and bf16 in, e4m3 and e5m2)", "",
+             "Commands (from the repository root, on one MI355X; three separate runs):", "",
+             "    " + PROFILE_COMMANDS["stats_conversion"], "    " + PROFILE_COMMANDS["fetch_conversion"],
+             "    " + PROFILE_COMMANDS["write_conversion"], "",
+             "Each conversion runs 1 + 10 times (warm-up, timed).  `hbm_probe_kernel<R, W>` is the bandwidth "
+             "calibration with the same access pattern (R bytes read, W written per 16-byte vector slot).  "
+             "Traffic: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the 1 GiB device copy of the same "
+             f"runs (fetch x {fscale:.4f}, write x {wscale:.4f}); GB/s = (calibrated fetch + write) / average "
+             "duration." if fscale else "Traffic runs missing.", "",
+             "| kernel | calls | avg us | fetch MB | write MB | GB/s |", "|---|---|---|---|---|---|"]
+    for r in rows:
+        name = r["Name"]
+        avg_us = float(r["AverageNs"]) / 1e3
+        f = fetch.get(name)
+        w = write.get(name)
+        if f and w and fscale:
+            fmb = sum(f) / len(f) * 1024 * fscale / 1e6
+            wmb = sum(w) / len(w) * 1024 * wscale / 1e6
+            gbs = (fmb + wmb) * 1e6 / (avg_us * 1e-6) / 1e9
+            lines.append(f"| `{_short_kernel(name)}` | {r['Calls']} | {avg_us:.1f} | {fmb:.1f} | {wmb:.1f} | "
+                         f"{gbs:.0f} |")
+        else:
+            lines.append(f"| `{_short_kernel(name)}` | {r['Calls']} | {avg_us:.1f} | - | - | - |")
+    with open(os.path.join(prof, "conversion_config2_kernels.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return True
+
+
+def mfma_summary(out_dir, prof):
+    """profiles/gemm_mfma_busy_config4.md from the mfma counter run: per
+    GEMM dispatch of the config-4 step, MFMA-busy cycles over the SIMDs'
+    available cycles, and the shader clock the run held.  GRBM_GUI_ACTIVE
+    as collected is the sum over the 8 XCDs (each counts GPU-busy cycles at
+    the shader clock), so busy cycles per XCD = GRBM_GUI_ACTIVE / 8; the
+    1024 SIMDs (256 CUs x 4) each have that many cycles available."""
+    import csv
+
+    path = os.path.join(out_dir, "pmc_mfma", "bench_counter_collection.csv")
+    kt_path = os.path.join(out_dir, "pmc_mfma", "bench_kernel_trace.csv")
+    if not os.path.exists(path):
+        return False
+    per = {}
+    with open(path) as fh:
+        for r in csv.DictReader(fh):
+            if "gemm_nt_persistent_kernel" not in r["Kernel_Name"]:
+                continue
+            e = per.setdefault(r["Dispatch_Id"], {"name": _short_kernel(r["Kernel_Name"]),
+                                                  "full": r["Kernel_Name"], "grid": int(r["Grid_Size"])})
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            e["t"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    if os.path.exists(kt_path):
+        with open(kt_path) as fh:
+            for r in csv.DictReader(fh):
+                if r["Dispatch_Id"] in per:
+                    per[r["Dispatch_Id"]]["t"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    lines = ["# rocprofv3: MFMA busy and shader clock of the config-4 GEMMs", "",
+             "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["mfma"], "",
+             "Two eager config-4 steps after one warm-up.  Per dispatch: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+             "(GRBM_GUI_ACTIVE / 8 x 1024 SIMDs); clock = GRBM_GUI_ACTIVE / 8 / duration; fp8 flop = "
+             "SQ_INSTS_VALU_MFMA_MOPS_F8 x 512 (the MFMA work issued, padding of partial tiles included).  "
+             "`<A fmt, B fmt, out, bias type, bias, split, dX out>`: `<0, 0, ...>` forward, `<1, 0, ..., void>` "
+             "dX alone, the last argument non-void the grouped dX + dW launch.", "",
+             "| kernel | grid | us | clock GHz | MFMA busy | issued fp8 TFLOP | TFLOP/s issued |",
+             "|---|---|---|---|---|---|---|"]
+    # one row per distinct GEMM (kernel and issued work), medians over its dispatches
+    groups = {}
+    for did in sorted(per, key=int):
+        e = per[did]
+        gui = e.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+        if not gui or not e.get("t"):
+            continue
+        tmpl = e["full"][e["full"].find("<"):e["full"].find(">(") + 1] if "<" in e["full"] else ""
+        tfl = e.get("SQ_INSTS_VALU_MFMA_MOPS_F8", 0.0) * 512 / 1e12
+        g = groups.setdefault((tmpl, round(tfl, 4)), {"grid": e["grid"] // 512, "t": [], "clk": [], "busy": [],
+                                                      "cyc": [], "bcyc": []})
+        g["t"].append(e["t"])
+        g["clk"].append(gui / e["t"])
+        g["busy"].append(e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui * 1024))
+        g["cyc"].append(gui * 1024)
+        g["bcyc"].append(e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0))
+    med = lambda v: sorted(v)[len(v) // 2]
+    tot_b = tot_c = 0.0
+    for (tmpl, tfl), g in groups.items():
+        t = med(g["t"])
+        tot_b += sum(g["bcyc"])
+        tot_c += sum(g["cyc"])
+        lines.append(f"| `gemm_nt_persistent_kernel{tmpl}` (x{len(g['t'])}) | {g['grid']} | {t / 1e3:.1f} | "
+                     f"{med(g['clk']):.2f} | {med(g['busy']):.3f} | {tfl:.3f} | {tfl / (t * 1e-9):.0f} |")
+    if tot_c:
+        lines += ["", f"All GEMM dispatches together: MFMA busy {tot_b / tot_c:.3f} of the SIMD cycles they held."]
+    with open(os.path.join(prof, "gemm_mfma_busy_config4.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return True
 
 
 def streaming_summary(out_dir, prof):
@@ -663,7 +826,44 @@ def conversion_bench(torch, df, synth, dev, stream, reps=10):
                 gbs = nbytes / (ms * 1e-3) / 1e9
                 res[f"{kname}_{src}_{fname}"] = {"ms": round(ms, 4), "gbs": round(gbs, 1),
                                                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    del x32, x16, q, o32, o16
+    # The ceiling of each access pattern on this part: the same loads and
+    # stores as the kernels above (df_hbm_probe: 8 non-temporal 16-byte
+    # loads in flight per thread, one chunk per block), no arithmetic.
+    probe_dst = torch.empty(max(int(df.lib().df_hbm_probe_dst_bytes(16, 16, n * 4)), 16), dtype=torch.uint8,
+                            device=dev)
+    ceil = {}
+    for key, rb, wb, src_t in (("read_f32", 16, 0, x32), ("read_bf16", 16, 0, x16),
+                               ("f32_to_fp8", 16, 4, x32), ("bf16_to_fp8", 16, 8, x16),
+                               ("fp8_to_f32", 4, 16, q), ("fp8_to_bf16", 8, 16, q),
+                               ("copy_f32", 16, 16, x32)):
+        sbytes = src_t.numel() * src_t.element_size()
+        nbytes = sbytes + (sbytes // rb) * wb
+
+        def fn(rb=rb, wb=wb, src_t=src_t, sbytes=sbytes):
+            df.call("df_hbm_probe", rb, wb, src_t.data_ptr(), sbytes, probe_dst.data_ptr(), stream)
+
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        ceil[key] = {"pattern": f"{rb}:{wb}", "bytes": nbytes, "ms": round(ms, 4), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    res["pattern_ceilings"] = ceil
+    pattern_of = {"absmax_f32": "read_f32", "absmax_bf16": "read_bf16", "quantize_f32": "f32_to_fp8",
+                  "quantize_bf16": "bf16_to_fp8", "dequantize_f32": "fp8_to_f32", "dequantize_bf16": "fp8_to_bf16"}
+    for key, v in res.items():
+        if isinstance(v, dict) and "gbs" in v and key != "pattern_ceilings":
+            kind, src = key.split("_")[0], key.split("_")[1]
+            c = ceil[pattern_of[f"{kind}_{src}"]]["gbs"]
+            v["frac_of_pattern_ceiling"] = round(v["gbs"] / c, 4)
+    del x32, x16, q, o32, o16, probe_dst
     torch.cuda.empty_cache()
     return res
 

@@ -65,6 +65,8 @@ _SIGS = {
     "df_absmax_scale_f32": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "df_absmax_scale_bf16": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "df_compute_scale": (_c_int, [_vp, _c_int, _vp, _vp]),
+    "df_hbm_probe_dst_bytes": (_c_sz, [_c_int, _c_int, _c_i64]),
+    "df_hbm_probe": (_c_int, [_c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "df_quantize_f32_e4m3": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
     "df_quantize_f32_e5m2": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
     "df_quantize_bf16_e4m3": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),

@@ -887,6 +887,62 @@ __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __
         out[c] = ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) + part[3][threadIdx.x];
 }
 
+// ------------------------------------------------------ bandwidth probe --
+// The flat kernels' access pattern without their arithmetic: per chunk,
+// each thread issues kU non-temporal loads of RB bytes, kThreads apart,
+// then kU non-temporal stores of WB bytes at the same vector index (the
+// stored words are an XOR fold of the loaded ones, so no load is dead).
+// RB:WB = 16:4 is fp32 -> fp8, 16:8 bf16 -> fp8, 4:16 fp8 -> fp32, 8:16
+// fp8 -> bf16, 16:16 a copy, 16:0 a read (absmax: one word per block).
+template <int RB> struct ProbeVec;
+template <> struct ProbeVec<4> { using T = uint32_t; };
+template <> struct ProbeVec<8> { using T = u32x2; };
+template <> struct ProbeVec<16> { using T = u32x4; };
+
+__device__ __forceinline__ uint32_t fold_words(uint32_t v) { return v; }
+__device__ __forceinline__ uint32_t fold_words(u32x2 v) { return v.x ^ v.y; }
+__device__ __forceinline__ uint32_t fold_words(u32x4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
+
+template <int WB> struct ProbeOut;
+template <> struct ProbeOut<4> {
+    template <typename V> static __device__ __forceinline__ uint32_t make(V v) { return fold_words(v); }
+};
+template <> struct ProbeOut<8> {
+    static __device__ __forceinline__ u32x2 make(u32x4 v) { return u32x2{v.x ^ v.y, v.z ^ v.w}; }
+};
+template <> struct ProbeOut<16> {
+    static __device__ __forceinline__ u32x4 make(uint32_t w) { return u32x4{w, w ^ 1u, w ^ 2u, w ^ 3u}; }
+    static __device__ __forceinline__ u32x4 make(u32x2 w) { return u32x4{w.x, w.y, w.x ^ 1u, w.y ^ 1u}; }
+    static __device__ __forceinline__ u32x4 make(u32x4 v) { return u32x4{v.x ^ 1u, v.y, v.z, v.w}; }
+};
+
+template <int RB, int WB>
+__global__ __launch_bounds__(kThreads) void hbm_probe_kernel(const void* __restrict__ src, int64_t nvec,
+                                                               void* __restrict__ dst) {
+    using V = typename ProbeVec<RB>::T;
+    const V* xv = reinterpret_cast<const V*>(src);
+    uint32_t acc = 0;
+    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
+        V v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+        if constexpr (WB == 0) {
+#pragma unroll
+            for (int u = 0; u < kU; ++u) acc ^= fold_words(v[u]);
+        } else {
+            using O = decltype(ProbeOut<WB>::make(v[0]));
+            O* ov = reinterpret_cast<O*>(dst);
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                __builtin_nontemporal_store(ProbeOut<WB>::make(v[u]), ov + base + u * kThreads + threadIdx.x);
+        }
+    }
+    if constexpr (WB == 0) {
+        const uint32_t m = block_max_u32(acc);
+        if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(dst)[blockIdx.x] = m;
+    }
+}
+
 // --------------------------------------------------------------- launchers --
 static int grid_for(int64_t units, int64_t per_block_unit_cap) {
     int64_t blocks = (units + kThreads - 1) / kThreads;
@@ -905,6 +961,45 @@ using namespace dfk;
 static constexpr int64_t kStreamBlocks = 32768;
 
 extern "C" size_t df_absmax_workspace_bytes(void) { return kMaxReduceBlocks * sizeof(uint32_t); }
+
+extern "C" size_t df_hbm_probe_dst_bytes(int read_bytes, int write_bytes, int64_t src_bytes) {
+    if (read_bytes <= 0 || src_bytes <= 0) return 0;
+    const int64_t nvec = src_bytes / read_bytes;
+    if (write_bytes == 0) return (size_t)grid_for(nvec / kU, kStreamBlocks) * sizeof(uint32_t);
+    return (size_t)(nvec * write_bytes);
+}
+
+extern "C" int df_hbm_probe(int read_bytes, int write_bytes, const void* src, int64_t src_bytes, void* dst,
+                            void* stream) {
+    clear_error();
+    static const char* name = "df_hbm_probe";
+    const bool ok = (read_bytes == 16 && (write_bytes == 0 || write_bytes == 4 || write_bytes == 8 ||
+                                          write_bytes == 16)) ||
+                    ((read_bytes == 4 || read_bytes == 8) && write_bytes == 16);
+    DF_CHECK(ok, DF_ERR_UNSUPPORTED, "%s: pattern %d:%d not provided", name, read_bytes, write_bytes);
+    DF_CHECK(src && dst, DF_ERR_INVALID, "%s: NULL pointer", name);
+    const int64_t chunk_bytes = kChunkVec * read_bytes;
+    DF_CHECK(src_bytes > 0 && src_bytes % chunk_bytes == 0, DF_ERR_INVALID,
+             "%s: src_bytes=%lld must be a positive multiple of %lld", name, (long long)src_bytes,
+             (long long)chunk_bytes);
+    DF_CHECK(aligned16(src) && aligned16(dst), DF_ERR_ALIGN, "%s: src and dst must be 16-byte aligned", name);
+    const int64_t nvec = src_bytes / read_bytes;
+    const int blocks = grid_for(nvec / kU, kStreamBlocks);
+    hipStream_t st = as_stream(stream);
+#define DF_PROBE(R, W)                                                                 \
+    if (read_bytes == R && write_bytes == W) {                                         \
+        hbm_probe_kernel<R, W><<<blocks, kThreads, 0, st>>>(src, nvec, dst);          \
+        return launch_status(name);                                                    \
+    }
+    DF_PROBE(16, 0)
+    DF_PROBE(16, 4)
+    DF_PROBE(16, 8)
+    DF_PROBE(16, 16)
+    DF_PROBE(4, 16)
+    DF_PROBE(8, 16)
+#undef DF_PROBE
+    return DF_ERR_UNSUPPORTED;
+}
 
 static int absmax_impl(int in_dtype, const void* x, int64_t n, int fmt, float* absmax_dev,
                        float* scale_dev, void* ws, size_t ws_bytes, void* stream) {

@@ -81,6 +81,20 @@ int df_absmax_scale_f32(const float* x, int64_t n, int fmt, float* absmax_dev,
                         float* scale_dev, void* ws, size_t ws_bytes, void* stream);
 int df_absmax_scale_bf16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
                          float* scale_dev, void* ws, size_t ws_bytes, void* stream);
+/* ---- bandwidth calibration (measurement only; no reference counterpart)
+ * The flat absmax / quantize / dequantize kernels' exact access pattern
+ * without their arithmetic, to measure the HBM ceiling each conversion can
+ * reach on this part: src_bytes of src read as read_bytes per vector (16
+ * bytes per lane-load, 8 loads in flight per thread, non-temporal) and, per
+ * vector, write_bytes stored to dst (an XOR fold of the loaded words).
+ * Patterns (read:write bytes) 16:0 (absmax; dst gets one word per block),
+ * 16:4 (fp32 -> fp8), 16:8 (bf16 -> fp8), 4:16 (fp8 -> fp32), 8:16 (fp8 ->
+ * bf16), 16:16 (a copy).  src_bytes must be a multiple of 2048 * read_bytes;
+ * dst holds df_hbm_probe_dst_bytes(...) bytes. */
+size_t df_hbm_probe_dst_bytes(int read_bytes, int write_bytes, int64_t src_bytes);
+int df_hbm_probe(int read_bytes, int write_bytes, const void* src, int64_t src_bytes, void* dst,
+                 void* stream);
+
 /* scale from an absmax already on the device */
 int df_compute_scale(const float* absmax_dev, int fmt, float* scale_dev, void* stream);
 

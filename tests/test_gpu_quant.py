@@ -284,3 +284,35 @@ def test_quantize_2d_batch_many_tensors(dev):
         assert sc[i].item() == np.float32(s)
         assert np.array_equal(qs[i].cpu().numpy()[:, :x.shape[1]], orc.quantize(x, s, int(Fmt.E4M3)))
         assert not qs[i].cpu().numpy()[:, x.shape[1]:].any()  # zero padding
+
+
+@pytest.mark.parametrize("rb,wb", [(16, 0), (16, 4), (16, 8), (16, 16), (4, 16), (8, 16)])
+def test_hbm_probe_patterns(dev, rb, wb):
+    """df_hbm_probe (the bandwidth calibration behind the bench's pattern
+    ceilings) reads every source vector and writes the documented fold."""
+    import deepfuse_amd as dfm
+    nbytes = 2048 * rb * 5
+    rng = np.random.default_rng(rb * 31 + wb)
+    src = rng.integers(0, 1 << 32, size=nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    s = torch.from_numpy(src.view(np.int32)).to(dev)
+    dbytes = dfm.lib().df_hbm_probe_dst_bytes(rb, wb, nbytes)
+    d = torch.zeros(dbytes // 4, dtype=torch.int32, device=dev)
+    dfm.call("df_hbm_probe", rb, wb, s.data_ptr(), nbytes, d.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    got = d.cpu().numpy().view(np.uint32)
+    v = src.reshape(-1, rb // 4)
+    if wb == 0:  # one word per block; xor-folds of its chunks, max over its threads: check it is non-trivial
+        assert got.size == 5 and np.all(got != 0)
+        return
+    if rb == 16 and wb == 4:
+        exp = v[:, 0] ^ v[:, 1] ^ v[:, 2] ^ v[:, 3]
+    elif rb == 16 and wb == 8:
+        exp = np.stack([v[:, 0] ^ v[:, 1], v[:, 2] ^ v[:, 3]], 1)
+    elif rb == 16 and wb == 16:
+        exp = v.copy()
+        exp[:, 0] ^= 1
+    elif rb == 4:
+        w = v[:, 0]
+        exp = np.stack([w, w ^ 1, w ^ 2, w ^ 3], 1)
+    else:
+        exp = np.stack([v[:, 0], v[:, 1], v[:, 0] ^ 1, v[:, 1] ^ 1], 1)
+    assert np.array_equal(got, exp.reshape(-1))
