@@ -74,7 +74,8 @@ def parse():
     p.add_argument("--stream-layers", type=int, default=48)
     p.add_argument("--stream-slots", type=int, default=6,
                    help="device weight slots of the streaming leg (>= 3: loads run slots-2 layers ahead)")
-    p.add_argument("--cpu-tokens", type=int, default=3072, help="token slice for the CPU baseline")
+    p.add_argument("--cpu-tokens", type=int, default=512,
+                   help="token slice of configs 3 and 4 for the CPU baseline (all cores; one core: a 1/8 slice)")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run one plain 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
@@ -1410,29 +1411,44 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
 
 
 def cpu_baseline(tokens):
-    """Oracle (plain C restatement of the reference's FC kernel loops) on a
-    `tokens`-row slice of the workload: forward, dX and dW of the four XL
-    Linears on dequantized operands, one thread per core."""
+    """The reference's host path timed on this host (BASELINE.md's plan):
+    plain C restatements of the reference's FC loops -- (i) the GTest helper's
+    bias-first forward (tests/layers/fully_connected_layer_test.cu:29-46;
+    its backward helpers are the kernel's loop order for dX and a one-sample
+    outer product for dW), (ii) the kernel-order forward, dX and dW
+    (dnn/layers/fully_connected_layer.cu:29-35,54-59,78-83) -- and the
+    conversion contract (absmax, e4m3 quantize, dequantize), built with
+    -O3 -march=native for this host's CPU (make -C oracle native; falls back
+    to the -O2 oracle build if the compiler is unavailable).  Each runs on
+    one thread and on every core this process may use; `tokens` is the token
+    slice of configs 3 and 4 on all cores (single-thread config 4 uses an
+    eighth of it).  Config 1 and config 2 run in full."""
+    import subprocess
+    import tempfile
+
     import numpy as np
 
     from deepfuse_amd import synth
     from oracle import pyoracle as orc
 
-    threads = orc.nthreads()
-    flops = 0
-    t_total = 0.0
-    for i, (name, K, N) in enumerate(XL_LINEARS):
-        seed = synth.SEED_BASE + 4 + 10 * i
-        X = synth.normal((tokens, K), 1.0, seed=seed)
-        W = synth.normal((N, K), 0.02, seed=seed + 1)
-        b = synth.normal((N,), 0.02, seed=seed + 2)
-        dY = synth.normal((tokens, N), 1e-3, seed=seed + 3)
-        t0 = time.perf_counter()
-        orc.fc_forward(X, W, b, threads=threads)
-        orc.fc_backward_input(dY, W, threads=threads)
-        orc.fc_backward_weights(dY, X, threads=threads)
-        t_total += time.perf_counter() - t0
-        flops += 3 * 2 * tokens * N * K
+    root = os.path.dirname(os.path.abspath(__file__))
+    build = "-O3 -march=native (make -C oracle native)"
+    tmp = tempfile.mkdtemp(prefix="df_cpu_baseline_")
+    out = os.path.join(tmp, "libdf_oracle_native.so")
+    try:
+        subprocess.run(["make", "-s", "-C", os.path.join(root, "oracle"), "native", f"NATIVE_OUT={out}"],
+                       check=True, timeout=120, capture_output=True)
+        L = orc.load(out)
+    except (OSError, subprocess.SubprocessError):
+        build = "-O2 -ffp-contract=off (the oracle build; the native build failed)"
+        L = orc.lib()
+    hw = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = hw
+    omp = os.environ.get("OMP_NUM_THREADS")
+    all_threads = max(1, min(avail, int(omp))) if omp and omp.isdigit() else avail
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -1442,28 +1458,101 @@ def cpu_baseline(tokens):
                     break
     except OSError:
         pass
-    # the conversion contract on the first 2^26 elements of the config-2 fp32
-    # tensor (outliers, +-inf, NaN, subnormals), e4m3
-    n = 1 << 26
-    x = synth.conversion_input(n)
-    conv = {"n": n, "input": "config-2 fp32 tensor, first 2^26 elements", "fmt": "e4m3"}
-    t0 = time.perf_counter()
-    am = orc.absmax(x)
-    conv["absmax_gbs_1thread"] = round(4 * n / (time.perf_counter() - t0) / 1e9, 3)
-    sc = orc.scale(am, orc.E4M3)
-    for nt in (1, threads):
-        t0 = time.perf_counter()
-        q = orc.quantize(x, sc, orc.E4M3, threads=nt)
-        conv[f"quantize_gbs_{nt}thread" + ("s" if nt > 1 else "")] = round(5 * n / (time.perf_counter() - t0) / 1e9, 3)
-    t0 = time.perf_counter()
-    orc.dequantize(q, sc, orc.E4M3)
-    conv["dequantize_f32_gbs_1thread"] = round(5 * n / (time.perf_counter() - t0) / 1e9, 3)
-    return {"value": round(flops / t_total / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port", "seconds": round(t_total, 2), "cpu": model,
-            "sample": f"oracle fp32 kernel-order loops, fwd+dX+dW of the 4 GPT-2 XL Linears on a "
-                      f"{tokens}-token slice ({flops} flop), {threads} threads",
-            "conversion": conv}
+    P = lambda a: a.ctypes.data
 
+    def best(fn, reps):
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        return min(t)
+
+    def fc_case(N, K, O, seed, threads, reps, backward):
+        X = synth.normal((N, K), 1.0, seed=seed)
+        W = synth.normal((O, K), 0.02, seed=seed + 1)
+        b = synth.normal((O,), 0.02, seed=seed + 2)
+        Y = np.empty((N, O), np.float32)
+        r = {}
+        fl = 2.0 * N * K * O
+        t = best(lambda: L.dfo_fc_forward(P(X), P(W), P(b), P(Y), N, K, O, threads), reps)
+        r["fwd_kernel_order"] = fl / t / 1e9
+        t = best(lambda: L.dfo_fc_forward_bias_first(P(X), P(W), P(b), P(Y), N, K, O, threads), reps)
+        r["fwd_gtest_bias_first"] = fl / t / 1e9
+        if backward:
+            dY = synth.normal((N, O), 1e-3, seed=seed + 3)
+            dX = np.empty((N, K), np.float32)
+            dW = np.empty((O, K), np.float32)
+            t = best(lambda: (L.dfo_fc_backward_input(P(dY), P(W), P(dX), N, K, O, threads),
+                              L.dfo_fc_backward_weights(P(dY), P(X), P(dW), N, K, O, threads)), reps)
+            r["bwd_dx_dw_kernel_order"] = 2 * fl / t / 1e9
+        return r, fl
+
+    res = {"build": build, "hardware_concurrency": hw, "cores_available": avail, "threads_all": all_threads,
+           "cpu": model, "unit": "GFLOP/s (FC) or GB/s (conversion), best of the repetitions"}
+    # config 1: 64 x 768 -> 3072, in full
+    for th in (1, all_threads):
+        r, _ = fc_case(64, 768, 3072, synth.SEED_BASE + 1, th, 5, False)
+        res[f"config1_{th}t"] = {k: round(v, 2) for k, v in r.items()}
+    # config 3: the four GPT-2 small Linears, forward, on a token slice
+    for th, n_tok, reps in ((1, tokens, 1), (all_threads, tokens, 3)):
+        agg = {}
+        for i, (_, K, N) in enumerate(SMALL_LINEARS):
+            r, fl = fc_case(n_tok, K, N, synth.SEED_BASE + 3 + 10 * i, th, reps, False)
+            for k, v in r.items():
+                agg.setdefault(k, [0.0, 0.0])
+                agg[k][0] += fl
+                agg[k][1] += fl / (v * 1e9)
+        res[f"config3_{th}t"] = {"tokens": n_tok, **{k: round(a / b / 1e9, 2) for k, (a, b) in agg.items()}}
+    # config 4: the four GPT-2 XL Linears, forward and backward
+    c4_flops = c4_time = 0.0
+    for th, n_tok, reps in ((1, max(tokens // 8, 16), 1), (all_threads, tokens, 2)):
+        agg = {}
+        for i, (_, K, N) in enumerate(XL_LINEARS):
+            r, fl = fc_case(n_tok, K, N, synth.SEED_BASE + 4 + 10 * i, th, reps, True)
+            for k, v in r.items():
+                w = 2 * fl if k.startswith("bwd") else fl
+                agg.setdefault(k, [0.0, 0.0])
+                agg[k][0] += w
+                agg[k][1] += w / (v * 1e9)
+        res[f"config4_{th}t"] = {"tokens": n_tok, **{k: round(a / b / 1e9, 2) for k, (a, b) in agg.items()}}
+        if th == all_threads:
+            c4_flops = agg["fwd_kernel_order"][0] + agg["bwd_dx_dw_kernel_order"][0]
+            c4_time = agg["fwd_kernel_order"][1] + agg["bwd_dx_dw_kernel_order"][1]
+    # config 2: the conversion contract on the full 2^28-element fp32 tensor, e4m3
+    n = 1 << 28
+    x = synth.conversion_input(n)
+    q = np.empty(n, np.uint8)
+    d = np.empty(n, np.float32)
+    conv = {"n": n, "input": "config-2 fp32 tensor (outliers, +-inf, NaN, subnormals)", "fmt": "e4m3"}
+    t = best(lambda: L.dfo_absmax_f32(P(x), n), 1)
+    am = L.dfo_absmax_f32(P(x), n)
+    conv["absmax_1t"] = round(4 * n / t / 1e9, 3)
+    sc = L.dfo_scale(am, orc.E4M3)
+    t = best(lambda: L.dfo_quantize_f32(P(x), n, sc, orc.E4M3, P(q)), 1)
+    conv["quantize_1t"] = round(5 * n / t / 1e9, 3)
+    chunk = (n + all_threads - 1) // all_threads
+
+    def quant_all():
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(all_threads) as ex:
+            list(ex.map(lambda j: L.dfo_quantize_f32(P(x) + 4 * j * chunk, min(chunk, n - j * chunk), sc,
+                                                     orc.E4M3, P(q) + j * chunk), range(all_threads)))
+
+    t = best(quant_all, 2)
+    conv[f"quantize_{all_threads}t"] = round(5 * n / t / 1e9, 3)
+    t = best(lambda: L.dfo_dequantize_f32(P(q), n, sc, orc.E4M3, P(d)), 1)
+    conv["dequantize_1t"] = round(5 * n / t / 1e9, 3)
+    res["config2"] = conv
+    del x, q, d
+    value = c4_flops / c4_time / 1e12
+    return {"value": round(value, 5), "unit": "TFLOP/s", "cores": all_threads, "kind": "port",
+            "cpu": model, "hardware_concurrency": hw, "build": build,
+            "sample": f"kernel-order FC loops (the reference's fully_connected_layer.cu:29-35,54-59,78-83, "
+                      f"restated in C), fwd + dX + dW of the 4 GPT-2 XL Linears on a {tokens}-token slice of "
+                      f"config 4, {all_threads} threads ({hw} hardware threads on this host); per-config and "
+                      f"single-thread figures in `detail`",
+            "detail": res}
 
 if __name__ == "__main__":
     main()

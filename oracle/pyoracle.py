@@ -57,17 +57,23 @@ _SIGS = {
 _lib = None
 
 
+def load(path: str) -> ctypes.CDLL:
+    """A build of df_oracle.c at `path` with every signature declared (the
+    default build, or the CPU-baseline build of `make -C oracle native`)."""
+    L = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} missing: run make -C oracle")
-        L = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in _SIGS.items():
-            fn = getattr(L, name)
-            fn.restype = res
-            fn.argtypes = args
-        _lib = L
+        _lib = load(LIB_PATH)
     return _lib
 
 
