@@ -346,10 +346,11 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
 // up to ldq) and of qt (columns up to ldqt) is written in the same pass.
 // NT (default: AMAX without LN, i.e. delayed scaling, where no absmax or
 // statistics pass has just read x) makes the loads of x and the stores of
-// q / qt non-temporal.  On the 16384 x {1600, 4800,
-// 6400} bf16 operands of GPT-2 XL that made the delayed-scaling step 3.5%
-// faster; after an absmax pass the cached re-read of x hits the Infinity
-// Cache and plain accesses are faster.
+// q / qt non-temporal.  On the 16384 x {1600, 4800, 6400} bf16 operands of
+// GPT-2 XL that made the delayed-scaling config-4 step about 2% faster
+// (2.001-2.016 ms against 2.039-2.057 ms, alternating runs on one box);
+// after an absmax pass the cached re-read of x hits the Infinity Cache and
+// plain accesses are faster.
 // With COLSUM the block also folds the fp32 values of its tile into one
 // partial sum per column (rows in fixed order), written to
 // colpart[tile_row][col] for a deterministic second pass.

@@ -102,6 +102,7 @@ private:
     std::optional<tensor<fp8_e4m3>> xt_cache_;  // X^T codes [in, round16(N)] + scale
     Scratch absmax_ws_, colsum_ws_, gemm_ws_, codes_a_, codes_b_, codes_c_, scales_, colsum_;
     Scratch codes_wt_;  // W^T codes [in, round16(out)] from the training forward, read by backward
+    bool wt_stale_ = false;  // load() replaced the weights after the forward that wrote codes_wt_
     int history_len_ = 0;
     Delayed dx_, dw_, ddy_;
     const float* sx_used_ = nullptr;  // delayed: scales of the cached forward's X and W codes

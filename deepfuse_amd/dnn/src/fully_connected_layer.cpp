@@ -267,14 +267,23 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
     uint8_t* dyq = codes_a_.get((size_t)N * Op);
     uint8_t* dyt = codes_c_.get((size_t)out_features_ * Np);
     float* db = reinterpret_cast<float*>(colsum_.get((size_t)out_features_ * sizeof(float)));
-    // W^T codes and their scale: written by the forward's W pass
+    // W^T codes and their scale: written by the forward's W pass, or here
+    // when load() replaced the weights after that forward (the reference's
+    // backward reads weights_ as they are now)
     const uint8_t* wt = codes_wt_.p;
     const float* sdy = sc + 2;
     const float* sw = sc + 1;
     const float* sx = xt_cache_->scale_data();
+    if (wt_stale_) {
+        uint8_t* wtn = codes_wt_.get((size_t)in_features_ * Op);
+        quantize_operand(this->weights_.data(), out_features_, in_features_, DF_FMT_E4M3, sc + 1, nullptr, 0, wtn,
+                         Op, nullptr);
+        wt = wtn;
+        wt_stale_ = false;
+    }
     if (history_len_ > 0 && sx_used_) {
         sdy = quantize_delayed(ddy_, grad_output.data(), N, out_features_, DF_FMT_E5M2, dyq, Op, dyt, Np, db);
-        sw = sw_used_;
+        if (sw_used_) sw = sw_used_;
         sx = sx_used_;
     } else {
         quantize_operand(grad_output.data(), N, out_features_, DF_FMT_E5M2, sc + 2, dyq, Op, dyt, Np, db);
@@ -308,6 +317,7 @@ void FullyConnectedLayer<TT>::save_fp8(std::ostream& out) const {
 
 template <typename TT>
 void FullyConnectedLayer<TT>::load(std::istream& in) {
+    const int old_in = in_features_, old_out = out_features_;
     in.read(reinterpret_cast<char*>(&in_features_), sizeof(in_features_));
     in.read(reinterpret_cast<char*>(&out_features_), sizeof(out_features_));
     this->weights_.load(in);
@@ -315,8 +325,15 @@ void FullyConnectedLayer<TT>::load(std::istream& in) {
     if (this->grad_weights_.shape() != this->weights_.shape())
         this->grad_weights_ = tensor<TT>(this->weights_.shape());
     if (this->grad_bias_.shape() != this->bias_.shape()) this->grad_bias_ = tensor<TT>(this->bias_.shape());
-    xt_cache_.reset();
-    cached_n_ = -1;
+    if (in_features_ != old_in || out_features_ != old_out) {
+        // a layer of another shape: the cached input no longer fits
+        xt_cache_.reset();
+        cached_n_ = -1;
+    }
+    // like the reference, a backward after load() uses the cached input and
+    // the loaded weights: their W^T codes are made again by that backward
+    wt_stale_ = true;
+    sw_used_ = nullptr;
 }
 
 template class FullyConnectedLayer<float>;

@@ -769,6 +769,29 @@ TEST_F(FullyConnectedLayerTest, SaveLoadRoundTrip) {
     EXPECT_TRUE(a.forward(input).equals(b.forward(input)));
 }
 
+TEST_F(FullyConnectedLayerTest, BackwardAfterLoadUsesLoadedWeights) {
+    // The reference's backward reads weights_ at backward time and keeps its
+    // input cache across load(): forward on layer a, load b's weights into a,
+    // then backward equals a fresh layer with b's weights run forward +
+    // backward on the same input (same X codes, same W codes, same dY).
+    FullyConnectedLayer<float> a(48, 20, true), b(48, 20, true);
+    tensor<float> input({8, 48}), grad({8, 20});
+    const auto xi = uniform(8 * 48, -1.0f, 1.0f, 41), gi = uniform(8 * 20, -0.01f, 0.01f, 42);
+    input.upload(xi.data());
+    grad.upload(gi.data());
+    a.forward(input);
+    std::stringstream ss;
+    b.save(ss);
+    a.load(ss);
+    const auto dxa = download(a.backward(grad));
+    b.forward(input);
+    const auto dxb = download(b.backward(grad));
+    ASSERT_EQ(dxa.size(), dxb.size());
+    for (size_t i = 0; i < dxa.size(); ++i) EXPECT_EQ(dxa[i], dxb[i]);
+    EXPECT_TRUE(a.gradients()[0]->equals(*b.gradients()[0]));
+    EXPECT_TRUE(a.gradients()[1]->equals(*b.gradients()[1]));
+}
+
 TEST_F(FullyConnectedLayerTest, SaveFp8LoadsDequantizedWeights) {
     FullyConnectedLayer<float> a(40, 24, false);
     std::stringstream full, small;

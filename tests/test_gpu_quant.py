@@ -249,12 +249,15 @@ def test_quantize_2d_layouts(dev, fmt):
 BATCH_SHAPES = [(4800, 1600), (1600, 1600), (0, 5), (1, 1), (129, 257), (6400, 1600), (3, 40), (1600, 6400)]
 
 
+@pytest.mark.parametrize("given_absmax", [False, True], ids=["own_absmax", "given_absmax"])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("fmt", [Fmt.E4M3, Fmt.E5M2])
-def test_quantize_2d_batch_matches_single_calls(dev, dtype, fmt):
+def test_quantize_2d_batch_matches_single_calls(dev, dtype, fmt, given_absmax):
     """df_quantize_2d_batch gives every tensor the absmax, scale, row codes
     and transposed codes that df_absmax_scale + df_quantize_2d give it alone
-    (ragged shapes, an empty tensor, a 1x1, the GPT-2 XL weights)."""
+    (ragged shapes, an empty tensor, a 1x1, the GPT-2 XL weights).  With the
+    absmax given (df_quantize_2d_batch_absmax) the tile pass runs its
+    non-temporal instantiation, for both dtypes and formats."""
     rng = np.random.default_rng(7)
     ts = []
     for i, (r, c) in enumerate(BATCH_SHAPES):
@@ -263,13 +266,32 @@ def test_quantize_2d_batch_matches_single_calls(dev, dtype, fmt):
             x.reshape(-1)[rng.integers(0, x.size)] = 50.0 * (i + 1)  # an outlier sets each tensor's scale
         t = to_dev_f32(x, dev)
         ts.append(t if dtype == "f32" else t.to(torch.bfloat16))
-    am, sc, qs, qts = df.quantize_2d_batch(ts, fmt)
+    given = None
+    if given_absmax:
+        given = torch.stack([df.absmax_scale(t, fmt)[0][0] if t.numel() else torch.zeros((), device=dev)
+                             for t in ts]).contiguous()
+    am, sc, qs, qts = df.quantize_2d_batch(ts, fmt, absmax=given)
     for i, t in enumerate(ts):
         a1, s1 = df.absmax_scale(t, fmt)
         q1, qt1 = df.quantize_2d(t, s1, fmt, want_q=True, want_qt=True)
         assert am[i].item() == a1.item() and sc[i].item() == s1.item(), f"tensor {i} {tuple(t.shape)}"
         assert torch.equal(qs[i], q1), f"q of tensor {i} {tuple(t.shape)}"
         assert torch.equal(qts[i], qt1), f"qt of tensor {i} {tuple(t.shape)}"
+
+
+def test_quantize_2d_batch_beyond_cache(dev):
+    """A batch whose inputs exceed the 256 MB Infinity Cache (4 x 8192 x
+    2304 fp32 = 302 MB) takes the non-temporal tile pass after its own
+    absmax pass; every tensor still gets the single calls' scale and codes."""
+    ts = [torch.randn((8192, 2304), device=dev) * (0.5 + i) for i in range(4)]
+    am, sc, qs, qts = df.quantize_2d_batch(ts, Fmt.E4M3)
+    for i, t in enumerate(ts):
+        a1, s1 = df.absmax_scale(t, Fmt.E4M3)
+        q1, qt1 = df.quantize_2d(t, s1, Fmt.E4M3, want_q=True, want_qt=True)
+        assert am[i].item() == a1.item() and sc[i].item() == s1.item(), f"tensor {i}"
+        assert torch.equal(qs[i], q1) and torch.equal(qts[i], qt1), f"codes of tensor {i}"
+    del ts, qs, qts
+    torch.cuda.empty_cache()
 
 
 def test_quantize_2d_batch_many_tensors(dev):
