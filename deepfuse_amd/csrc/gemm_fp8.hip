@@ -472,6 +472,17 @@ __device__ __forceinline__ constexpr int waitcnt_vm_lgkm0(int n) {
     return (n & 15) | ((n >> 4) << 14) | 0x70;
 }
 
+// The lane index, computed afresh where it is called.  The asm is opaque to
+// the optimiser, so offsets derived from it stay where they are used: taken
+// from threadIdx, the epilogue's per-lane offsets were hoisted out of the
+// tile loop and, at the main loop's register pressure, spilled; each reload
+// in the epilogue then waited on vmcnt(0), i.e. for the DMA in flight.
+__device__ __forceinline__ int fresh_lane() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 // Epilogue geometry for an output element of ES bytes: each 32-row block of
 // a wave's 128x64 quarter passes through an LDS slab of SR rows.
 template <int ES>
@@ -523,6 +534,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = w >> 2, wn = w & 3;
     uint8_t* const slab = lds + 2 * kPStage + kPBiasSlots * kPBiasSlot + w * SLAB;
+    // a bf16 bias of odd length: its last element, which the dword bias DMA
+    // cannot deliver (it shares a dword with the end of the buffer), read
+    // once here rather than in every epilogue
+    uint32_t bias_tail = 0;
+    if (HAS_BIAS && sizeof(BiasT) == 2 && (N & 1))
+        bias_tail = __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint16_t*>(bias)[N - 1]);
     const int tiles_m = (M + kPBM - 1) / kPBM, tiles_n = (N + kPBN - 1) / kPBN;
     const int ntiles = tiles_m * tiles_n;
     const int nk = (K + kPKB - 1) / kPKB;
@@ -645,7 +662,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 q1 ? rB1 : rB, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
                 ((d & 1) ? ob1 : ob0) + (uint32_t)(d >> 1) * b16, 0, 0, 0);
-        } else if (HAS_BIAS) {
+        } else if (HAS_BIAS && d_k == 0) {  // a tile's bias, once, with its first step
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rBias,
                 (__attribute__((address_space(3))) void*)(lbias + ((uint32_t)d_tile % kPBiasSlots) * kPBiasSlot +
@@ -774,9 +791,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         constexpr int ES = (int)sizeof(T);
         constexpr int SR = EpiGeom<ES>::SR, SROW = EpiGeom<ES>::SROW;
         constexpr int NPASS = EpiGeom<ES>::NPASS, SPP = EpiGeom<ES>::SPP;
+        const int el = fresh_lane(), efr = el & 31;
         const int rowb = tm0 + wm * 128;
         const int colw = tn0 + wn * 64;
-        const int h4 = (lane >> 5) * 4;
+        const int h4 = (el >> 5) * 4;
         const uint8_t* bsl = lbias + ((uint32_t)tile % kPBiasSlots) * kPBiasSlot;
         // bias of the lane's columns colw + 32j + 8g + h4 + (0..3): fp32 as
         // values (bv), bf16 as the raw pairs (braw: 16 registers instead of
@@ -784,12 +802,11 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         // epilogue within the register budget next to the next tile's
         // fragments).  A bf16 bias of odd length: its last element shares a
         // dword with the end of the buffer, which the dword DMA returned as
-        // zero, so it is patched in from global memory.
+        // zero, so it is patched in from bias_tail.
         constexpr bool PACKB = BIAS && sizeof(BiasT) == 2;
         float bv[FN][4][4];
         uint32_t braw[FN][4][2];
-        uint32_t tbits = 0;
-        if (PACKB && (No & 1) && colw + 64 >= No) tbits = reinterpret_cast<const uint16_t*>(bias)[No - 1];
+        const uint32_t tbits = bias_tail;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -818,10 +835,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         // slab read-back geometry: lane -> (row, 16-byte chunk)
         constexpr int CPR = 64 * ES / 16;
         constexpr int RPS = 64 / CPR;
-        const int srow = lane / CPR, rc = lane % CPR;
+        const int srow = el / CPR, rc = el % CPR;
         const int scol = colw + rc * (16 / ES);
         const bool col_full = veco && scol + 16 / ES <= No;
-        const int my_sr = fr % SR, my_pass = fr / SR;
+        const int my_sr = efr % SR, my_pass = efr / SR;
         typedef typename std::conditional<ES == 2, u32x2, f32x4>::type Pk;
         // LDS operations of one wave execute in order, so a pass's reads see
         // its writes and precede the next pass's writes; the empty asm
