@@ -503,7 +503,7 @@ struct PProb {
     void* C;
     const float* sa;
     const float* sb;
-    int lda, ldb, M, N, K, ldc, vec_out;
+    int lda, ldb, M, N, K, ldc, vec_out;  // vec_out: an epi_store_mode
 };
 
 // cost of a work unit beyond its DMA steps (pipeline fill, epilogue), in
@@ -883,7 +883,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                     if (row < Mo) {
                         T* dst = Cu + (int64_t)row * ldco + scol;
                         if (col_full) {
-                            __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+                            if (veco == 2)
+                                __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+                            else
+                                *reinterpret_cast<u32x4*>(dst) = val;
                         } else {
                             const T* ev = reinterpret_cast<const T*>(&val);
 #pragma unroll
@@ -1065,6 +1068,18 @@ static void launch_cfg(const GemmArgs& g) {
                                                                 static_cast<OutT*>(g.C), g.ldc, vec_red);
 }
 
+// Store mode of the persistent kernel's epilogue: 0 element stores, 1
+// 16-byte stores, 2 16-byte non-temporal stores.  One store instruction
+// writes whole 64-column row segments (128 bytes of bf16, 256 of fp32);
+// non-temporal stores are kept to rows that start on a 128-byte boundary, so
+// that no cache line is written in parts by several non-temporal stores (in
+// a probe that did so -- 8-byte non-temporal stores -- one output of sixteen
+// came back different, where plain stores matched).
+static int epi_store_mode(const void* C, int64_t ldc_bytes) {
+    if (ldc_bytes % 16 != 0 || !aligned16(C)) return 0;
+    return (ldc_bytes % 128 == 0 && ((uintptr_t)C & 127u) == 0) ? 2 : 1;
+}
+
 // The persistent kernel takes outputs with at least one 256x256 tile per CU
 // (smaller ones keep the split-K plan below).  Its per-lane buffer offsets
 // reach a tile past the last row, so M*lda and N*ldb stay below 2^31 (and
@@ -1112,7 +1127,7 @@ static PSplit persistent_split_plan(int M, int N, int K, size_t ws_bytes, int cu
 
 template <int FA, int FB, typename OutT, typename BiasT>
 static void launch_persistent(const GemmArgs& g, int grid) {
-    const int vec_out = ((int64_t)g.ldc * (int64_t)sizeof(OutT)) % 16 == 0 && aligned16(g.C);
+    const int vec_out = epi_store_mode(g.C, (int64_t)g.ldc * (int64_t)sizeof(OutT));
     if (g.bias)
         gemm_nt_persistent_kernel<FA, FB, OutT, BiasT, true><<<grid, 512, 0, g.st>>>(
             g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, static_cast<const BiasT*>(g.bias),
@@ -1167,7 +1182,8 @@ static void launch_shape(const GemmArgs& g) {
             return;
         }
         gemm_nt_persistent_kernel<FA, FB, float, BiasT, false, true><<<p.grid, 512, 0, g.st>>>(
-            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, g.ws, g.N, g.N % 4 == 0, p.L, p.split);
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, g.ws, g.N,
+            epi_store_mode(g.ws, (int64_t)g.N * 4), p.L, p.split);
         const int64_t total = (int64_t)g.M * g.N;
         const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
         const bool vec_red = (g.N % 4 == 0) && ((int64_t)g.ldc * (int64_t)sizeof(OutT)) % 16 == 0 && aligned16(g.C);
@@ -1234,17 +1250,17 @@ static GroupPlan grouped_plan(const GemmArgs& dw, const GemmArgs& dx, size_t ws_
 template <typename DwT, typename DxT>
 static void launch_grouped(const GemmArgs& dw, const GemmArgs& dx, const GroupPlan& gp, int cus) {
     const PProb p1{dx.A, dx.B, dx.C, dx.sa, dx.sb, dx.lda, dx.ldb, dx.M, dx.N, dx.K, dx.ldc,
-                   ((int64_t)dx.ldc * (int64_t)sizeof(DxT)) % 16 == 0 && aligned16(dx.C)};
+                   epi_store_mode(dx.C, (int64_t)dx.ldc * (int64_t)sizeof(DxT))};
     if (gp.S == 1) {
-        const int vec_out = ((int64_t)dw.ldc * (int64_t)sizeof(DwT)) % 16 == 0 && aligned16(dw.C);
+        const int vec_out = epi_store_mode(dw.C, (int64_t)dw.ldc * (int64_t)sizeof(DwT));
         gemm_nt_persistent_kernel<E5M2, E4M3, DwT, float, false, false, DxT><<<cus, 512, 0, dw.st>>>(
             dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, static_cast<DwT*>(dw.C), dw.ldc,
             vec_out, 0, 1, p1);
         return;
     }
     gemm_nt_persistent_kernel<E5M2, E4M3, float, float, false, true, DxT><<<cus, 512, 0, dw.st>>>(
-        dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, dw.ws, dw.N, dw.N % 4 == 0, gp.L, gp.S,
-        p1);
+        dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, dw.ws, dw.N,
+        epi_store_mode(dw.ws, (int64_t)dw.N * 4), gp.L, gp.S, p1);
     const int64_t total = (int64_t)dw.M * dw.N;
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
     const bool vec_red = (dw.N % 4 == 0) && ((int64_t)dw.ldc * (int64_t)sizeof(DwT)) % 16 == 0 && aligned16(dw.C);
