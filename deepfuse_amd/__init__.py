@@ -64,6 +64,8 @@ _SIGS = {
     "df_absmax_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _c_sz, _vp]),
     "df_absmax_scale_f32": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "df_absmax_scale_bf16": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "df_absmax_f16": (_c_int, [_vp, _c_i64, _vp, _vp, _c_sz, _vp]),
+    "df_absmax_scale_f16": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "df_compute_scale": (_c_int, [_vp, _c_int, _vp, _vp]),
     "df_hbm_probe_dst_bytes": (_c_sz, [_c_int, _c_int, _c_i64]),
     "df_hbm_probe": (_c_int, [_c_int, _c_int, _vp, _c_i64, _vp, _vp]),
@@ -196,7 +198,13 @@ def _in_dtype(t) -> DType:
         return DType.FLOAT32
     if t.dtype == torch.bfloat16:
         return DType.BFLOAT16
+    if t.dtype == torch.float16:
+        return DType.HALF
     raise TypeError(f"unsupported input dtype {t.dtype}")
+
+
+_ABSMAX_SCALE = {DType.FLOAT32: "df_absmax_scale_f32", DType.BFLOAT16: "df_absmax_scale_bf16",
+                 DType.HALF: "df_absmax_scale_f16"}
 
 
 _WS = {}
@@ -216,8 +224,8 @@ def absmax_scale(x, fmt: Fmt):
     am = torch.empty(1, dtype=torch.float32, device=x.device)
     sc = torch.empty(1, dtype=torch.float32, device=x.device)
     ws = _workspace(x.device)
-    fn = "df_absmax_scale_f32" if _in_dtype(x) == DType.FLOAT32 else "df_absmax_scale_bf16"
-    call(fn, _ptr(x), x.numel(), int(fmt), _ptr(am), _ptr(sc), _ptr(ws), ws.numel(), _stream())
+    call(_ABSMAX_SCALE[_in_dtype(x)], _ptr(x), x.numel(), int(fmt), _ptr(am), _ptr(sc), _ptr(ws), ws.numel(),
+         _stream())
     return am, sc
 
 
@@ -294,8 +302,8 @@ def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dty
     out_dtype = out_dtype or torch.float32
     M, N = a_q.shape[0], b_q.shape[0]
     c = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
-    bias_dt = int(DType.FLOAT32) if bias is None or bias.dtype == torch.float32 else int(DType.BFLOAT16)
-    c_dt = int(DType.FLOAT32) if out_dtype == torch.float32 else int(DType.BFLOAT16)
+    bias_dt = int(DType.FLOAT32) if bias is None else int(_in_dtype(bias))
+    c_dt = int(_in_dtype(c))
     ws = gemm_workspace(M, N, K, a_q.device) if split_k else None
     call("df_fp8_gemm_nt", int(fmt_a), _ptr(a_q), a_q.stride(0), int(fmt_b), _ptr(b_q), b_q.stride(0),
          M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _ptr(ws),
@@ -331,7 +339,7 @@ def gemm_bwd(dy_q, wt_q, dyt_q, xt_q, M: int, N: int, K: int, sdy, sw, sx, dx_dt
     dev = dy_q.device
     dX = torch.empty((M, K), dtype=dx_dtype, device=dev)
     dW = torch.empty((N, K), dtype=dw_dtype, device=dev)
-    dt = lambda t: int(DType.FLOAT32) if t == torch.float32 else int(DType.BFLOAT16)
+    dt = lambda t: int(_in_dtype(torch.empty(0, dtype=t)))
     ws = None
     if workspace:
         ws = _scratch(dev, max(int(lib().df_fp8_gemm_bwd_workspace_bytes(M, N, K)), 16), "gemm_bwd")

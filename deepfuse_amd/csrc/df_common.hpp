@@ -201,6 +201,13 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
     return nan ? __uint_as_float(((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x03FFu) << 13)) : v;
 }
 
+// A binary16 element in kernel templates: the storage of DF_DTYPE_HALF,
+// distinct from uint16_t, which there always holds bf16 bits.
+struct f16_t {
+    uint16_t bits;
+};
+static_assert(sizeof(f16_t) == 2, "f16_t is two bytes");
+
 // ------------------------------------------------------------- host side --
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();

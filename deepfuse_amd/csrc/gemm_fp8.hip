@@ -56,8 +56,12 @@ template <> struct OutCvt<float> {
 template <> struct OutCvt<uint16_t> {  // bf16 bits
     static __device__ __forceinline__ uint16_t cvt(float v) { return (uint16_t)f32_to_bf16_rne(v); }
 };
+template <> struct OutCvt<f16_t> {
+    static __device__ __forceinline__ f16_t cvt(float v) { return f16_t{(uint16_t)f32_to_f16_rne(v)}; }
+};
 __device__ __forceinline__ float bias_ld(const float* b, int i) { return b[i]; }
 __device__ __forceinline__ float bias_ld(const uint16_t* b, int i) { return bf16_to_f32(b[i]); }
+__device__ __forceinline__ float bias_ld(const f16_t* b, int i) { return f16_to_f32(b[i].bits); }
 
 // 4 consecutive outputs of one row: one 16-byte (fp32) or 8-byte (bf16) store
 __device__ __forceinline__ void store4(float* p, const float* v) {
@@ -66,6 +70,10 @@ __device__ __forceinline__ void store4(float* p, const float* v) {
 __device__ __forceinline__ void store4(uint16_t* p, const float* v) {
     *reinterpret_cast<u32x2*>(p) = u32x2{f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16),
                                         f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16)};
+}
+__device__ __forceinline__ void store4(f16_t* p, const float* v) {
+    *reinterpret_cast<u32x2*>(p) = u32x2{f32_to_f16_rne(v[0]) | (f32_to_f16_rne(v[1]) << 16),
+                                        f32_to_f16_rne(v[2]) | (f32_to_f16_rne(v[3]) << 16)};
 }
 
 __device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
@@ -534,7 +542,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = w >> 2, wn = w & 3;
     uint8_t* const slab = lds + 2 * kPStage + kPBiasSlots * kPBiasSlot + w * SLAB;
-    // a bf16 bias of odd length: its last element, which the dword bias DMA
+    // a 2-byte bias of odd length: its last element, which the dword bias DMA
     // cannot deliver (it shares a dword with the end of the buffer), read
     // once here rather than in every epilogue
     uint32_t bias_tail = 0;
@@ -797,10 +805,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const int h4 = (el >> 5) * 4;
         const uint8_t* bsl = lbias + ((uint32_t)tile % kPBiasSlots) * kPBiasSlot;
         // bias of the lane's columns colw + 32j + 8g + h4 + (0..3): fp32 as
-        // values (bv), bf16 as the raw pairs (braw: 16 registers instead of
+        // values (bv), bf16 or f16 as the raw pairs (braw: 16 registers instead of
         // 32, widened where they are added, which keeps the forward's
         // epilogue within the register budget next to the next tile's
-        // fragments).  A bf16 bias of odd length: its last element shares a
+        // fragments).  A 2-byte bias of odd length: its last element shares a
         // dword with the end of the buffer, which the dword DMA returned as
         // zero, so it is patched in from bias_tail.
         constexpr bool PACKB = BIAS && sizeof(BiasT) == 2;
@@ -852,7 +860,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 for (int g = 0; g < 4; ++g) {
                     const v16f& a = acc[i][j];
                     float c0 = bv[j][g][0], c1 = bv[j][g][1], c2 = bv[j][g][2], c3 = bv[j][g][3];
-                    if (PACKB) {
+                    if (PACKB && std::is_same<BiasT, f16_t>::value) {
+                        // plain widening: a NaN bias makes a NaN output,
+                        // whose payload the output conversion replaces
+                        c0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(braw[j][g][0] & 0xFFFFu));
+                        c1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(braw[j][g][0] >> 16));
+                        c2 = (float)__builtin_bit_cast(_Float16, (uint16_t)(braw[j][g][1] & 0xFFFFu));
+                        c3 = (float)__builtin_bit_cast(_Float16, (uint16_t)(braw[j][g][1] >> 16));
+                    } else if (PACKB) {
                         c0 = __uint_as_float(braw[j][g][0] << 16);
                         c1 = __uint_as_float(braw[j][g][0] & 0xFFFF0000u);
                         c2 = __uint_as_float(braw[j][g][1] << 16);
@@ -860,7 +875,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                     }
                     const float v0 = a[4 * g] * sabo + c0, v1 = a[4 * g + 1] * sabo + c1;
                     const float v2 = a[4 * g + 2] * sabo + c2, v3 = a[4 * g + 3] * sabo + c3;
-                    if constexpr (ES == 2)
+                    if constexpr (std::is_same<T, f16_t>::value)
+                        pk[j][g] = u32x2{f32_to_f16_rne(v0) | (f32_to_f16_rne(v1) << 16),
+                                         f32_to_f16_rne(v2) | (f32_to_f16_rne(v3) << 16)};
+                    else if constexpr (ES == 2)
                         pk[j][g] = u32x2{pack_bf16_rne(v0, v1), pack_bf16_rne(v2, v3)};
                     else
                         pk[j][g] = f32x4{v0, v1, v2, v3};
@@ -1268,12 +1286,18 @@ static void launch_grouped(const GemmArgs& dw, const GemmArgs& dx, const GroupPl
                                                                  static_cast<DwT*>(dw.C), dw.ldc, vec_red);
 }
 
+// output and bias element types (nt_args admits: fp32 or bf16 output with
+// an fp32 or bf16 bias, f16 output with an fp32 or f16 bias)
 template <int FA, int FB>
 static void dispatch_out(const GemmArgs& g, int bias_dtype, int c_dtype) {
     const bool bf16_bias = g.bias && bias_dtype == DF_DTYPE_BFLOAT16;
+    const bool f16_bias = g.bias && bias_dtype == DF_DTYPE_HALF;
     if (c_dtype == DF_DTYPE_FLOAT32) {
         if (bf16_bias) launch_shape<FA, FB, float, uint16_t>(g);
         else launch_shape<FA, FB, float, float>(g);
+    } else if (c_dtype == DF_DTYPE_HALF) {
+        if (f16_bias) launch_shape<FA, FB, f16_t, f16_t>(g);
+        else launch_shape<FA, FB, f16_t, float>(g);
     } else {
         if (bf16_bias) launch_shape<FA, FB, uint16_t, uint16_t>(g);
         else launch_shape<FA, FB, uint16_t, float>(g);
@@ -1311,10 +1335,12 @@ static int nt_args(const char* fn, int fmt_a, const uint8_t* A, int lda, int fmt
     DF_CHECK(M >= 0 && N >= 0 && K >= 0, DF_ERR_INVALID, "%s: negative size M=%d N=%d K=%d", fn, M, N, K);
     DF_CHECK((fmt_a == E4M3 || fmt_a == E5M2) && (fmt_b == E4M3 || fmt_b == E5M2), DF_ERR_UNSUPPORTED,
              "%s: bad fp8 formats %d %d", fn, fmt_a, fmt_b);
-    DF_CHECK(c_dtype == DF_DTYPE_FLOAT32 || c_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
-             "%s: output dtype %d not supported", fn, c_dtype);
-    DF_CHECK(!bias || bias_dtype == DF_DTYPE_FLOAT32 || bias_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
-             "%s: bias dtype %d not supported", fn, bias_dtype);
+    DF_CHECK(c_dtype == DF_DTYPE_FLOAT32 || c_dtype == DF_DTYPE_BFLOAT16 || c_dtype == DF_DTYPE_HALF,
+             DF_ERR_UNSUPPORTED, "%s: output dtype %d not supported", fn, c_dtype);
+    DF_CHECK(!bias || bias_dtype == DF_DTYPE_FLOAT32 || bias_dtype == DF_DTYPE_BFLOAT16 || bias_dtype == DF_DTYPE_HALF,
+             DF_ERR_UNSUPPORTED, "%s: bias dtype %d not supported", fn, bias_dtype);
+    DF_CHECK(!bias || (bias_dtype == DF_DTYPE_HALF) == (c_dtype == DF_DTYPE_HALF) || bias_dtype == DF_DTYPE_FLOAT32,
+             DF_ERR_UNSUPPORTED, "%s: bias dtype %d with output dtype %d not supported", fn, bias_dtype, c_dtype);
     DF_CHECK(ldc >= N, DF_ERR_INVALID, "%s: ldc=%d < N=%d", fn, ldc, N);
     empty = M == 0 || N == 0;
     if (empty) return DF_OK;
@@ -1441,7 +1467,10 @@ extern "C" int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq,
     if (st != DF_OK) return st;
     const int cus = device_cu_count();
     GroupPlan gp{false, 1, 0};
-    if (!ex && !ew && M > 0 && N > 0 && cus > 0 && persistent_ok(dx) && persistent_ok(dw))
+    // grouped launches for fp32/bf16 outputs and for f16 dX with f16 dW;
+    // other pairs with f16 take the two separate launches
+    const bool h_dx = dx_dtype == DF_DTYPE_HALF, h_dw = dw_dtype == DF_DTYPE_HALF;
+    if (!ex && !ew && M > 0 && N > 0 && cus > 0 && persistent_ok(dx) && persistent_ok(dw) && h_dx == h_dw)
         gp = grouped_plan(dw, dx, dw.ws ? dw.ws_bytes : 0, cus);
     if (!gp.grouped) {
         st = df_fp8_gemm_bwd_dx(dYq, lddy, Wtq, ldwt, M, N, K, sdy_dev, sw_dev, dx_dtype, dX, lddx, ws, ws_bytes,
@@ -1451,7 +1480,8 @@ extern "C" int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq,
                                   stream);
     }
     const bool dw32 = dw_dtype == DF_DTYPE_FLOAT32, dx32 = dx_dtype == DF_DTYPE_FLOAT32;
-    if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus);
+    if (h_dx) launch_grouped<f16_t, f16_t>(dw, dx, gp, cus);
+    else if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus);
     else if (dw32) launch_grouped<float, uint16_t>(dw, dx, gp, cus);
     else if (dx32) launch_grouped<uint16_t, float>(dw, dx, gp, cus);
     else launch_grouped<uint16_t, uint16_t>(dw, dx, gp, cus);

@@ -109,6 +109,37 @@ __device__ __forceinline__ uint32_t absmax_bf16_block(const uint16_t* __restrict
     return block_max_u32(m);
 }
 
+// binary16: 16-byte loads hold 8 values, each widened exactly.
+__device__ __forceinline__ uint32_t fold_f16x2(uint32_t m, uint32_t w) {
+    m = fold_f32(m, __float_as_uint(f16_to_f32(w & 0xFFFFu)));
+    return fold_f32(m, __float_as_uint(f16_to_f32(w >> 16)));
+}
+__device__ __forceinline__ uint32_t absmax_f16_block(const uint16_t* __restrict__ x, int64_t n, int bi, int nb) {
+    uint32_t m = 0;
+    const int64_t nvec = n >> 3;
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    for (int64_t base = (int64_t)bi * kChunkVec; base < nvec; base += (int64_t)nb * kChunkVec) {
+        if (base + kChunkVec <= nvec) {
+            u32x4 v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                m = fold_f16x2(m, v[u].x); m = fold_f16x2(m, v[u].y);
+                m = fold_f16x2(m, v[u].z); m = fold_f16x2(m, v[u].w);
+            }
+        } else {
+            for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
+                const u32x4 v = xv[i];
+                m = fold_f16x2(m, v.x); m = fold_f16x2(m, v.y); m = fold_f16x2(m, v.z); m = fold_f16x2(m, v.w);
+            }
+        }
+    }
+    if (bi == 0 && threadIdx.x < (n & 7))
+        m = fold_f32(m, __float_as_uint(f16_to_f32(x[(nvec << 3) + threadIdx.x])));
+    return block_max_u32(m);
+}
+
 // Stage 1: one partial maximum per block.
 __global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __restrict__ x, int64_t n,
                                                                uint32_t* __restrict__ partial) {
@@ -119,6 +150,12 @@ __global__ __launch_bounds__(kThreads) void absmax_f32_stage1(const float* __res
 __global__ __launch_bounds__(kThreads) void absmax_bf16_stage1(const uint16_t* __restrict__ x, int64_t n,
                                                                 uint32_t* __restrict__ partial) {
     const uint32_t m = absmax_bf16_block(x, n, blockIdx.x, gridDim.x);
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void absmax_f16_stage1(const uint16_t* __restrict__ x, int64_t n,
+                                                               uint32_t* __restrict__ partial) {
+    const uint32_t m = absmax_f16_block(x, n, blockIdx.x, gridDim.x);
     if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
@@ -383,6 +420,21 @@ template <> struct Ld<uint16_t> {
     }
     static __device__ __forceinline__ float one(const uint16_t* p) { return bf16_to_f32(*p); }
 };
+template <> struct Ld<f16_t> {
+    static constexpr int E = 8;
+    static __device__ __forceinline__ void widen(const u32x4 t, float* v) {
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = f16_to_f32(w[i] & 0xFFFFu);
+            v[2 * i + 1] = f16_to_f32(w[i] >> 16);
+        }
+    }
+    static __device__ __forceinline__ void vec(const f16_t* p, float* v) {
+        widen(*reinterpret_cast<const u32x4*>(p), v);
+    }
+    static __device__ __forceinline__ float one(const f16_t* p) { return f16_to_f32(p->bits); }
+};
 
 // ---------------------------------------------------------------- LayerNorm --
 // Row statistics and the per-element map of the reference's
@@ -405,11 +457,15 @@ struct LnArgs {
 template <typename InT> __device__ __forceinline__ float round_to(float v);
 template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
 template <> __device__ __forceinline__ float round_to<uint16_t>(float v) { return bf16_to_f32(f32_to_bf16_rne(v)); }
+template <> __device__ __forceinline__ float round_to<f16_t>(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
 
 template <typename InT> __device__ __forceinline__ void store_one(InT* p, float v);
 template <> __device__ __forceinline__ void store_one<float>(float* p, float v) { *p = v; }
 template <> __device__ __forceinline__ void store_one<uint16_t>(uint16_t* p, float v) {
     *p = (uint16_t)f32_to_bf16_rne(v);
+}
+template <> __device__ __forceinline__ void store_one<f16_t>(f16_t* p, float v) {
+    p->bits = (uint16_t)f32_to_f16_rne(v);
 }
 // 16 bytes of values already rounded to the element type
 template <typename InT> __device__ __forceinline__ void store_vec(InT* p, const float* v);
@@ -422,6 +478,14 @@ template <> __device__ __forceinline__ void store_vec<uint16_t>(uint16_t* p, con
     w.y = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[3]) & 0xFFFF0000u);
     w.z = (__float_as_uint(v[4]) >> 16) | (__float_as_uint(v[5]) & 0xFFFF0000u);
     w.w = (__float_as_uint(v[6]) >> 16) | (__float_as_uint(v[7]) & 0xFFFF0000u);
+    *reinterpret_cast<u32x4*>(p) = w;
+}
+template <> __device__ __forceinline__ void store_vec<f16_t>(f16_t* p, const float* v) {
+    u32x4 w;
+    w.x = f32_to_f16_rne(v[0]) | (f32_to_f16_rne(v[1]) << 16);
+    w.y = f32_to_f16_rne(v[2]) | (f32_to_f16_rne(v[3]) << 16);
+    w.z = f32_to_f16_rne(v[4]) | (f32_to_f16_rne(v[5]) << 16);
+    w.w = f32_to_f16_rne(v[6]) | (f32_to_f16_rne(v[7]) << 16);
     *reinterpret_cast<u32x4*>(p) = w;
 }
 
@@ -1021,6 +1085,8 @@ static int absmax_impl(int in_dtype, const void* x, int64_t n, int fmt, float* a
         absmax_f32_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), n, part);
     else if (in_dtype == DF_DTYPE_BFLOAT16)
         absmax_bf16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
+    else if (in_dtype == DF_DTYPE_HALF)
+        absmax_f16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
     else
         DF_CHECK(false, DF_ERR_UNSUPPORTED, "absmax: dtype %d not supported", in_dtype);
     absmax_stage2<<<1, kThreads, 0, st>>>(part, blocks, fmt, absmax_dev, scale_dev);
@@ -1037,6 +1103,11 @@ extern "C" int df_absmax_bf16(const uint16_t* x, int64_t n, float* absmax_dev, v
     DF_CHECK(absmax_dev, DF_ERR_INVALID, "df_absmax_bf16: absmax_dev is NULL");
     return absmax_impl(DF_DTYPE_BFLOAT16, x, n, E4M3, absmax_dev, nullptr, ws, ws_bytes, stream);
 }
+extern "C" int df_absmax_f16(const uint16_t* x, int64_t n, float* absmax_dev, void* ws,
+                             size_t ws_bytes, void* stream) {
+    DF_CHECK(absmax_dev, DF_ERR_INVALID, "df_absmax_f16: absmax_dev is NULL");
+    return absmax_impl(DF_DTYPE_HALF, x, n, E4M3, absmax_dev, nullptr, ws, ws_bytes, stream);
+}
 extern "C" int df_absmax_scale_f32(const float* x, int64_t n, int fmt, float* absmax_dev,
                                    float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
     return absmax_impl(DF_DTYPE_FLOAT32, x, n, fmt, absmax_dev, scale_dev, ws, ws_bytes, stream);
@@ -1044,6 +1115,10 @@ extern "C" int df_absmax_scale_f32(const float* x, int64_t n, int fmt, float* ab
 extern "C" int df_absmax_scale_bf16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
                                     float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
     return absmax_impl(DF_DTYPE_BFLOAT16, x, n, fmt, absmax_dev, scale_dev, ws, ws_bytes, stream);
+}
+extern "C" int df_absmax_scale_f16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
+                                   float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
+    return absmax_impl(DF_DTYPE_HALF, x, n, fmt, absmax_dev, scale_dev, ws, ws_bytes, stream);
 }
 
 extern "C" int df_compute_scale(const float* absmax_dev, int fmt, float* scale_dev, void* stream) {
@@ -1168,8 +1243,8 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
     DF_CHECK(q || qt || colsum || empty, DF_ERR_INVALID, "%s: no output", name);
     DF_CHECK((scale_dev || (!q && !qt)) && (x || rows * (int64_t)cols == 0), DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad format %d", name, fmt);
-    DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED,
-             "%s: dtype %d not supported", name, in_dtype);
+    DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16 || in_dtype == DF_DTYPE_HALF,
+             DF_ERR_UNSUPPORTED, "%s: dtype %d not supported", name, in_dtype);
     if (q) {
         DF_CHECK(ldq >= cols && ldq % 16 == 0, DF_ERR_ALIGN, "%s: ldq=%d must be >= cols and a multiple of 16", name, ldq);
         DF_CHECK(aligned16(q), DF_ERR_ALIGN, "%s: q must be 16-byte aligned", name);
@@ -1224,12 +1299,18 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
         if (in_dtype == DF_DTYPE_FLOAT32)
             quantize_2d_kernel<float, E4M3, true, false><<<grid, kThreads, 0, st>>>(
                 static_cast<const float*>(x), rows, cols, ldx, vec_ok, nullptr, nullptr, 0, nullptr, 0, part);
+        else if (in_dtype == DF_DTYPE_HALF)
+            quantize_2d_kernel<f16_t, E4M3, true, false><<<grid, kThreads, 0, st>>>(
+                static_cast<const f16_t*>(x), rows, cols, ldx, vec_ok, nullptr, nullptr, 0, nullptr, 0, part);
         else
             quantize_2d_kernel<uint16_t, E4M3, true, false><<<grid, kThreads, 0, st>>>(
                 static_cast<const uint16_t*>(x), rows, cols, ldx, vec_ok, nullptr, nullptr, 0, nullptr, 0, part);
     } else if (in_dtype == DF_DTYPE_FLOAT32) {
         if (fmt == E4M3) { if (colsum) DF_Q2D(float, E4M3, true); else DF_Q2D(float, E4M3, false); }
         else { if (colsum) DF_Q2D(float, E5M2, true); else DF_Q2D(float, E5M2, false); }
+    } else if (in_dtype == DF_DTYPE_HALF) {
+        if (fmt == E4M3) { if (colsum) DF_Q2D(f16_t, E4M3, true); else DF_Q2D(f16_t, E4M3, false); }
+        else { if (colsum) DF_Q2D(f16_t, E5M2, true); else DF_Q2D(f16_t, E5M2, false); }
     } else {
         if (fmt == E4M3) { if (colsum) DF_Q2D(uint16_t, E4M3, true); else DF_Q2D(uint16_t, E4M3, false); }
         else { if (colsum) DF_Q2D(uint16_t, E5M2, true); else DF_Q2D(uint16_t, E5M2, false); }
@@ -1495,8 +1576,8 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     clear_error();
     DF_CHECK(rows >= 0 && cols >= 0 && (ldx >= cols || rows == 0), DF_ERR_INVALID,
              "%s: bad shape rows=%d cols=%d ldx=%d", name, rows, cols, ldx);
-    DF_CHECK(dtype == DF_DTYPE_FLOAT32 || dtype == DF_DTYPE_BFLOAT16, DF_ERR_UNSUPPORTED, "%s: dtype %d not supported",
-             name, dtype);
+    DF_CHECK(dtype == DF_DTYPE_FLOAT32 || dtype == DF_DTYPE_BFLOAT16 || dtype == DF_DTYPE_HALF, DF_ERR_UNSUPPORTED,
+             "%s: dtype %d not supported", name, dtype);
     DF_CHECK((gamma == nullptr) == (beta == nullptr), DF_ERR_INVALID, "%s: gamma and beta go together", name);
     DF_CHECK(eps >= 0.0f, DF_ERR_INVALID, "%s: eps < 0", name);
     const bool empty = rows == 0 || cols == 0;
@@ -1527,7 +1608,21 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     hipStream_t st = as_stream(stream);
     float2* stat = static_cast<float2*>(ws);
     uint32_t* parts = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + part_off);
-    const bool bf = dtype == DF_DTYPE_BFLOAT16;
+    const bool bf = dtype == DF_DTYPE_BFLOAT16, h16 = dtype == DF_DTYPE_HALF;
+    // STMT once per element type, with T the kernels' element type
+#define DF_BY_TYPE(STMT)            \
+    do {                            \
+        if (bf) {                   \
+            using T = uint16_t;     \
+            STMT;                   \
+        } else if (h16) {           \
+            using T = f16_t;        \
+            STMT;                   \
+        } else {                    \
+            using T = float;        \
+            STMT;                   \
+        }                           \
+    } while (0)
     if (empty) {
         // no values: absmax 0, scale 1 (stage 2 over no partials)
         if (mode == 1)
@@ -1537,7 +1632,7 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     }
     // statistics pass
     const int sblocks = (rows + 3) / 4;
-    const int esz = bf ? 2 : 4;
+    const int esz = (bf || h16) ? 2 : 4;
     const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
     const bool gb_vec = gamma && aligned16(gamma) && aligned16(beta);
 #define DF_LNS(T, A)                                                                                           \
@@ -1545,8 +1640,7 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
                                                         gb_vec, eps,                                            \
                                                         static_cast<const T*>(gamma), static_cast<const T*>(beta), \
                                                         stat, parts)
-    if (bf) { if (mode == 1) DF_LNS(uint16_t, true); else DF_LNS(uint16_t, false); }
-    else { if (mode == 1) DF_LNS(float, true); else DF_LNS(float, false); }
+    DF_BY_TYPE(if (mode == 1) DF_LNS(T, true); else DF_LNS(T, false));
 #undef DF_LNS
     if (mode == 1)
         absmax_stage2<<<1, kThreads, 0, st>>>(parts, sblocks, fmt, next_scale, const_cast<float*>(scale_dev));
@@ -1564,16 +1658,15 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     quantize_2d_kernel<T, F, false, CODES, AMAX, true><<<grid, kThreads, 0, st>>>(                             \
         static_cast<const T*>(x), rows, cols, ldx, vec_ok, scale_dev, q, ldq, qt, ldqt, nullptr, parts, la)
     if (mode == 0) {
-        if (bf) DF_LNT(uint16_t, E4M3, false, false); else DF_LNT(float, E4M3, false, false);
+        DF_BY_TYPE(DF_LNT(T, E4M3, false, false));
     } else if (mode == 1) {
-        if (bf) { if (fmt == E4M3) DF_LNT(uint16_t, E4M3, true, false); else DF_LNT(uint16_t, E5M2, true, false); }
-        else { if (fmt == E4M3) DF_LNT(float, E4M3, true, false); else DF_LNT(float, E5M2, true, false); }
+        DF_BY_TYPE(if (fmt == E4M3) DF_LNT(T, E4M3, true, false); else DF_LNT(T, E5M2, true, false));
     } else {
-        if (bf) { if (fmt == E4M3) DF_LNT(uint16_t, E4M3, true, true); else DF_LNT(uint16_t, E5M2, true, true); }
-        else { if (fmt == E4M3) DF_LNT(float, E4M3, true, true); else DF_LNT(float, E5M2, true, true); }
+        DF_BY_TYPE(if (fmt == E4M3) DF_LNT(T, E4M3, true, true); else DF_LNT(T, E5M2, true, true));
         amax_history_kernel<<<1, kThreads, 0, st>>>(parts, (int)(grid.x * grid.y), fmt, history, len, next_scale);
     }
 #undef DF_LNT
+#undef DF_BY_TYPE
     return launch_status(name);
 }
 

@@ -18,6 +18,20 @@ namespace dnn {
 namespace {
 inline int round16(int v) { return (v + 15) & ~15; }
 inline void* st() { return reinterpret_cast<void*>(Hip::stream()); }
+
+// absmax (and, with scale_dev, the scale for fmt) of n elements of TT
+template <typename TT>
+void absmax_of(const TT* x, int64_t n, int fmt, float* absmax_dev, float* scale_dev, void* ws, size_t wb) {
+    if constexpr (std::is_same_v<TT, float>) {
+        CHECK_DF_EX(df_absmax_scale_f32(x, n, fmt, absmax_dev, scale_dev, ws, wb, st()));
+    } else if constexpr (std::is_same_v<TT, __half>) {
+        CHECK_DF_EX(df_absmax_scale_f16(reinterpret_cast<const uint16_t*>(x), n, fmt, absmax_dev, scale_dev, ws, wb,
+                                        st()));
+    } else {
+        CHECK_DF_EX(df_absmax_scale_bf16(reinterpret_cast<const uint16_t*>(x), n, fmt, absmax_dev, scale_dev, ws, wb,
+                                         st()));
+    }
+}
 }  // namespace
 
 template <typename TT>
@@ -76,12 +90,7 @@ void FullyConnectedLayer<TT>::quantize_operand(const TT* x, int rows, int cols, 
     constexpr int dt = dtype_traits<TT>::value;
     const size_t ab = df_absmax_workspace_bytes();
     uint8_t* aws = absmax_ws_.get(ab);
-    const int64_t n = (int64_t)rows * cols;
-    if constexpr (std::is_same_v<TT, float>)
-        CHECK_DF_EX(df_absmax_scale_f32(x, n, fmt, nullptr, scale_dev, aws, ab, st()));
-    else
-        CHECK_DF_EX(df_absmax_scale_bf16(reinterpret_cast<const uint16_t*>(x), n, fmt, nullptr, scale_dev, aws, ab,
-                                         st()));
+    absmax_of(x, (int64_t)rows * cols, fmt, nullptr, scale_dev, aws, ab);
     if (colsum) {
         const size_t cb = df_quantize_2d_workspace_bytes(rows, cols);
         CHECK_DF_EX(df_quantize_2d_colsum(dt, x, rows, cols, cols, fmt, scale_dev, q, ldq, qt, ldqt, colsum,
@@ -127,11 +136,7 @@ const float* FullyConnectedLayer<TT>::quantize_delayed(Delayed& d, const TT* x, 
         // the first pass seeds the history with its own absmax
         const size_t ab = df_absmax_workspace_bytes();
         uint8_t* aws = absmax_ws_.get(ab);
-        const int64_t n = (int64_t)rows * cols;
-        if constexpr (std::is_same_v<TT, float>)
-            CHECK_DF_EX(df_absmax_f32(x, n, sc + 2, aws, ab, st()));
-        else
-            CHECK_DF_EX(df_absmax_bf16(reinterpret_cast<const uint16_t*>(x), n, sc + 2, aws, ab, st()));
+        absmax_of(x, (int64_t)rows * cols, fmt, sc + 2, nullptr, aws, ab);
         CHECK_DF_EX(df_amax_history_init(sc + 2, fmt, hist, history_len_, used, st()));
         d.seeded = true;
     }
@@ -337,6 +342,7 @@ void FullyConnectedLayer<TT>::load(std::istream& in) {
 }
 
 template class FullyConnectedLayer<float>;
+template class FullyConnectedLayer<__half>;
 template class FullyConnectedLayer<bfloat16>;
 
 }  // namespace dnn

@@ -108,6 +108,7 @@ void LayerNormLayer<T>::load(std::istream& in) {
 }
 
 template class LayerNormLayer<float>;
+template class LayerNormLayer<__half>;
 template class LayerNormLayer<bfloat16>;
 
 }  // namespace dnn

@@ -286,13 +286,15 @@ void tensor<TT>::load(std::istream& in) {
             if (fp8_dtype != dtype_traits<TT>::value)
                 throw std::runtime_error("tensor::load: the file holds the other fp8 format");
             *this = read_fp8_body<TT>(in, shape);
-        } else if constexpr (std::is_same_v<TT, float> || std::is_same_v<TT, bfloat16>) {
+        } else if constexpr (std::is_same_v<TT, float> || std::is_same_v<TT, bfloat16> ||
+                             std::is_same_v<TT, __half>) {
             if (fp8_dtype == DF_DTYPE_FP8E4M3)
                 *this = dequantize<TT>(read_fp8_body<fp8_e4m3>(in, shape));
             else
                 *this = dequantize<TT>(read_fp8_body<fp8_e5m2>(in, shape));
         } else {
-            throw std::runtime_error("tensor::load: an fp8 record loads into fp8, float or bfloat16 tensors only");
+            throw std::runtime_error(
+                "tensor::load: an fp8 record loads into fp8, float, __half or bfloat16 tensors only");
         }
         return;
     }
@@ -313,15 +315,25 @@ void tensor<TT>::load(std::istream& in) {
 template <typename Q, typename T>
 tensor<Q> quantize(const tensor<T>& x) {
     static_assert(dtype_traits<Q>::is_fp8, "quantize<Q>: Q must be fp8_e4m3 or fp8_e5m2");
-    static_assert(std::is_same_v<T, float> || std::is_same_v<T, bfloat16>, "quantize: float or bfloat16 input");
+    static_assert(std::is_same_v<T, float> || std::is_same_v<T, bfloat16> || std::is_same_v<T, __half>,
+                  "quantize: float, __half or bfloat16 input");
     constexpr int fmt = dtype_traits<Q>::fmt;
+    if constexpr (std::is_same_v<T, __half>) {
+        // binary16 widens to binary32 exactly: the codes and scale of the
+        // widened copy are those of the binary16 values
+        tensor<float> wide(x.shape());
+        CHECK_DF_EX(df_convert(DF_DTYPE_HALF, x.data(), DF_DTYPE_FLOAT32, wide.data(), x.size(), stream_arg()));
+        return quantize<Q>(wide);
+    }
     tensor<Q> q(x.shape());
     const int64_t n = x.size();
     const size_t ws_bytes = df_absmax_workspace_bytes();
     tensor<uint8_t> ws({(int)ws_bytes});
     void* st = stream_arg();
     uint8_t* codes = reinterpret_cast<uint8_t*>(q.data());
-    if constexpr (std::is_same_v<T, float>) {
+    if constexpr (std::is_same_v<T, __half>) {
+        // handled above
+    } else if constexpr (std::is_same_v<T, float>) {
         CHECK_DF_EX(df_absmax_scale_f32(x.data(), n, fmt, nullptr, q.scale_data(), ws.data(), ws_bytes, st));
         if (fmt == DF_FMT_E4M3) CHECK_DF_EX(df_quantize_f32_e4m3(x.data(), n, q.scale_data(), codes, st));
         else CHECK_DF_EX(df_quantize_f32_e5m2(x.data(), n, q.scale_data(), codes, st));
@@ -339,6 +351,14 @@ template <typename T, typename Q>
 tensor<T> dequantize(const tensor<Q>& q) {
     static_assert(dtype_traits<Q>::is_fp8, "dequantize<T, Q>: Q must be fp8_e4m3 or fp8_e5m2");
     constexpr int fmt = dtype_traits<Q>::fmt;
+    if constexpr (std::is_same_v<T, __half>) {
+        // code * scale in binary32, then rounded to nearest even binary16
+        const tensor<float> wide = dequantize<float>(q);
+        tensor<__half> out(q.shape());
+        CHECK_DF_EX(df_convert(DF_DTYPE_FLOAT32, wide.data(), DF_DTYPE_HALF, out.data(), q.size(), stream_arg()));
+        CHECK_HIP_EX(hipStreamSynchronize(Hip::stream()));  // wide is released on return
+        return out;
+    }
     tensor<T> out(q.shape());
     const int64_t n = q.size();
     const uint8_t* codes = reinterpret_cast<const uint8_t*>(q.data());
@@ -346,8 +366,8 @@ tensor<T> dequantize(const tensor<Q>& q) {
     if constexpr (std::is_same_v<T, float>) {
         if (fmt == DF_FMT_E4M3) CHECK_DF_EX(df_dequantize_e4m3_f32(codes, n, q.scale_data(), out.data(), st));
         else CHECK_DF_EX(df_dequantize_e5m2_f32(codes, n, q.scale_data(), out.data(), st));
-    } else {
-        static_assert(std::is_same_v<T, bfloat16>, "dequantize: float or bfloat16 output");
+    } else if constexpr (!std::is_same_v<T, __half>) {
+        static_assert(std::is_same_v<T, bfloat16>, "dequantize: float, __half or bfloat16 output");
         uint16_t* ob = reinterpret_cast<uint16_t*>(out.data());
         if (fmt == DF_FMT_E4M3) CHECK_DF_EX(df_dequantize_e4m3_bf16(codes, n, q.scale_data(), ob, st));
         else CHECK_DF_EX(df_dequantize_e5m2_bf16(codes, n, q.scale_data(), ob, st));
@@ -376,5 +396,9 @@ template tensor<float> dequantize<float, fp8_e4m3>(const tensor<fp8_e4m3>&);
 template tensor<float> dequantize<float, fp8_e5m2>(const tensor<fp8_e5m2>&);
 template tensor<bfloat16> dequantize<bfloat16, fp8_e4m3>(const tensor<fp8_e4m3>&);
 template tensor<bfloat16> dequantize<bfloat16, fp8_e5m2>(const tensor<fp8_e5m2>&);
+template tensor<fp8_e4m3> quantize<fp8_e4m3, __half>(const tensor<__half>&);
+template tensor<fp8_e5m2> quantize<fp8_e5m2, __half>(const tensor<__half>&);
+template tensor<__half> dequantize<__half, fp8_e4m3>(const tensor<fp8_e4m3>&);
+template tensor<__half> dequantize<__half, fp8_e5m2>(const tensor<fp8_e5m2>&);
 
 }  // namespace dnn

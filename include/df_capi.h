@@ -76,11 +76,16 @@ int df_absmax_f32(const float* x, int64_t n, float* absmax_dev,
                   void* ws, size_t ws_bytes, void* stream);
 int df_absmax_bf16(const uint16_t* x, int64_t n, float* absmax_dev,
                    void* ws, size_t ws_bytes, void* stream);
+/* x: binary16 bits (DF_DTYPE_HALF) */
+int df_absmax_f16(const uint16_t* x, int64_t n, float* absmax_dev,
+                  void* ws, size_t ws_bytes, void* stream);
 /* absmax and the scale for `fmt` in one call (scale_dev may equal NULL). */
 int df_absmax_scale_f32(const float* x, int64_t n, int fmt, float* absmax_dev,
                         float* scale_dev, void* ws, size_t ws_bytes, void* stream);
 int df_absmax_scale_bf16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
                          float* scale_dev, void* ws, size_t ws_bytes, void* stream);
+int df_absmax_scale_f16(const uint16_t* x, int64_t n, int fmt, float* absmax_dev,
+                        float* scale_dev, void* ws, size_t ws_bytes, void* stream);
 /* ---- bandwidth calibration (measurement only; no reference counterpart)
  * The flat absmax / quantize / dequantize kernels' exact access pattern
  * without their arithmetic, to measure the HBM ceiling each conversion can
@@ -122,7 +127,8 @@ int df_dequantize_e5m2_bf16(const uint8_t* q, int64_t n, const float* scale_dev,
 
 /* ---- 2-D quantize into GEMM operand layout (new) ----
  * x: row-major [rows, cols] with leading dimension ldx (elements), dtype
- * DF_DTYPE_FLOAT32 or DF_DTYPE_BFLOAT16.  Writes, when non-NULL:
+ * DF_DTYPE_FLOAT32, DF_DTYPE_HALF or DF_DTYPE_BFLOAT16 (both 2-byte types
+ * widen to binary32 exactly before the code is taken).  Writes, when non-NULL:
  *   q  [rows, ldq]  : q[r*ldq + c] = code(x[r,c]); columns [cols, ldq) = 0
  *   qt [cols, ldqt] : qt[c*ldqt + r] = code(x[r,c]); columns [rows, ldqt) = 0
  * ldq and ldqt must be multiples of 16 (the GEMM's K granule).  qt is the
@@ -226,7 +232,7 @@ int df_quantize_2d_delayed_noalloc(int in_dtype, const void* x, int rows, int co
 /* ---- LayerNorm with the quantize of its output fused in (producer side of
  * the qkv / fc1 Linears; layer_norm_forward_kernel,
  * dnn/layers/layer_norm_layer.cu:26-63) ----
- * Per row of x [rows, cols] (ldx elements apart), dtype fp32 or bf16:
+ * Per row of x [rows, cols] (ldx elements apart), dtype fp32, f16 or bf16:
  *   mean = sum(x)/cols, var = sum((x - mean)^2)/cols, rstd = 1/sqrt(var + eps)
  *   y = (x - mean) * rstd, then y = fma(y, gamma, beta) when gamma/beta
  *   (both [cols], same dtype) are given; y is rounded to the dtype (RNE).
@@ -265,8 +271,10 @@ int df_layernorm_quantize_delayed(int dtype, const void* x, int rows, int cols, 
  *   A [M, lda] fp8 (fmt_a), B [N, ldb] fp8 (fmt_b), both row-major with the
  *   reduction dimension contiguous; lda, ldb multiples of 16 and >= K;
  *   A, B 16-byte aligned; sa, sb device scalars; bias NULL or [N] of
- *   bias_dtype (FLOAT32 or BFLOAT16); C [M, ldc] of c_dtype (FLOAT32 or
- *   BFLOAT16), overwritten.  fp32 accumulation on CDNA4 fp8 MFMA.
+ *   bias_dtype; C [M, ldc] of c_dtype, overwritten: an FLOAT32 or BFLOAT16
+ *   C with an FLOAT32 or BFLOAT16 bias, or a HALF C (the FP16 layer's) with
+ *   an FLOAT32 or HALF bias; a 2-byte C is rounded to nearest even.  fp32
+ *   accumulation on CDNA4 fp8 MFMA.
  *   When K is not a multiple of 16, columns [K, roundup(K,16)) of A and B
  *   must hold zero codes (df_quantize_2d writes its padding that way).
  *   ws / ws_bytes: optional device workspace (16-byte aligned) for split-K
@@ -333,8 +341,8 @@ int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ld
  * df_fp8_gemm_bwd_dw whenever both split its K range alike (they may pick
  * different slice counts, which changes dW's fp32 rounding, within the
  * 1e-4 bar either way).  Falls back to the two calls where the grouped
- * launch does not apply (degenerate sizes, operands beyond 2^31 bytes) or
- * would not be faster.  ws: df_fp8_gemm_bwd_workspace_bytes(M, N, K) never
+ * launch does not apply (degenerate sizes, operands beyond 2^31 bytes, a
+ * HALF output paired with a non-HALF one) or would not be faster.  ws: df_fp8_gemm_bwd_workspace_bytes(M, N, K) never
  * limits the plan; smaller only narrows it.  Together these replace
  * fc_backward_input and fc_backward_weights (fully_connected_layer.cu:43-89)
  * as FullyConnectedLayer::backward launches them (:310-338). */

@@ -93,6 +93,27 @@ void upload_bf16(tensor<bfloat16>& t, const std::vector<float>& v) {
     t.upload(reinterpret_cast<const bfloat16*>(h.data()));
 }
 
+// binary16 through the oracle's conversions (dfo_f32_to_f16: nearest even)
+std::vector<float> round_f16(const std::vector<float>& f) {
+    std::vector<float> r(f.size());
+    for (size_t i = 0; i < f.size(); ++i) r[i] = dfo_f16_to_f32(dfo_f32_to_f16(f[i]));
+    return r;
+}
+
+std::vector<float> download_f(const tensor<__half>& t) {
+    std::vector<uint16_t> h(t.size());
+    t.download(reinterpret_cast<__half*>(h.data()));
+    std::vector<float> f(h.size());
+    for (size_t i = 0; i < h.size(); ++i) f[i] = dfo_f16_to_f32(h[i]);
+    return f;
+}
+
+void upload_f16(tensor<__half>& t, const std::vector<float>& v) {
+    std::vector<uint16_t> h(v.size());
+    for (size_t i = 0; i < v.size(); ++i) h[i] = dfo_f32_to_f16(v[i]);
+    t.upload(reinterpret_cast<const __half*>(h.data()));
+}
+
 class HipFixture : public mini_test::Test {
 protected:
     std::unique_ptr<Hip> hip_;
@@ -735,6 +756,57 @@ TEST_F(FullyConnectedLayerTest, BFloat16LayerMatchesOracle) {
     EXPECT_LE(rel_err(db, edb), tol);
 }
 
+// the FP16 layer (fully_connected_layer.cu:405): operands quantized from
+// binary16, outputs the fp32 products rounded to nearest even binary16
+TEST_F(FullyConnectedLayerTest, HalfLayerMatchesOracle) {
+    const int N = 64, in_f = 96, out_f = 80;
+    FullyConnectedLayer<__half> layer(in_f, out_f, true);
+    const auto w = round_f16(uniform((size_t)out_f * in_f, -0.3f, 0.3f, 51));
+    const auto b = round_f16(uniform(out_f, -1.0f, 1.0f, 52));
+    const auto x = round_f16(uniform((size_t)N * in_f, -3.0f, 3.0f, 53));
+    const auto dy = round_f16(uniform((size_t)N * out_f, -0.5f, 0.5f, 54));
+    upload_f16(*layer.weights(), w);
+    upload_f16(*layer.bias(), b);
+    tensor<__half> input({N, in_f}), grad_out({N, out_f});
+    upload_f16(input, x);
+    upload_f16(grad_out, dy);
+    const auto y = download_f(layer.forward(input));
+    const auto dx = download_f(layer.backward(grad_out));
+    const auto dw = download_f(*layer.grad_weights());
+    const auto db = download_f(*layer.grad_bias());
+
+    const auto xd = fp8_values(x, DFO_E4M3), wd = fp8_values(w, DFO_E4M3), dyd = fp8_values(dy, DFO_E5M2);
+    std::vector<float> ey((size_t)N * out_f), edx((size_t)N * in_f), edw(w.size()), edb(out_f);
+    dfo_fc_forward(xd.data(), wd.data(), b.data(), ey.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_input(dyd.data(), wd.data(), edx.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_weights(dyd.data(), xd.data(), edw.data(), N, in_f, out_f, 4);
+    dfo_fc_backward_bias(dy.data(), edb.data(), N, out_f);
+    // f16 outputs against the oracle's rounded to f16: the 1e-4 bar plus the
+    // binary16 unit roundoff 2^-11 where the fp32 sums straddle a tie
+    const double tol = 1e-4 + 1.0 / 2048;
+    EXPECT_LE(rel_err(y, round_f16(ey)), tol);
+    EXPECT_LE(rel_err(dx, round_f16(edx)), tol);
+    EXPECT_LE(rel_err(dw, round_f16(edw)), tol);
+    EXPECT_LE(rel_err(db, round_f16(edb)), tol);
+}
+
+// save_fp8 of an FP16 layer: e4m3 codes of the binary16 weights; load()
+// gives the dequantized values rounded to binary16, the bias unchanged
+TEST_F(FullyConnectedLayerTest, HalfSaveFp8RoundTrip) {
+    const int in_f = 40, out_f = 24;
+    FullyConnectedLayer<__half> a(in_f, out_f, false);
+    const auto w = round_f16(uniform((size_t)out_f * in_f, -0.5f, 0.5f, 55));
+    const auto b = round_f16(uniform(out_f, -1.0f, 1.0f, 56));
+    upload_f16(*a.weights(), w);
+    upload_f16(*a.bias(), b);
+    std::stringstream ss;
+    a.save_fp8(ss);
+    FullyConnectedLayer<__half> c(in_f, out_f, false);
+    c.load(ss);
+    EXPECT_TRUE(download_f(*c.weights()) == round_f16(fp8_values(w, DFO_E4M3)));
+    EXPECT_TRUE(download_f(*c.bias()) == b);
+}
+
 // all launches follow Hip::stream(): results on a created stream equal
 // those on the legacy stream, bit for bit
 TEST_F(FullyConnectedLayerTest, RunsOnTheCurrentStream) {
@@ -950,6 +1022,18 @@ TEST_F(LayerNormLayerTest, BFloat16MatchesOracle) {
     std::vector<float> e(x.size());
     dfo_layernorm(x.data(), rows, C, nullptr, nullptr, 1e-5f, 1, e.data());
     EXPECT_LE(rel_err(y, e), 1e-2);  // one bf16 step where the binary32 sums differ in order
+}
+
+TEST_F(LayerNormLayerTest, HalfMatchesOracle) {
+    const int rows = 20, C = 96;
+    LayerNormLayer<__half> ln(C);
+    const auto x = round_f16(uniform((size_t)rows * C, -2.0f, 2.0f, 108));
+    tensor<__half> t({rows, C});
+    upload_f16(t, x);
+    const auto y = download_f(ln.forward(t));
+    std::vector<float> e(x.size());
+    dfo_layernorm(x.data(), rows, C, nullptr, nullptr, 1e-5f, 0, e.data());
+    EXPECT_LE(rel_err(y, round_f16(e)), 2e-3);  // one binary16 step where the sums differ in order
 }
 
 // fc.forward(x, ln) == fc.forward(ln.forward(x)), forward and backward, just

@@ -54,7 +54,7 @@ def test_argument_errors():
     assert status("df_compute_scale", FAKE, 3, FAKE, None) == -2
     # 2-D quantize: ld rules
     assert status("df_quantize_2d", int(DType.FLOAT32), FAKE, 4, 20, 20, 0, FAKE, FAKE, 20, None, 0, None) == -4
-    assert status("df_quantize_2d", int(DType.HALF), FAKE, 4, 4, 4, 0, FAKE, FAKE, 16, None, 0, None) == -2
+    assert status("df_quantize_2d", int(DType.INT8), FAKE, 4, 4, 4, 0, FAKE, FAKE, 16, None, 0, None) == -2
     assert status("df_quantize_2d", int(DType.FLOAT32), FAKE, 4, 4, 3, 0, FAKE, FAKE, 16, None, 0, None) == -1
     assert status("df_quantize_2d_colsum", int(DType.FLOAT32), FAKE, 4, 4, 4, 0, FAKE, None, 0, None, 0,
                   FAKE, None, 0, None) == -5
@@ -64,7 +64,11 @@ def test_argument_errors():
     assert g(0, FAKE, 24, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -4  # ld % 16
     assert g(0, FAKE + 8, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -4
     assert g(0, FAKE, 16, 3, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -2
-    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, int(DType.HALF), FAKE, 4, None, 0, None) == -2
+    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, int(DType.INT8), FAKE, 4, None, 0, None) == -2
+    # an f16 bias goes with an f16 output only; a bf16 bias not with an f16 output
+    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, int(DType.HALF), FAKE, 0, FAKE, 4, None, 0, None) == -2
+    assert g(0, FAKE, 16, 0, FAKE, 16, 4, 4, 16, FAKE, FAKE, int(DType.BFLOAT16), FAKE, int(DType.HALF), FAKE, 4,
+             None, 0, None) == -2
     assert g(0, FAKE, 16, 0, FAKE, 16, 4, 5, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1  # ldc < N
     assert g(0, FAKE, 16, 0, FAKE, 16, -1, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1
     assert g(0, FAKE, 16, 0, FAKE, 16, 0, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == 0  # M = 0
@@ -122,7 +126,7 @@ def test_grouped_backward_and_batch_argument_errors():
     bad[5] = 24  # ldyt not a multiple of 16
     assert status("df_fp8_gemm_bwd", *bad) == -4 and "(dW)" in err()
     bad = list(args)
-    bad[17] = int(DType.HALF)  # dW dtype
+    bad[17] = int(DType.INT8)  # dW dtype
     assert status("df_fp8_gemm_bwd", *bad) == -2
     g, sl = ctypes.c_int(7), ctypes.c_int(7)
     assert status("df_fp8_gemm_bwd_plan", 0, 10, 10, 0, ctypes.byref(g), ctypes.byref(sl)) == 0

@@ -5,7 +5,8 @@ Bars:
   - y against the oracle's restatement of layer_norm_forward_kernel
     (dnn/layers/layer_norm_layer.cu:26-63): within 1e-5 of the row's unit
     scale for fp32 (different summation order), within one bf16 step for
-    bf16;
+    bf16, within one binary16 step for f16 (LayerNormLayer<__half>,
+    layer_norm_layer.cu:123; the oracle's fp32 y rounded by dfo_convert);
   - the fused codes bit-identical to df_quantize_2d applied to the y that
     df_layernorm writes, at a scale bit-identical to the oracle's D1/D2
     scale of absmax(y): the fusion changes no value;
@@ -27,7 +28,16 @@ SHAPES = [(1, 8), (3, 7), (37, 100), (129, 257), (256, 1600), (1000, 768)]
 def dev_tensor(x, kind, dev):
     if kind == "f32":
         return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
+    if kind == "f16":
+        return torch.from_numpy(orc.convert(x, 0, 1).view(np.int16)).to(dev).view(torch.float16)
     return torch.from_numpy(synth.f32_to_bf16_bits(x).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def oracle_y(xh, gh, bh, kind):
+    ref = orc.layernorm(xh, gh, bh, eps=1e-5, round_bf16=(kind == "bf16"))
+    if kind == "f16":  # the fp32 result rounded to nearest even binary16
+        ref = orc.convert(orc.convert(ref, 0, 1), 1, 0).reshape(ref.shape)
+    return ref
 
 
 def host_f32(t):
@@ -46,21 +56,22 @@ def case(rows, cols, kind, affine, dev, seed):
     return xd, gd, bd, xh, gh, bh
 
 
-@pytest.mark.parametrize("kind", ["f32", "bf16"])
+@pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("affine", [False, True])
 def test_layernorm_matches_oracle(dev, kind, affine):
     for i, (rows, cols) in enumerate(SHAPES):
         xd, gd, bd, xh, gh, bh = case(rows, cols, kind, affine, dev, 500 + i)
         y = host_f32(df.layernorm(xd, gd, bd, eps=1e-5))
-        ref = orc.layernorm(xh, gh, bh, eps=1e-5, round_bf16=(kind == "bf16"))
+        ref = oracle_y(xh, gh, bh, kind)
         unit = 1.0 if not affine else np.abs(gh).max() + 1.0
         if kind == "f32":
             assert np.abs(y - ref).max() <= 1e-5 * unit, f"{rows}x{cols}"  # ~10 ulp of max|y|
-        else:  # at most one bf16 step apart (2^-7 relative, plus rounding near 0)
-            assert (np.abs(y - ref) <= np.abs(ref) * 2 ** -7 + 1e-6 * unit).all(), f"{rows}x{cols}"
+        else:  # at most one step of the 2-byte type apart (plus rounding near 0)
+            step = 2 ** -7 if kind == "bf16" else 2 ** -10
+            assert (np.abs(y - ref) <= np.abs(ref) * step + 1e-6 * unit).all(), f"{rows}x{cols}"
 
 
-@pytest.mark.parametrize("kind", ["f32", "bf16"])
+@pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("fmt", [Fmt.E4M3, Fmt.E5M2])
 def test_fused_quantize_equals_layernorm_then_quantize(dev, kind, fmt):
     for i, (rows, cols) in enumerate(SHAPES):
@@ -68,8 +79,8 @@ def test_fused_quantize_equals_layernorm_then_quantize(dev, kind, fmt):
         y0 = df.layernorm(xd, gd, bd)
         y, q, qt, s = df.layernorm(xd, gd, bd, fmt=fmt, want_y=True, want_q=True, want_qt=True)
         torch.cuda.synchronize()
-        assert torch.equal(y.view(torch.int16) if kind == "bf16" else y,
-                           y0.view(torch.int16) if kind == "bf16" else y0), f"{rows}x{cols}: y"
+        assert torch.equal(y.view(torch.int16) if kind != "f32" else y,
+                           y0.view(torch.int16) if kind != "f32" else y0), f"{rows}x{cols}: y"
         yh = host_f32(y0)
         s_exp = np.float32(orc.scale(orc.absmax(np.ascontiguousarray(yh)), int(fmt)))
         assert s.item() == s_exp, f"{rows}x{cols}: scale"
@@ -134,6 +145,6 @@ def test_argument_errors(dev):
         df.call("df_layernorm", 0, x.data_ptr(), 4, 8, 8, None, None, 1e-5, x.data_ptr(), 8, x.data_ptr(), 0, None)
     assert ei.value.status == -5
     with pytest.raises(df.DFError) as ei:
-        df.call("df_layernorm", 1, x.data_ptr(), 4, 8, 8, None, None, 1e-5, x.data_ptr(), 8, x.data_ptr(), 4096,
-                None)
+        df.call("df_layernorm", 2, x.data_ptr(), 4, 8, 8, None, None, 1e-5, x.data_ptr(), 8, x.data_ptr(), 4096,
+                None)  # int8
     assert ei.value.status == -2
