@@ -81,6 +81,8 @@ def parse():
                    help="first run one plain 1 GiB device copy (HBM counter calibration under rocprofv3 --pmc)")
     p.add_argument("--conversion-only", action="store_true",
                    help="run only the config-2 conversion leg and print its JSON (profiling runs)")
+    p.add_argument("--config3-only", action="store_true",
+                   help="run only the config-3 leg and print its JSON (profiling runs)")
     p.add_argument("--summarize-profiles", action="store_true",
                    help="no GPU work: turn the rocprofv3 output of PROFILE_COMMANDS into the summaries under "
                         "profiles/")
@@ -155,6 +157,9 @@ def main():
 
     if args.conversion_only:
         print(json.dumps({"conversion": conversion_bench(torch, df, synth, dev, cur())}))
+        return
+    if args.config3_only:
+        print(json.dumps({"config3": config3_bench(torch, df, synth, dev, cur())}))
         return
 
     def to_bf16(a):
@@ -467,6 +472,8 @@ PROFILE_COMMANDS = {
     "stats_producer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_producer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-optimizer --no-delayed --no-config3"),
+    "stats_config3": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_config3 -o bench "
+                      "-- python3 bench.py --config3-only"),
 }
 # extra kernel-stat summaries: (command key, csv directory, output file, title,
 # substrings that select the leg's own kernels)
@@ -611,6 +618,8 @@ def summarize_profiles():
         extra.append(fname)
     if streaming_summary(out_dir, prof):
         extra.append("streaming_h2d_copies_config5.md")
+    if config3_summary(out_dir, prof):
+        extra.append("gemm_config3_kernels.md")
     print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)}, extra {extra})")
 
 
@@ -674,6 +683,53 @@ def conversion_summary(out_dir, prof):
         else:
             lines.append(f"| `{_short_kernel(name)}` | {r['Calls']} | {avg_us:.1f} | - | - | - |")
     with open(os.path.join(prof, "conversion_config2_kernels.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return True
+
+
+def config3_summary(out_dir, prof):
+    """profiles/gemm_config3_kernels.md from the config-3 run: config3_bench
+    launches each Linear's GEMM 1 + reps times back to back (qkv, attn_proj,
+    fc, proj), so the GEMM dispatches in start order split into those runs;
+    per Linear the median duration of its timed launches (a split-K GEMM adds
+    its reduce kernel) against the bench's attainable bound."""
+    import csv
+
+    path = os.path.join(out_dir, "prof_config3", "bench_kernel_trace.csv")
+    if not os.path.exists(path):
+        return False
+    with open(path) as fh:
+        tr = sorted(csv.DictReader(fh), key=lambda r: int(r["Start_Timestamp"]))
+    reps = 20
+    gem = [r for r in tr if "gemm_nt_persistent_kernel" in r["Kernel_Name"] or "gemm_nt_dma128" in r["Kernel_Name"]
+           or "gemm_nt_kernel" in r["Kernel_Name"]]
+    if len(gem) < 4 * (reps + 1):
+        return False
+    red = [r for r in tr if "splitk_reduce_kernel" in r["Kernel_Name"]]
+    med = lambda v: sorted(v)[len(v) // 2]
+    M = 8192
+    lines = ["# rocprofv3: config-3 GEMMs (GPT-2 small Linears, M = 8192, forward, bf16 out + bf16 bias)", "",
+             "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["stats_config3"], "",
+             f"Each Linear's GEMM runs 1 + {reps} times back to back; the table takes the median of its {reps} timed "
+             "dispatches (kernel start to end; a split-K launch adds its reduce kernel).  Attainable bound: "
+             "min(5.0 PFLOP/s, AI x 8 TB/s), AI = 2MNK / (MK + NK + 2MN) (fp8 operands read once, bf16 output "
+             "written once).", "",
+             "| Linear | M x N x K | kernel | grid | us | TFLOP/s | attainable TFLOP/s | fraction |",
+             "|---|---|---|---|---|---|---|---|"]
+    for i, (name, K, N) in enumerate(SMALL_LINEARS):
+        run = gem[i * (reps + 1) + 1:(i + 1) * (reps + 1)]
+        t0, t1 = int(run[0]["Start_Timestamp"]), int(run[-1]["End_Timestamp"])
+        rd = [r for r in red if t0 <= int(r["Start_Timestamp"]) <= t1]
+        dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in run]
+        t = med(dur) + (med([int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rd]) if rd else 0)
+        flops = 2.0 * M * N * K
+        bound = min(5.0e15, flops / (M * K + N * K + 2 * M * N) * 8.0e12)
+        grid = int(run[0].get("Grid_Size", run[0].get("Grid_Size_X", 0))) // max(
+            1, int(run[0].get("Workgroup_Size", run[0].get("Workgroup_Size_X", 1))))
+        lines.append(f"| {name} | {M} x {N} x {K} | `{_short_kernel(run[0]['Kernel_Name'])}`"
+                     f"{' + reduce' if rd else ''} | {grid} | {t / 1e3:.1f} | {flops / (t * 1e-9) / 1e12:.0f} | "
+                     f"{bound / 1e12:.0f} | {flops / (t * 1e-9) / bound:.3f} |")
+    with open(os.path.join(prof, "gemm_config3_kernels.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
     return True
 
@@ -752,7 +808,10 @@ def streaming_summary(out_dir, prof):
     copy size taken from the same run's bench line."""
     import csv
     path = os.path.join(out_dir, "prof_streaming", "bench_memory_copy_trace.csv")
-    log = os.path.join(out_dir, "prof_streaming.log")
+    # the run's stdout (its bench line), saved as gpurun_out/prof_stats_streaming.log
+    log = os.path.join(out_dir, "prof_stats_streaming.log")
+    if not os.path.exists(log):
+        log = os.path.join(out_dir, "prof_streaming.log")
     if not (os.path.exists(path) and os.path.exists(log)):
         return False
     line = [l for l in open(log) if l.startswith('{"metric"')]
