@@ -232,8 +232,10 @@ def absmax_scale(x, fmt: Fmt):
 def quantize(x, scale, fmt: Fmt):
     """Flat quantize of a contiguous fp32/bf16 tensor -> uint8 codes (same shape)."""
     torch = _torch()
+    src = {DType.FLOAT32: "f32", DType.BFLOAT16: "bf16"}.get(_in_dtype(x))
+    if src is None:  # the flat kernels take fp32 and bf16; df_quantize_2d also binary16
+        raise TypeError(f"quantize: {x.dtype} has no flat kernel (use quantize_2d)")
     q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
-    src = "f32" if _in_dtype(x) == DType.FLOAT32 else "bf16"
     fn = f"df_quantize_{src}_{'e4m3' if fmt == Fmt.E4M3 else 'e5m2'}"
     call(fn, _ptr(x), x.numel(), _ptr(scale), _ptr(q), _stream())
     return q
@@ -241,6 +243,8 @@ def quantize(x, scale, fmt: Fmt):
 
 def dequantize(q, scale, fmt: Fmt, out_dtype):
     torch = _torch()
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"dequantize: output {out_dtype} not supported (fp32 or bf16)")
     out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
     dst = "f32" if out_dtype == torch.float32 else "bf16"
     fn = f"df_dequantize_{'e4m3' if fmt == Fmt.E4M3 else 'e5m2'}_{dst}"

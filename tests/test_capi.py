@@ -156,3 +156,14 @@ def test_grouped_backward_and_batch_argument_errors():
     one_n = (ctypes.c_int64 * 1)(64)
     assert status("df_adam_update_absmax_f32", one_f, one_f, one_f, one_f, one_n, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0,
                   1, None, 0.0, None, None) == -1
+
+
+def test_flat_wrappers_refuse_binary16():
+    """The flat quantize/dequantize kernels take fp32 and bf16 only; a float16
+    tensor is refused on the host rather than sent to the bf16 kernel."""
+    import torch
+    from deepfuse_amd import Fmt
+    with pytest.raises(TypeError):
+        df.quantize(torch.zeros(8, dtype=torch.float16), None, Fmt.E4M3)
+    with pytest.raises(TypeError):
+        df.dequantize(torch.zeros(8, dtype=torch.uint8), None, Fmt.E4M3, torch.float16)
