@@ -144,6 +144,62 @@ __device__ __forceinline__ uint32_t quant4_t(float a, float b, float c, float d,
            (encode2_hw<FMT>(qdiv_t<FAST>(c, q), qdiv_t<FAST>(d, q)) << 16);
 }
 
+// The same codes for inputs known not to be NaN, fast division form only
+// (kernels test a group of values with one wave-wide ballot and take
+// quant4_t when any lane holds a NaN).  About half the instructions:
+//  - |x| above 2^60 (inf included) is clamped to 2^60 before the division
+//    instead of selected around it: the quotient is then above 2^20, beyond
+//    both formats' maximum, and saturates to the same code;
+//  - the clamp to +-max is one v_med3 (no NaN to canonicalise first), and
+//    no NaN patch follows the conversion;
+//  - the second pair of codes is converted into the high half of the first
+//    pair's register (word select) instead of being masked and shifted.
+// med3 returns one of its operands, so -0 stays -0 through both clamps.
+template <int FMT>
+__device__ __forceinline__ float qdiv_clamp_nonan(float x, const QDiv& d) {
+    const float xc = __builtin_amdgcn_fmed3f(x, -0x1p60f, 0x1p60f);
+    const float y0 = xc * d.r;
+    const float e0 = __builtin_fmaf(-d.s, y0, xc);
+    const float y1 = __builtin_fmaf(e0, d.r, y0);
+    const float e1 = __builtin_fmaf(-d.s, y1, xc);
+    const float q = __builtin_copysignf(__builtin_fmaf(e1, d.r, y1), x);
+    constexpr float fm = Fp8<FMT>::fmax;
+    return __builtin_amdgcn_fmed3f(q, -fm, fm);
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t quant4_nonan(float a, float b, float c, float d, const QDiv& q) {
+    const float qa = qdiv_clamp_nonan<FMT>(a, q), qb = qdiv_clamp_nonan<FMT>(b, q);
+    const float qc = qdiv_clamp_nonan<FMT>(c, q), qd = qdiv_clamp_nonan<FMT>(d, q);
+    if (FMT == E4M3)
+        return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(qc, qd, __builtin_amdgcn_cvt_pk_fp8_f32(qa, qb, 0, false),
+                                                         true);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(qc, qd, __builtin_amdgcn_cvt_pk_bf8_f32(qa, qb, 0, false),
+                                                     true);
+}
+
+// True when any lane of the wave holds a NaN among v[0..N-1] (uniform).
+template <int N>
+__device__ __forceinline__ bool wave_any_nan(const float* v) {
+    uint64_t m = 0;
+#pragma unroll
+    for (int e = 0; e < N; ++e) m |= __builtin_amdgcn_ballot_w64(v[e] != v[e]);
+    return m != 0;
+}
+
+// Four packed codes per row for rows a..d -> the four columns (byte i of
+// column j = byte j of row i): a 4x4 byte transpose in eight v_perm_b32.
+__device__ __forceinline__ void transpose4x4_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t* col) {
+    const uint32_t ab01 = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+    const uint32_t cd01 = __builtin_amdgcn_perm(d, c, 0x05010400u);  // c0 d0 c1 d1
+    const uint32_t ab23 = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+    const uint32_t cd23 = __builtin_amdgcn_perm(d, c, 0x07030602u);  // c2 d2 c3 d3
+    col[0] = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u);          // a0 b0 c0 d0
+    col[1] = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u);          // a1 b1 c1 d1
+    col[2] = __builtin_amdgcn_perm(cd23, ab23, 0x05040100u);
+    col[3] = __builtin_amdgcn_perm(cd23, ab23, 0x07060302u);
+}
+
 // ----------------------------------------------------------------- decode --
 // fp8 code (low byte) -> binary32, exact.  The magnitude bits shifted into
 // the binary32 exponent/significand position are the value times

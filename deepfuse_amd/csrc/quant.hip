@@ -215,10 +215,18 @@ __device__ __forceinline__ void quantize_f32_body(const float* __restrict__ x, i
             f32x4 v[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+            const float* t = reinterpret_cast<const float*>(v);
+            if (FAST && !wave_any_nan<4 * kU>(t)) {
 #pragma unroll
-            for (int u = 0; u < kU; ++u)
-                __builtin_nontemporal_store(quant4_t<FMT, FAST>(v[u].x, v[u].y, v[u].z, v[u].w, d),
-                                            qv + base + u * kThreads + threadIdx.x);
+                for (int u = 0; u < kU; ++u)
+                    __builtin_nontemporal_store(quant4_nonan<FMT>(v[u].x, v[u].y, v[u].z, v[u].w, d),
+                                                qv + base + u * kThreads + threadIdx.x);
+            } else {
+#pragma unroll
+                for (int u = 0; u < kU; ++u)
+                    __builtin_nontemporal_store(quant4_t<FMT, FAST>(v[u].x, v[u].y, v[u].z, v[u].w, d),
+                                                qv + base + u * kThreads + threadIdx.x);
+            }
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
                 const f32x4 v = xv[i];
@@ -251,6 +259,23 @@ __device__ __forceinline__ uint32_t quant_bf16x4(uint32_t w0, uint32_t w1, const
                                bf16_to_f32(w1 >> 16), d);
 }
 
+// eight bf16 values of one 16-byte load -> eight codes
+template <int FMT, bool FAST>
+__device__ __forceinline__ u32x2 quant_bf16x8(const u32x4 w, const QDiv& d) {
+    const float t[8] = {bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu),
+                        bf16_to_f32(w.y >> 16),     bf16_to_f32(w.z & 0xFFFFu), bf16_to_f32(w.z >> 16),
+                        bf16_to_f32(w.w & 0xFFFFu), bf16_to_f32(w.w >> 16)};
+    u32x2 o;
+    if (FAST && !wave_any_nan<8>(t)) {
+        o.x = quant4_nonan<FMT>(t[0], t[1], t[2], t[3], d);
+        o.y = quant4_nonan<FMT>(t[4], t[5], t[6], t[7], d);
+    } else {
+        o.x = quant4_t<FMT, FAST>(t[0], t[1], t[2], t[3], d);
+        o.y = quant4_t<FMT, FAST>(t[4], t[5], t[6], t[7], d);
+    }
+    return o;
+}
+
 template <int FMT, bool FAST>
 __device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ x, int64_t n, const QDiv& d,
                                                    uint8_t* __restrict__ q) {
@@ -263,12 +288,8 @@ __device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ 
 #pragma unroll
             for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                u32x2 o;
-                o.x = quant_bf16x4<FMT, FAST>(v[u].x, v[u].y, d);
-                o.y = quant_bf16x4<FMT, FAST>(v[u].z, v[u].w, d);
-                __builtin_nontemporal_store(o, qv + base + u * kThreads + threadIdx.x);
-            }
+            for (int u = 0; u < kU; ++u)
+                __builtin_nontemporal_store(quant_bf16x8<FMT, FAST>(v[u], d), qv + base + u * kThreads + threadIdx.x);
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
                 const u32x4 v = xv[i];
@@ -604,9 +625,15 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
             for (int e = 0; e < E; ++e) am = fold_f32(am, __float_as_uint(v[e]));
         }
         if (!CODES) return;
+        if (FAST && !wave_any_nan<E>(v)) {
 #pragma unroll
-        for (int g = 0; g < E / 4; ++g)
-            codes[rr][g] = quant4_t<FMT, FAST>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
+            for (int g = 0; g < E / 4; ++g)
+                codes[rr][g] = quant4_nonan<FMT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
+        } else {
+#pragma unroll
+            for (int g = 0; g < E / 4; ++g)
+                codes[rr][g] = quant4_t<FMT, FAST>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], d);
+        }
         if (q && r < rows && c < ldq) {
             uint8_t* const dst = q + (int64_t)r * ldq + c;
             if (E == 8)
@@ -645,17 +672,22 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     }
     if (CODES && qt) {
         // column e of this thread's chunk: RPT codes down rows rg*RPT...
+        // (wcol[e][k]: rows 4k..4k+3, byte i = row 4k+i)
+        uint32_t wcol[E][RPT / 4];
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            uint32_t w[RPT / 4];
+        for (int g = 0; g < E / 4; ++g) {
 #pragma unroll
             for (int k = 0; k < RPT / 4; ++k) {
-                uint32_t acc = 0;
+                uint32_t col[4];
+                transpose4x4_bytes(codes[4 * k][g], codes[4 * k + 1][g], codes[4 * k + 2][g], codes[4 * k + 3][g],
+                                   col);
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc |= ((codes[4 * k + b][e >> 2] >> (8 * (e & 3))) & 0xFFu) << (8 * b);
-                w[k] = acc;
+                for (int j = 0; j < 4; ++j) wcol[4 * g + j][k] = col[j];
             }
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const uint32_t* w = wcol[e];
             uint8_t* dst = tile + (tc + e) * TSTRIDE + rg * RPT;
             if (RPT == 16)
                 *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[RPT / 4 > 1 ? 1 : 0], w[RPT / 4 > 2 ? 2 : 0],
