@@ -663,7 +663,7 @@ def conversion_summary(out_dir, prof):
              "Commands (from the repository root, on one MI355X; three separate runs):", "",
              "    " + PROFILE_COMMANDS["stats_conversion"], "    " + PROFILE_COMMANDS["fetch_conversion"],
              "    " + PROFILE_COMMANDS["write_conversion"], "",
-             "Each conversion runs 1 + 10 times (warm-up, timed).  `hbm_probe_kernel<R, W>` is the bandwidth "
+             "Each conversion runs 1 + 10 times (warm-up, timed).  `hbm_probe_kernel<R, W, U>` is the bandwidth "
              "calibration with the same access pattern (R bytes read, W written per 16-byte vector slot).  "
              "Traffic: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the 1 GiB device copy of the same "
              f"runs (fetch x {fscale:.4f}, write x {wscale:.4f}); GB/s = (calibrated fetch + write) / average "
@@ -887,8 +887,9 @@ def conversion_bench(torch, df, synth, dev, stream, reps=10):
                 res[f"{kname}_{src}_{fname}"] = {"ms": round(ms, 4), "gbs": round(gbs, 1),
                                                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
     # The ceiling of each access pattern on this part: the same loads and
-    # stores as the kernels above (df_hbm_probe: 8 non-temporal 16-byte
-    # loads in flight per thread, one chunk per block), no arithmetic.
+    # stores as the kernels above (df_hbm_probe: non-temporal loads and
+    # stores, as many per thread as the kernel with that pattern issues,
+    # one chunk per block), no arithmetic.
     probe_dst = torch.empty(max(int(df.lib().df_hbm_probe_dst_bytes(16, 16, n * 4)), 16), dtype=torch.uint8,
                             device=dev)
     ceil = {}

@@ -53,6 +53,13 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t m) {
 // element-guarded loop.
 constexpr int kU = 8;
 constexpr int64_t kChunkVec = (int64_t)kThreads * kU;
+// Loads per thread and chunk of the flat conversions (the absmax reads keep
+// kU).  The store-heavy dequantize streams run best at 2048 elements per
+// 256-thread block (config 2, one MI355X): fp8 -> fp32 5.85 -> 6.21-6.37
+// TB/s going from 8 to 2 vectors per thread, fp8 -> bf16 5.97-6.01 ->
+// 6.29-6.36 from 8 to 1.  The quantize kernels keep 8: fp32 -> fp8 measured
+// 1-3% slower at 2 (5.89-6.06 against 6.09-6.13 TB/s), bf16 -> fp8 within 1%.
+constexpr int kUQuantF32 = 8, kUQuantBf16 = 8, kUDeqF32 = 2, kUDeqBf16 = 1;
 
 // Stage 1 bodies: the block's maximum over its chunks (block bi of nb
 // blocks walking the chunks with a stride of nb).  |x| bit patterns, NaN
@@ -207,23 +214,25 @@ __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* _
 template <int FMT, bool FAST>
 __device__ __forceinline__ void quantize_f32_body(const float* __restrict__ x, int64_t n, const QDiv& d,
                                                   uint8_t* __restrict__ q) {
+    constexpr int U = kUQuantF32;
+    constexpr int64_t CH = (int64_t)kThreads * U;
     const int64_t nvec = n >> 2;
     const f32x4* xv = reinterpret_cast<const f32x4*>(x);
     uint32_t* qv = reinterpret_cast<uint32_t*>(q);
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
-        if (base + kChunkVec <= nvec) {
-            f32x4 v[kU];
+    for (int64_t base = (int64_t)blockIdx.x * CH; base < nvec; base += (int64_t)gridDim.x * CH) {
+        if (base + CH <= nvec) {
+            f32x4 v[U];
 #pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
             const float* t = reinterpret_cast<const float*>(v);
-            if (FAST && !wave_any_nan<4 * kU>(t)) {
+            if (FAST && !wave_any_nan<4 * U>(t)) {
 #pragma unroll
-                for (int u = 0; u < kU; ++u)
+                for (int u = 0; u < U; ++u)
                     __builtin_nontemporal_store(quant4_nonan<FMT>(v[u].x, v[u].y, v[u].z, v[u].w, d),
                                                 qv + base + u * kThreads + threadIdx.x);
             } else {
 #pragma unroll
-                for (int u = 0; u < kU; ++u)
+                for (int u = 0; u < U; ++u)
                     __builtin_nontemporal_store(quant4_t<FMT, FAST>(v[u].x, v[u].y, v[u].z, v[u].w, d),
                                                 qv + base + u * kThreads + threadIdx.x);
             }
@@ -279,16 +288,18 @@ __device__ __forceinline__ u32x2 quant_bf16x8(const u32x4 w, const QDiv& d) {
 template <int FMT, bool FAST>
 __device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ x, int64_t n, const QDiv& d,
                                                    uint8_t* __restrict__ q) {
+    constexpr int U = kUQuantBf16;
+    constexpr int64_t CH = (int64_t)kThreads * U;
     const int64_t nvec = n >> 3;
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
     u32x2* qv = reinterpret_cast<u32x2*>(q);
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
-        if (base + kChunkVec <= nvec) {
-            u32x4 v[kU];
+    for (int64_t base = (int64_t)blockIdx.x * CH; base < nvec; base += (int64_t)gridDim.x * CH) {
+        if (base + CH <= nvec) {
+            u32x4 v[U];
 #pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-            for (int u = 0; u < kU; ++u)
+            for (int u = 0; u < U; ++u)
                 __builtin_nontemporal_store(quant_bf16x8<FMT, FAST>(v[u], d), qv + base + u * kThreads + threadIdx.x);
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
@@ -369,13 +380,15 @@ __global__ __launch_bounds__(kThreads) void dequantize_f32_kernel(const uint8_t*
         o.w = dequant_fp8<FMT>(w >> 24, s);
         return o;
     };
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
-        if (base + kChunkVec <= nvec) {
-            uint32_t w[kU];
+    constexpr int U = kUDeqF32;
+    constexpr int64_t CH = (int64_t)kThreads * U;
+    for (int64_t base = (int64_t)blockIdx.x * CH; base < nvec; base += (int64_t)gridDim.x * CH) {
+        if (base + CH <= nvec) {
+            uint32_t w[U];
 #pragma unroll
-            for (int u = 0; u < kU; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(deq4(w[u]), ov + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) __builtin_nontemporal_store(deq4(w[u]), ov + base + u * kThreads + threadIdx.x);
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) ov[i] = deq4(qv[i]);
         }
@@ -406,13 +419,15 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
         return u32x4{deq_bf16x2<FMT, false>(w.x, s), deq_bf16x2<FMT, true>(w.x, s), deq_bf16x2<FMT, false>(w.y, s),
                      deq_bf16x2<FMT, true>(w.y, s)};
     };
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
-        if (base + kChunkVec <= nvec) {
-            u32x2 w[kU];
+    constexpr int U = kUDeqBf16;
+    constexpr int64_t CH = (int64_t)kThreads * U;
+    for (int64_t base = (int64_t)blockIdx.x * CH; base < nvec; base += (int64_t)gridDim.x * CH) {
+        if (base + CH <= nvec) {
+            u32x2 w[U];
 #pragma unroll
-            for (int u = 0; u < kU; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(deq8(w[u]), ov + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) __builtin_nontemporal_store(deq8(w[u]), ov + base + u * kThreads + threadIdx.x);
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) ov[i] = deq8(qv[i]);
         }
@@ -1016,9 +1031,11 @@ __global__ __launch_bounds__(kThreads) void colsum_reduce_kernel(const float* __
 
 // ------------------------------------------------------ bandwidth probe --
 // The flat kernels' access pattern without their arithmetic: per chunk,
-// each thread issues kU non-temporal loads of RB bytes, kThreads apart,
-// then kU non-temporal stores of WB bytes at the same vector index (the
-// stored words are an XOR fold of the loaded ones, so no load is dead).
+// each thread issues U non-temporal loads of RB bytes, kThreads apart,
+// then U non-temporal stores of WB bytes at the same vector index (the
+// stored words are an XOR fold of the loaded ones, so no load is dead); U
+// is the depth of the kernel with that pattern (kU for the read, kUQuant*
+// and kUDeq* for the conversions, kUDeqF32 for the copy).
 // RB:WB = 16:4 is fp32 -> fp8, 16:8 bf16 -> fp8, 4:16 fp8 -> fp32, 8:16
 // fp8 -> bf16, 16:16 a copy, 16:0 a read (absmax: one word per block).
 template <int RB> struct ProbeVec;
@@ -1043,24 +1060,25 @@ template <> struct ProbeOut<16> {
     static __device__ __forceinline__ u32x4 make(u32x4 v) { return u32x4{v.x ^ 1u, v.y, v.z, v.w}; }
 };
 
-template <int RB, int WB>
+template <int RB, int WB, int U>
 __global__ __launch_bounds__(kThreads) void hbm_probe_kernel(const void* __restrict__ src, int64_t nvec,
                                                                void* __restrict__ dst) {
     using V = typename ProbeVec<RB>::T;
     const V* xv = reinterpret_cast<const V*>(src);
+    constexpr int64_t CH = (int64_t)kThreads * U;
     uint32_t acc = 0;
-    for (int64_t base = (int64_t)blockIdx.x * kChunkVec; base < nvec; base += (int64_t)gridDim.x * kChunkVec) {
-        V v[kU];
+    for (int64_t base = (int64_t)blockIdx.x * CH; base < nvec; base += (int64_t)gridDim.x * CH) {
+        V v[U];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
         if constexpr (WB == 0) {
 #pragma unroll
-            for (int u = 0; u < kU; ++u) acc ^= fold_words(v[u]);
+            for (int u = 0; u < U; ++u) acc ^= fold_words(v[u]);
         } else {
             using O = decltype(ProbeOut<WB>::make(v[0]));
             O* ov = reinterpret_cast<O*>(dst);
 #pragma unroll
-            for (int u = 0; u < kU; ++u)
+            for (int u = 0; u < U; ++u)
                 __builtin_nontemporal_store(ProbeOut<WB>::make(v[u]), ov + base + u * kThreads + threadIdx.x);
         }
     }
@@ -1081,11 +1099,17 @@ static int grid_for(int64_t units, int64_t per_block_unit_cap) {
 
 using namespace dfk;
 
-// Grid cap for the quantize/dequantize kernels: about one chunk per block up
-// to 2^28 fp32 elements, grid-stride beyond.  Many short-lived blocks keep
-// more of the chip's store traffic in flight than 2048 looping blocks:
-// +5-7% at config 2 (e.g. fp32 -> e4m3 5.52-5.65 -> 5.91-6.01 TB/s).
-static constexpr int64_t kStreamBlocks = 32768;
+// Grid cap for the quantize/dequantize kernels: one chunk per block up to
+// 2^28 elements, grid-stride beyond.  Many short-lived blocks keep more of
+// the chip's store traffic in flight than 2048 looping blocks: +5-7% at
+// config 2 (e.g. fp32 -> e4m3 5.52-5.65 -> 5.91-6.01 TB/s with 8 vectors
+// per thread).
+static constexpr int64_t kStreamBlocks = 131072;
+
+// blocks for n elements, per elements per thread vector, U vectors per thread
+static int stream_grid(int64_t n, int per, int U) {
+    return grid_for((n / per + 1 + U - 1) / U, kStreamBlocks);
+}
 
 extern "C" size_t df_absmax_workspace_bytes(void) { return kMaxReduceBlocks * sizeof(uint32_t); }
 
@@ -1105,25 +1129,28 @@ extern "C" int df_hbm_probe(int read_bytes, int write_bytes, const void* src, in
                     ((read_bytes == 4 || read_bytes == 8) && write_bytes == 16);
     DF_CHECK(ok, DF_ERR_UNSUPPORTED, "%s: pattern %d:%d not provided", name, read_bytes, write_bytes);
     DF_CHECK(src && dst, DF_ERR_INVALID, "%s: NULL pointer", name);
-    const int64_t chunk_bytes = kChunkVec * read_bytes;
+    const int U = read_bytes == 16 ? (write_bytes == 0 ? kU : write_bytes == 4 ? kUQuantF32
+                                                          : write_bytes == 8 ? kUQuantBf16 : kUDeqF32)
+                                    : (read_bytes == 4 ? kUDeqF32 : kUDeqBf16);
+    const int64_t chunk_bytes = (int64_t)kThreads * U * read_bytes;
     DF_CHECK(src_bytes > 0 && src_bytes % chunk_bytes == 0, DF_ERR_INVALID,
              "%s: src_bytes=%lld must be a positive multiple of %lld", name, (long long)src_bytes,
              (long long)chunk_bytes);
     DF_CHECK(aligned16(src) && aligned16(dst), DF_ERR_ALIGN, "%s: src and dst must be 16-byte aligned", name);
     const int64_t nvec = src_bytes / read_bytes;
-    const int blocks = grid_for(nvec / kU, kStreamBlocks);
+    const int blocks = grid_for(nvec / U, kStreamBlocks);
     hipStream_t st = as_stream(stream);
-#define DF_PROBE(R, W)                                                                 \
+#define DF_PROBE(R, W, UU)                                                             \
     if (read_bytes == R && write_bytes == W) {                                         \
-        hbm_probe_kernel<R, W><<<blocks, kThreads, 0, st>>>(src, nvec, dst);          \
+        hbm_probe_kernel<R, W, UU><<<blocks, kThreads, 0, st>>>(src, nvec, dst);      \
         return launch_status(name);                                                    \
     }
-    DF_PROBE(16, 0)
-    DF_PROBE(16, 4)
-    DF_PROBE(16, 8)
-    DF_PROBE(16, 16)
-    DF_PROBE(4, 16)
-    DF_PROBE(8, 16)
+    DF_PROBE(16, 0, kU)
+    DF_PROBE(16, 4, kUQuantF32)
+    DF_PROBE(16, 8, kUQuantBf16)
+    DF_PROBE(16, 16, kUDeqF32)
+    DF_PROBE(4, 16, kUDeqF32)
+    DF_PROBE(8, 16, kUDeqBf16)
 #undef DF_PROBE
     return DF_ERR_UNSUPPORTED;
 }
@@ -1199,7 +1226,7 @@ static int quantize_f32_impl(const float* x, int64_t n, const float* scale, uint
     if (n == 0) return DF_OK;
     DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned16(x) && aligned4(q), DF_ERR_ALIGN, "%s: x must be 16-byte and q 4-byte aligned", name);
-    const int blocks = grid_for((n / 4 + 1 + kU - 1) / kU, kStreamBlocks);
+    const int blocks = stream_grid(n, 4, kUQuantF32);
     quantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
     return launch_status(name);
 }
@@ -1213,7 +1240,7 @@ static int quantize_bf16_impl(const uint16_t* x, int64_t n, const float* scale, 
     DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned16(x) && (((uintptr_t)q & 7u) == 0), DF_ERR_ALIGN,
              "%s: x must be 16-byte and q 8-byte aligned", name);
-    const int blocks = grid_for((n / 8 + 1 + kU - 1) / kU, kStreamBlocks);
+    const int blocks = stream_grid(n, 8, kUQuantBf16);
     quantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
     return launch_status(name);
 }
@@ -1240,7 +1267,7 @@ static int dequantize_f32_impl(const uint8_t* q, int64_t n, const float* scale, 
     DF_CHECK(q && scale && out, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned4(q) && aligned16(out), DF_ERR_ALIGN, "%s: q must be 4-byte and out 16-byte aligned",
              name);
-    const int blocks = grid_for((n / 4 + 1 + kU - 1) / kU, kStreamBlocks);
+    const int blocks = stream_grid(n, 4, kUDeqF32);
     dequantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
     return launch_status(name);
 }
@@ -1254,7 +1281,7 @@ static int dequantize_bf16_impl(const uint8_t* q, int64_t n, const float* scale,
     DF_CHECK(q && scale && out, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK((((uintptr_t)q & 7u) == 0) && aligned16(out), DF_ERR_ALIGN,
              "%s: q must be 8-byte and out 16-byte aligned", name);
-    const int blocks = grid_for((n / 8 + 1 + kU - 1) / kU, kStreamBlocks);
+    const int blocks = stream_grid(n, 8, kUDeqBf16);
     dequantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
     return launch_status(name);
 }
