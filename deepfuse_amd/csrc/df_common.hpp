@@ -271,6 +271,7 @@ int launch_status(const char* what);  // DF_OK or DF_ERR_HIP (checks hipGetLastE
 int device_cu_count();                 // compute units of the current device (cached; 0 on error)
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline bool aligned128(const void* p) { return ((uintptr_t)p & 127u) == 0; }
 inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -210,8 +210,24 @@ __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* _
 // x / s (correctly rounded: qdiv, contract D1), then the fp8 encoder
 // (encode2_hw: hardware round-to-nearest-even after saturation, NaN kept).
 
+// plain or non-temporal (NT) accesses.  The flat kernels store
+// non-temporal (NTS) when their output starts on a 128-byte boundary: every
+// wave store then covers whole cache lines.  A misaligned output takes plain
+// stores, so no line is assembled from several non-temporal partial writes
+// of neighbouring blocks.
+template <bool NT, typename T> __device__ __forceinline__ T ld_nt(const T* p) {
+    if (NT) return __builtin_nontemporal_load(p);
+    return *p;
+}
+template <bool NT, typename T> __device__ __forceinline__ void st_nt(T* p, const T v) {
+    if (NT)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
+}
+
 // fp32 -> fp8: a 16-byte load of 4 values -> a 4-byte store of 4 codes.
-template <int FMT, bool FAST>
+template <int FMT, bool FAST, bool NTS>
 __device__ __forceinline__ void quantize_f32_body(const float* __restrict__ x, int64_t n, const QDiv& d,
                                                   uint8_t* __restrict__ q) {
     constexpr int U = kUQuantF32;
@@ -228,13 +244,13 @@ __device__ __forceinline__ void quantize_f32_body(const float* __restrict__ x, i
             if (FAST && !wave_any_nan<4 * U>(t)) {
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    __builtin_nontemporal_store(quant4_nonan<FMT>(v[u].x, v[u].y, v[u].z, v[u].w, d),
-                                                qv + base + u * kThreads + threadIdx.x);
+                    st_nt<NTS>(qv + base + u * kThreads + threadIdx.x,
+                               quant4_nonan<FMT>(v[u].x, v[u].y, v[u].z, v[u].w, d));
             } else {
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    __builtin_nontemporal_store(quant4_t<FMT, FAST>(v[u].x, v[u].y, v[u].z, v[u].w, d),
-                                                qv + base + u * kThreads + threadIdx.x);
+                    st_nt<NTS>(qv + base + u * kThreads + threadIdx.x,
+                               quant4_t<FMT, FAST>(v[u].x, v[u].y, v[u].z, v[u].w, d));
             }
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
@@ -249,16 +265,16 @@ __device__ __forceinline__ void quantize_f32_body(const float* __restrict__ x, i
     }
 }
 
-template <int FMT>
+template <int FMT, bool NTS>
 __global__ __launch_bounds__(kThreads) void quantize_f32_kernel(const float* __restrict__ x,
                                                                  int64_t n,
                                                                  const float* __restrict__ scale,
                                                                  uint8_t* __restrict__ q) {
     const QDiv d = make_qdiv(scale[0]);
     if (d.fast)
-        quantize_f32_body<FMT, true>(x, n, d, q);
+        quantize_f32_body<FMT, true, NTS>(x, n, d, q);
     else
-        quantize_f32_body<FMT, false>(x, n, d, q);
+        quantize_f32_body<FMT, false, NTS>(x, n, d, q);
 }
 
 // bf16 -> fp8: one 16-byte load (8 values) -> one 8-byte store.
@@ -285,7 +301,7 @@ __device__ __forceinline__ u32x2 quant_bf16x8(const u32x4 w, const QDiv& d) {
     return o;
 }
 
-template <int FMT, bool FAST>
+template <int FMT, bool FAST, bool NTS>
 __device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ x, int64_t n, const QDiv& d,
                                                    uint8_t* __restrict__ q) {
     constexpr int U = kUQuantBf16;
@@ -300,7 +316,7 @@ __device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ 
             for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(xv + base + u * kThreads + threadIdx.x);
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                __builtin_nontemporal_store(quant_bf16x8<FMT, FAST>(v[u], d), qv + base + u * kThreads + threadIdx.x);
+                st_nt<NTS>(qv + base + u * kThreads + threadIdx.x, quant_bf16x8<FMT, FAST>(v[u], d));
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) {
                 const u32x4 v = xv[i];
@@ -317,16 +333,16 @@ __device__ __forceinline__ void quantize_bf16_body(const uint16_t* __restrict__ 
     }
 }
 
-template <int FMT>
+template <int FMT, bool NTS>
 __global__ __launch_bounds__(kThreads) void quantize_bf16_kernel(const uint16_t* __restrict__ x,
                                                                   int64_t n,
                                                                   const float* __restrict__ scale,
                                                                   uint8_t* __restrict__ q) {
     const QDiv d = make_qdiv(scale[0]);
     if (d.fast)
-        quantize_bf16_body<FMT, true>(x, n, d, q);
+        quantize_bf16_body<FMT, true, NTS>(x, n, d, q);
     else
-        quantize_bf16_body<FMT, false>(x, n, d, q);
+        quantize_bf16_body<FMT, false, NTS>(x, n, d, q);
 }
 
 // -------------------------------------------------------------- dequantize --
@@ -363,7 +379,7 @@ __device__ __forceinline__ uint32_t pack_bf16_hw(float a, float b) {
 
 // fp8 -> fp32: a 4-byte load (4 codes) -> a 16-byte store; the chunks count
 // output vectors.
-template <int FMT>
+template <int FMT, bool NTS>
 __global__ __launch_bounds__(kThreads) void dequantize_f32_kernel(const uint8_t* __restrict__ q,
                                                                    int64_t n,
                                                                    const float* __restrict__ scale,
@@ -388,7 +404,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_f32_kernel(const uint8_t*
 #pragma unroll
             for (int u = 0; u < U; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-            for (int u = 0; u < U; ++u) __builtin_nontemporal_store(deq4(w[u]), ov + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) st_nt<NTS>(ov + base + u * kThreads + threadIdx.x, deq4(w[u]));
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) ov[i] = deq4(qv[i]);
         }
@@ -406,7 +422,7 @@ __device__ __forceinline__ uint32_t deq_bf16x2(uint32_t w, float s) {
     return pack_bf16_hw(with_sign_of(v.x * s, w << (HI ? 8 : 24)), with_sign_of(v.y * s, w << (HI ? 0 : 16)));
 }
 
-template <int FMT>
+template <int FMT, bool NTS>
 __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t* __restrict__ q,
                                                                     int64_t n,
                                                                     const float* __restrict__ scale,
@@ -427,7 +443,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
 #pragma unroll
             for (int u = 0; u < U; ++u) w[u] = __builtin_nontemporal_load(qv + base + u * kThreads + threadIdx.x);
 #pragma unroll
-            for (int u = 0; u < U; ++u) __builtin_nontemporal_store(deq8(w[u]), ov + base + u * kThreads + threadIdx.x);
+            for (int u = 0; u < U; ++u) st_nt<NTS>(ov + base + u * kThreads + threadIdx.x, deq8(w[u]));
         } else {
             for (int64_t i = base + threadIdx.x; i < nvec; i += kThreads) ov[i] = deq8(qv[i]);
         }
@@ -562,17 +578,6 @@ __device__ __forceinline__ float ln_apply(float x, float mean, float rstd, bool 
     return round_to<InT>(n);
 }
 
-// plain or non-temporal (NT) 16-byte accesses
-template <bool NT, typename T> __device__ __forceinline__ T ld_nt(const T* p) {
-    if (NT) return __builtin_nontemporal_load(p);
-    return *p;
-}
-template <bool NT, typename T> __device__ __forceinline__ void st_nt(T* p, const T v) {
-    if (NT)
-        __builtin_nontemporal_store(v, p);
-    else
-        *p = v;
-}
 
 // With AMAX the block also folds |x| over finite values of its tile into one
 // partial maximum (binary32 bit pattern), amaxpart[tile index], for the
@@ -597,6 +602,12 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
     const int c = c0 + tc;
     const bool full = vec_ok && c + E <= cols;
+    // Non-temporal stores only where each 128-byte row segment a block
+    // writes is one whole cache line (output and its row stride 128-byte
+    // aligned), so no line is assembled from several non-temporal partial
+    // writes; other layouts take plain stores.
+    const bool q_lines = ((reinterpret_cast<uintptr_t>(q) | (uint32_t)ldq) & 127u) == 0;
+    const bool qt_lines = ((reinterpret_cast<uintptr_t>(qt) | (uint32_t)ldqt) & 127u) == 0;
     uint32_t codes[RPT][E / 4];
     float cs[E];
     uint32_t am = 0;
@@ -651,10 +662,17 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
         }
         if (q && r < rows && c < ldq) {
             uint8_t* const dst = q + (int64_t)r * ldq + c;
-            if (E == 8)
-                st_nt<NT>(reinterpret_cast<u32x2*>(dst), u32x2{codes[rr][0], codes[rr][E / 4 - 1]});
-            else
-                st_nt<NT>(reinterpret_cast<uint32_t*>(dst), codes[rr][0]);
+            if (NT && q_lines) {
+                if (E == 8)
+                    st_nt<true>(reinterpret_cast<u32x2*>(dst), u32x2{codes[rr][0], codes[rr][E / 4 - 1]});
+                else
+                    st_nt<true>(reinterpret_cast<uint32_t*>(dst), codes[rr][0]);
+            } else {
+                if (E == 8)
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{codes[rr][0], codes[rr][E / 4 - 1]};
+                else
+                    *reinterpret_cast<uint32_t*>(dst) = codes[rr][0];
+            }
         }
     };
     if (full && r0 + kT2 <= rows) {
@@ -721,9 +739,14 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
         for (int k = 0; k < 4; ++k) {
             const int idx = threadIdx.x + kThreads * k;
             const int col = idx >> 3, rc = (idx & 7) * 16;
-            if (c0 + col < cols && r0 + rc < ldqt)
-                st_nt<NT>(reinterpret_cast<u32x4*>(qt + (int64_t)(c0 + col) * ldqt + r0 + rc),
-                            *reinterpret_cast<const u32x4*>(tile + col * TSTRIDE + rc));
+            if (c0 + col < cols && r0 + rc < ldqt) {
+                u32x4* dst = reinterpret_cast<u32x4*>(qt + (int64_t)(c0 + col) * ldqt + r0 + rc);
+                const u32x4 v = *reinterpret_cast<const u32x4*>(tile + col * TSTRIDE + rc);
+                if (NT && qt_lines)
+                    st_nt<true>(dst, v);
+                else
+                    st_nt<false>(dst, v);
+            }
         }
     }
     if (COLSUM && r0 < rows && threadIdx.x < kT2 && c0 + threadIdx.x < cols) {
@@ -1227,7 +1250,10 @@ static int quantize_f32_impl(const float* x, int64_t n, const float* scale, uint
     DF_CHECK(x && scale && q, DF_ERR_INVALID, "%s: NULL pointer", name);
     DF_CHECK(aligned16(x) && aligned4(q), DF_ERR_ALIGN, "%s: x must be 16-byte and q 4-byte aligned", name);
     const int blocks = stream_grid(n, 4, kUQuantF32);
-    quantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
+    if (aligned128(q))
+        quantize_f32_kernel<FMT, true><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
+    else
+        quantize_f32_kernel<FMT, false><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
     return launch_status(name);
 }
 
@@ -1241,7 +1267,10 @@ static int quantize_bf16_impl(const uint16_t* x, int64_t n, const float* scale, 
     DF_CHECK(aligned16(x) && (((uintptr_t)q & 7u) == 0), DF_ERR_ALIGN,
              "%s: x must be 16-byte and q 8-byte aligned", name);
     const int blocks = stream_grid(n, 8, kUQuantBf16);
-    quantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
+    if (aligned128(q))
+        quantize_bf16_kernel<FMT, true><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
+    else
+        quantize_bf16_kernel<FMT, false><<<blocks, kThreads, 0, as_stream(stream)>>>(x, n, scale, q);
     return launch_status(name);
 }
 
@@ -1268,7 +1297,10 @@ static int dequantize_f32_impl(const uint8_t* q, int64_t n, const float* scale, 
     DF_CHECK(aligned4(q) && aligned16(out), DF_ERR_ALIGN, "%s: q must be 4-byte and out 16-byte aligned",
              name);
     const int blocks = stream_grid(n, 4, kUDeqF32);
-    dequantize_f32_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
+    if (aligned128(out))
+        dequantize_f32_kernel<FMT, true><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
+    else
+        dequantize_f32_kernel<FMT, false><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
     return launch_status(name);
 }
 
@@ -1282,7 +1314,10 @@ static int dequantize_bf16_impl(const uint8_t* q, int64_t n, const float* scale,
     DF_CHECK((((uintptr_t)q & 7u) == 0) && aligned16(out), DF_ERR_ALIGN,
              "%s: q must be 8-byte and out 16-byte aligned", name);
     const int blocks = stream_grid(n, 8, kUDeqBf16);
-    dequantize_bf16_kernel<FMT><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
+    if (aligned128(out))
+        dequantize_bf16_kernel<FMT, true><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
+    else
+        dequantize_bf16_kernel<FMT, false><<<blocks, kThreads, 0, as_stream(stream)>>>(q, n, scale, out);
     return launch_status(name);
 }
 

@@ -176,3 +176,57 @@ def test_random_f32_patterns(dev, fmt, nan):
         s32 = float(np.float32(s))
         q, qt = df.quantize_2d(xd, torch.tensor([s32], device=dev), fmt, want_q=True, want_qt=True)
         check_codes(q, qt, orc.quantize(x, s32, int(fmt)), 2048, 2304, f"s={s32}")
+
+
+@pytest.mark.parametrize("fmt", [Fmt.E4M3, Fmt.E5M2])
+def test_outputs_off_line_boundaries(dev, fmt):
+    """Outputs that do not start on (or whose rows do not stride by) 128
+    bytes take plain stores instead of non-temporal ones: the same codes and
+    values as aligned outputs, and the oracle's."""
+    st = torch.cuda.current_stream().cuda_stream
+    n = (1 << 20) + 40
+    x = synth.normal((n,), seed=synth.SEED_BASE + 950)
+    s = float(np.float32(orc.scale(orc.absmax(x), int(fmt))))
+    sd = torch.tensor([s], device=dev)
+    name = "e4m3" if fmt == Fmt.E4M3 else "e5m2"
+    exp = orc.quantize(x, s, int(fmt))
+    xd = torch.from_numpy(x).to(dev)
+    xb_bits = synth.f32_to_bf16_bits(x)
+    xb = torch.from_numpy(xb_bits.view(np.int16)).to(dev).view(torch.bfloat16)
+    expb = orc.quantize(xb_bits, s, int(fmt))
+    for off in (8, 72):  # bytes past a 128-byte boundary (q must be 8-byte aligned for bf16)
+        buf = torch.zeros(n + 256, dtype=torch.uint8, device=dev)
+        df.call(f"df_quantize_f32_{name}", xd.data_ptr(), n, sd.data_ptr(), buf.data_ptr() + off, st)
+        assert np.array_equal(buf[off:off + n].cpu().numpy(), exp), f"f32 codes at +{off}"
+        df.call(f"df_quantize_bf16_{name}", xb.data_ptr(), n, sd.data_ptr(), buf.data_ptr() + off, st)
+        assert np.array_equal(buf[off:off + n].cpu().numpy(), expb), f"bf16 codes at +{off}"
+    q = torch.from_numpy(exp).to(dev)
+    qb = torch.zeros(n + 256, dtype=torch.uint8, device=dev)
+    qb[8:8 + n] = q
+    for off in (16, 48):  # outputs must be 16-byte aligned
+        ref32 = df.dequantize(q, sd, fmt, torch.float32)
+        ref16 = df.dequantize(q, sd, fmt, torch.bfloat16)
+        o32 = torch.zeros(n + 64, dtype=torch.float32, device=dev)
+        df.call(f"df_dequantize_{name}_f32", qb.data_ptr() + 8, n, sd.data_ptr(), o32.data_ptr() + off, st)
+        assert torch.equal(o32[off // 4:off // 4 + n].view(torch.int32), ref32.view(torch.int32)), f"f32 at +{off}"
+        o16 = torch.zeros(n + 64, dtype=torch.bfloat16, device=dev)
+        df.call(f"df_dequantize_{name}_bf16", qb.data_ptr() + 8, n, sd.data_ptr(), o16.data_ptr() + off, st)
+        assert torch.equal(o16[off // 2:off // 2 + n].view(torch.int16), ref16.view(torch.int16)), f"bf16 at +{off}"
+    # 2-D outputs with row strides that are not multiples of 128 (delayed
+    # scaling, whose codes are otherwise stored non-temporal), against the
+    # aligned layout
+    rows, cols = 2048, 2304
+    xd2, _, vals = make(dev, rows, cols, "bf16", seed=synth.SEED_BASE + 951)
+    a = df.DelayedScale(fmt, 2, dev)
+    b = df.DelayedScale(fmt, 2, dev)
+    qa, qta = a.quantize_2d(xd2, want_q=True, want_qt=True)
+    ldq, ldqt = cols + 16, rows + 48
+    qo = torch.zeros((rows, ldq), dtype=torch.uint8, device=dev)
+    qto = torch.zeros((cols, ldqt), dtype=torch.uint8, device=dev)
+    nbytes = df.lib().df_quantize_2d_delayed_workspace_bytes(rows, cols, ldq, ldqt, 0)
+    ws = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+    df.call("df_quantize_2d_delayed", 4, xd2.data_ptr(), rows, cols, cols, int(fmt), b.scale.data_ptr(),
+            b.scale.data_ptr(), b.history.data_ptr(), 2, qo.data_ptr(), ldq, qto.data_ptr(), ldqt, None,
+            ws.data_ptr(), ws.numel(), st)
+    assert torch.equal(qo[:, :cols], qa[:, :cols]) and torch.equal(qto[:, :rows], qta[:, :rows])
+    assert torch.equal(a.history.view(torch.int32), b.history.view(torch.int32))
