@@ -54,12 +54,12 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t m) {
 constexpr int kU = 8;
 constexpr int64_t kChunkVec = (int64_t)kThreads * kU;
 // Loads per thread and chunk of the flat conversions (the absmax reads keep
-// kU).  The store-heavy dequantize streams run best at 2048 elements per
-// 256-thread block (config 2, one MI355X): fp8 -> fp32 5.85 -> 6.21-6.37
-// TB/s going from 8 to 2 vectors per thread, fp8 -> bf16 5.97-6.01 ->
-// 6.29-6.36 from 8 to 1.  The quantize kernels keep 8: fp32 -> fp8 measured
-// 1-3% slower at 2 (5.89-6.06 against 6.09-6.13 TB/s), bf16 -> fp8 within 1%.
-constexpr int kUQuantF32 = 8, kUQuantBf16 = 8, kUDeqF32 = 2, kUDeqBf16 = 1;
+// kU).  The fp32 conversions run best at 2048 elements per 256-thread block
+// (config 2, one MI355X, alternating runs on one box): fp8 -> fp32 5.85 ->
+// 6.21-6.37 TB/s going from 8 to 2 vectors per thread, fp8 -> bf16
+// 5.97-6.01 -> 6.29-6.36 from 8 to 1, fp32 -> fp8 6.08-6.11 -> 6.28-6.36
+// from 8 to 2.  bf16 -> fp8 is within 1% between 8, 4 and 2 and keeps 8.
+constexpr int kUQuantF32 = 2, kUQuantBf16 = 8, kUDeqF32 = 2, kUDeqBf16 = 1;
 
 // Stage 1 bodies: the block's maximum over its chunks (block bi of nb
 // blocks walking the chunks with a stride of nb).  |x| bit patterns, NaN
