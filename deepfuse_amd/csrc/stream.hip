@@ -1,9 +1,10 @@
 // stream.hip -- layer weight streaming: a ring of device slots filled from
-// pinned host memory by hipMemcpyAsync on the streamer's own copy stream,
-// ordered against the compute stream with events in both directions:
+// pinned host memory by hipMemcpyAsync on the streamer's own two copy
+// streams (consecutive loads alternate), ordered against the compute stream
+// with events in both directions:
 //   load(l)    : the calling thread waits until the event recorded when the
 //                slot's previous contents were released has completed, then
-//                enqueues the copy and records loaded[s] on the copy stream;
+//                enqueues the copy and records loaded[s] on its copy stream;
 //   wait(s)    : the compute stream waits for loaded[s];
 //   release(s) : records released[s] on the compute stream after the last
 //                launch that reads the slot.
@@ -11,6 +12,15 @@
 // layer l's launches), the thread blocks until layer l-2 has finished while
 // layers l-1 and l are queued, and the copies run S-2 layers ahead of the
 // kernels that read them.
+//
+// Two copy streams: a load is enqueued when its slot frees, which at the
+// compute pace often finds the copy engine idle, and a copy started on an
+// idle engine took about 90 us longer than one queued behind another
+// (30.72 MB copies: 0.54 ms back to back, gaps of 93-121 us between
+// host-paced ones).  That made the streamed config-5 step copy-bound (about
+// 0.63 ms of copy per layer against 0.56 ms of compute).  With consecutive
+// loads on alternating streams one copy's start overlaps the other's
+// transfer.
 //
 // The reference describes this as layer-serialized execution
 // (README.md:212-226) but implements only the host side of it: pinned
@@ -26,7 +36,7 @@
 
 namespace dfk {
 
-constexpr int kMaxSlots = 16;
+constexpr int kMaxSlots = 64;
 
 constexpr size_t kSlotAlign = 4096;
 
@@ -39,7 +49,8 @@ struct df_streamer_s {
     int slots = 0;
     size_t slot_bytes = 0;
     uint8_t* dev = nullptr;
-    hipStream_t copy = nullptr;
+    hipStream_t copy[2] = {};
+    unsigned loads = 0;  // loads issued: load i goes to copy[i % 2]
     hipEvent_t loaded[dfk::kMaxSlots] = {};
     hipEvent_t released[dfk::kMaxSlots] = {};
     int state[dfk::kMaxSlots] = {};
@@ -74,12 +85,14 @@ extern "C" int df_host_free(void* host_ptr) {
 
 static void destroy_streamer(df_streamer_s* s) {
     if (!s) return;
-    if (s->copy) (void)hipStreamSynchronize(s->copy);
+    for (hipStream_t c : s->copy)
+        if (c) (void)hipStreamSynchronize(c);
     for (int i = 0; i < kMaxSlots; ++i) {
         if (s->loaded[i]) (void)hipEventDestroy(s->loaded[i]);
         if (s->released[i]) (void)hipEventDestroy(s->released[i]);
     }
-    if (s->copy) (void)hipStreamDestroy(s->copy);
+    for (hipStream_t c : s->copy)
+        if (c) (void)hipStreamDestroy(c);
     if (s->dev) (void)hipFree(s->dev);
     delete s;
 }
@@ -98,7 +111,8 @@ extern "C" int df_streamer_create(int slots, size_t slot_bytes, df_streamer_s** 
     hipError_t e = hipGetDevice(&s->device);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->dev), s->slot_bytes * (size_t)slots);
     // default priority, non-blocking with respect to the null stream
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->copy, hipStreamNonBlocking);
+    for (hipStream_t& c : s->copy)
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&c, hipStreamNonBlocking);
     for (int i = 0; i < slots && e == hipSuccess; ++i) {
         e = hipEventCreateWithFlags(&s->loaded[i], hipEventDisableTiming);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&s->released[i], hipEventDisableTiming);
@@ -121,7 +135,7 @@ extern "C" int df_streamer_destroy(df_streamer_s* s) {
 extern "C" int df_streamer_copy_stream(df_streamer_s* s, void** stream) {
     clear_error();
     DF_CHECK(s && stream, DF_ERR_INVALID, "df_streamer_copy_stream: NULL argument");
-    *stream = s->copy;
+    *stream = s->copy[0];
     return DF_OK;
 }
 
@@ -147,8 +161,9 @@ extern "C" int df_streamer_load(df_streamer_s* s, const void* host_src, size_t b
     // 96-layer sweep whose kernels alone take 57.6 ms).
     if (s->state[k] == kReleased) DF_HIP(hipEventSynchronize(s->released[k]), "df_streamer_load");
     uint8_t* dst = s->dev + (size_t)k * s->slot_bytes;
-    if (bytes) DF_HIP(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, s->copy), "df_streamer_load");
-    DF_HIP(hipEventRecord(s->loaded[k], s->copy), "df_streamer_load");
+    hipStream_t cs = s->copy[s->loads++ & 1u];
+    if (bytes) DF_HIP(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, cs), "df_streamer_load");
+    DF_HIP(hipEventRecord(s->loaded[k], cs), "df_streamer_load");
     s->state[k] = kLoaded;
     s->next = (k + 1) % s->slots;
     *slot = k;

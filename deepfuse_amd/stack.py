@@ -8,7 +8,7 @@ Here every layer's four Linears (qkv 1600->4800, attn proj 1600->1600, fc
 1600->6400, proj 6400->1600) keep their e4m3 weight codes in pinned host
 memory: W [N, K] for the forward sweep and W^T [K, N] for the backward sweep
 (layers in reverse), brought to the device through a df_streamer ring of
-device slots on the streamer's copy stream while earlier layers compute.
+device slots on the streamer's copy streams while earlier layers compute.
 
 Per layer and Linear, forward: absmax + 2-D quantize of the activation X
 (e4m3, the row copy and the transposed copy that this layer's dW reads) and

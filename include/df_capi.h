@@ -364,12 +364,13 @@ int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
  * loader -- pinned cudaHostAlloc buffers, per-slot streams, cudaMemcpyAsync,
  * apps/host-multi/NVMeLoader_Linux.hpp:20-26,64-71,123-125) ----
  * A streamer owns `slots` device buffers of slot_bytes (rounded up to 4 KiB)
- * and a copy stream of default priority.  Per layer:
+ * and two copy streams of default priority (consecutive loads alternate, so
+ * one copy's start overlaps the other's transfer).  Per layer:
  *   df_streamer_load    : blocks the calling thread until the work recorded
  *                         by the next slot's last df_streamer_release has
  *                         completed, then enqueues the copy of `bytes` from
  *                         host memory (pinned, for the copy to be
- *                         asynchronous) into that slot (ring order) on the
+ *                         asynchronous) into that slot (ring order) on a
  *                         copy stream;
  *   df_streamer_wait    : makes `stream` wait until the slot's copy landed;
  *   df_streamer_release : records, on `stream`, the point after which the
@@ -388,7 +389,7 @@ int df_streamer_load(df_streamer* s, const void* host_src, size_t bytes, int* sl
 int df_streamer_wait(df_streamer* s, int slot, void* stream);
 int df_streamer_release(df_streamer* s, int slot, void* stream);
 int df_streamer_slot(df_streamer* s, int slot, void** dev_ptr);
-int df_streamer_copy_stream(df_streamer* s, void** stream);  /* the hipStream_t of the copies */
+int df_streamer_copy_stream(df_streamer* s, void** stream);  /* the first of the two copy streams */
 
 /* ---- consumer side of the fp32 gradients: global-norm clipping and Adam ----
  * Lists of fp32 tensors: the pointer arrays and `sizes` are HOST arrays of
