@@ -58,8 +58,9 @@ constexpr int64_t kChunkVec = (int64_t)kThreads * kU;
 // (config 2, one MI355X, alternating runs on one box): fp8 -> fp32 5.85 ->
 // 6.21-6.37 TB/s going from 8 to 2 vectors per thread, fp8 -> bf16
 // 5.97-6.01 -> 6.29-6.36 from 8 to 1, fp32 -> fp8 6.08-6.11 -> 6.28-6.36
-// from 8 to 2.  bf16 -> fp8 is within 1% between 8, 4 and 2 and keeps 8.
-constexpr int kUQuantF32 = 2, kUQuantBf16 = 8, kUDeqF32 = 2, kUDeqBf16 = 1;
+// from 8 to 2.  bf16 -> fp8 issues 4: 6.17-6.22 -> 6.24-6.30 TB/s from 8
+// (at 2, 5.83-6.08).
+constexpr int kUQuantF32 = 2, kUQuantBf16 = 4, kUDeqF32 = 2, kUDeqBf16 = 1;
 
 // Stage 1 bodies: the block's maximum over its chunks (block bi of nb
 // blocks walking the chunks with a stride of nb).  |x| bit patterns, NaN
