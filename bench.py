@@ -159,7 +159,7 @@ def main():
         print(json.dumps({"conversion": conversion_bench(torch, df, synth, dev, cur())}))
         return
     if args.config3_only:
-        print(json.dumps({"config3": config3_bench(torch, df, synth, dev, cur())}))
+        print(json.dumps({"config3": config3_bench(torch, df, synth, dev, cur(), vendor=args.vendor_compare)}))
         return
 
     def to_bf16(a):
@@ -413,7 +413,7 @@ def main():
     if args.vendor_compare:
         out["vendor_compare"] = vendor_bench(torch, df, dev, cur())
     if not args.no_config3:
-        out["config3"] = config3_bench(torch, df, synth, dev, cur())
+        out["config3"] = config3_bench(torch, df, synth, dev, cur(), vendor=args.vendor_compare)
     if not args.no_producer:
         out["producer"] = producer_bench(torch, df, synth, dev, cur())
     if not args.no_optimizer:
@@ -1087,7 +1087,7 @@ def vendor_bench(torch, df, dev, stream, M=16384, reps=10):
     return res
 
 
-def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20):
+def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20, vendor=False):
     """Config 3: the four GPT-2 small Linears at 8192 tokens, forward only.
     Per Linear: absmax + e4m3 codes of X [M, K] and W [N, K] (bf16), then
     the fp8 GEMM with the fused scale, bf16 bias and bf16 output.  Reported:
@@ -1095,7 +1095,9 @@ def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20):
     with its quantization (weights per Linear, and all four in one
     df_quantize_2d_batch call), against the per-shape attainable bound
     min(5.0 PF, AI x 8 TB/s) (AI: fp8 A and B read once, bf16 C written
-    once)."""
+    once).  With vendor, each GEMM is also timed on torch._scaled_mm
+    (hipBLASLt) over the same codes, bias and output type, unit scales: a
+    comparison, not part of the product path."""
     import numpy as np
     from deepfuse_amd import DType, Fmt
     BF, E4 = int(DType.BFLOAT16), int(Fmt.E4M3)
@@ -1147,10 +1149,23 @@ def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20):
         res["linears"][l["name"]] = {"shape": [M, N, K], "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
                                      "attainable_tflops": round(bound / 1e12, 1),
                                      "frac_of_attainable": round(flops / (ms * 1e-3) / bound, 4)}
+        if vendor:
+            one = torch.ones(1, dtype=torch.float32, device=dev)
+            a8, b8 = l["Xq"].view(torch.float8_e4m3fn), l["Wq"].view(torch.float8_e4m3fn)
+            try:
+                vms = timed(lambda: torch._scaled_mm(a8, b8.t(), scale_a=one, scale_b=one, bias=l["b"],
+                                                     out_dtype=torch.bfloat16))
+                res["linears"][l["name"]]["vendor"] = {"ms": round(vms, 4),
+                                                       "tflops": round(flops / (vms * 1e-3) / 1e12, 1),
+                                                       "frac_of_attainable": round(flops / (vms * 1e-3) / bound, 4)}
+            except Exception as exc:  # the vendor path may refuse the bias or the format
+                res["linears"][l["name"]]["vendor"] = {"error": type(exc).__name__}
         tot_flops += flops
         tot_ms += ms
     res["gemm_only"] = {"ms": round(tot_ms, 4), "tflops": round(tot_flops / (tot_ms * 1e-3) / 1e12, 1),
                         "frac_of_fp8_peak": round(tot_flops / (tot_ms * 1e-3) / 5.0e15, 4)}
+    if vendor:
+        res["vendor"] = "torch._scaled_mm (hipBLASLt), bf16 output + bf16 bias, unit scales"
 
     def forward():
         for l in lin:
