@@ -532,6 +532,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     using G1 = EpiGeom<(int)sizeof(Out1)>;
     constexpr int SLAB = G0::SLAB > G1::SLAB ? G0::SLAB : G1::SLAB;
     // after an epilogue, a wait that leaves the smaller store count in flight
+    // (only where the wave's whole 128x64 quarter was in range: every store
+    // of an edge quarter sits behind a branch on its lanes' range, so such a
+    // wave may have issued fewer, down to none, and then waits for vmcnt(0))
     constexpr int NSTMIN = G0::NST < G1::NST ? G0::NST : G1::NST;
     constexpr int W_AFTER = NSTMIN > 63 ? 63 : NSTMIN;
     constexpr uint32_t kOOB = 0x80000000u;
@@ -733,7 +736,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     auto half = [&](auto zero, auto odd, v8i* fa, v8i* fb, v8i* na, v8i* nb) {
         __builtin_amdgcn_sched_barrier(0);
         if (decltype(odd)::value) {
-            if (after_epi)
+            if (after_epi == 1)
                 __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(W_AFTER));
             else
                 __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
@@ -787,7 +790,8 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
 
     // Stores one finished tile: scale, bias, conversion to T, the slab pass
     // and the 16-byte row-segment stores (tile: this block's unit index, for
-    // the bias slot).
+    // the bias slot).  Returns whether the wave's 128x64 quarter lay wholly
+    // inside the output, i.e. whether it issued all its stores.
     // always inlined: when both problems store the same type this lambda is
     // called from two places, and an outlined copy would take acc by
     // reference, i.e. through scratch memory
@@ -916,18 +920,20 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 asm volatile("" ::: "memory");
             }
         }
+        return rowb + 32 * FM <= Mo && colw + 64 <= No;
     };
 
     auto epilogue = [&](int tile) {
         int tp, tm0, tn0, tkb, tnku, tslot;
         tile_mn(tile, tp, tm0, tn0, tkb, tnku, tslot);
+        bool whole;
         if (GROUPED && tp)
-            store_tile(Tag<Out1>{}, std::false_type{}, static_cast<Out1*>(p1.C), p1.M, p1.N, p1.ldc, p1.vec_out,
-                       sab1, tile, tm0, tn0);
+            whole = store_tile(Tag<Out1>{}, std::false_type{}, static_cast<Out1*>(p1.C), p1.M, p1.N, p1.ldc,
+                               p1.vec_out, sab1, tile, tm0, tn0);
         else
-            store_tile(Tag<OutT>{}, std::integral_constant<bool, HAS_BIAS>{}, SPLIT ? C + (int64_t)tslot * M * N : C,
-                       M, N, ldc, vec_out, sab, tile, tm0, tn0);
-        after_epi = 1;
+            whole = store_tile(Tag<OutT>{}, std::integral_constant<bool, HAS_BIAS>{},
+                               SPLIT ? C + (int64_t)tslot * M * N : C, M, N, ldc, vec_out, sab, tile, tm0, tn0);
+        after_epi = whole ? 1 : 2;
     };
 
     // prologue: DMA steps 0 and 1, fragments of half-step 0
