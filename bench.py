@@ -701,7 +701,7 @@ def config3_summary(out_dir, prof):
     with open(path) as fh:
         tr = sorted(csv.DictReader(fh), key=lambda r: int(r["Start_Timestamp"]))
     reps = 20
-    gem = [r for r in tr if "gemm_nt_persistent_kernel" in r["Kernel_Name"] or "gemm_nt_dma128" in r["Kernel_Name"]
+    gem = [r for r in tr if "gemm_nt_persistent" in r["Kernel_Name"] or "gemm_nt_dma128" in r["Kernel_Name"]
            or "gemm_nt_kernel" in r["Kernel_Name"]]
     if len(gem) < 4 * (reps + 1):
         return False

@@ -322,6 +322,7 @@ class GemmKernel(enum.IntEnum):
     TILED_DMA_128 = 2
     TILED_REG_256 = 3
     TILED_REG_128 = 4
+    PERSISTENT_NARROW = 5
 
 
 def gemm_plan(M: int, N: int, K: int, lda: int, ldb: int, bias=None, ws_bytes: int = 0):

@@ -438,7 +438,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_nt_dma128_kernel(
 // of the grouped tile order; bl remaps the block id so that each XCD owns a
 // contiguous range of P/8 concurrent tiles (sharing A rows and B columns in
 // its L2).  8 waves, two per SIMD, each owning a 128x64 quarter-row of the
-// 256x256 tile as 4x2 v_mfma_f32_32x32x64_f8f6f4 tiles.
+// 256x256 tile as 4x2 v_mfma_f32_32x32x64_f8f6f4 tiles (narrow tiles:
+// 256x128, a 64x64 part per wave as 2x2 MFMA tiles).
 //
 // Pipeline: K advances in half-steps of 64 bytes (one MFMA depth).  A DMA
 // step moves 128 bytes of K (whole cache lines) for the tile's 256 A rows
@@ -492,15 +493,15 @@ __device__ __forceinline__ int fresh_lane() {
 }
 
 // Epilogue geometry for an output element of ES bytes: each 32-row block of
-// a wave's 128x64 quarter passes through an LDS slab of SR rows.
-template <int ES>
+// a wave's FMR*32 x 64 part passes through an LDS slab of SR rows.
+template <int ES, int FMR = 4>
 struct EpiGeom {
     static constexpr int SR = ES == 2 ? 16 : 8;          // slab rows
     static constexpr int SROW = 64 * ES + 16;            // padded slab row (bytes)
     static constexpr int SLAB = SR * SROW;
     static constexpr int NPASS = 32 / SR;                // slab passes per 32-row block
     static constexpr int SPP = SR * 64 * ES / 1024;      // 16-byte stores per lane per pass
-    static constexpr int NST = 4 * NPASS * SPP;          // epilogue stores per wave
+    static constexpr int NST = FMR * NPASS * SPP;        // epilogue stores per wave
 };
 
 // The second GEMM of a grouped launch (see gemm_sched.hpp): its operands,
@@ -520,16 +521,25 @@ constexpr int kUnitOverhead = 3;
 
 template <typename T> struct Tag { using type = T; };
 
-template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT = false, typename OutT1 = void>
-__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
+// NARROW: 256x128 tiles (one problem, unsplit).  The eight waves own 64x64
+// parts (4 x 2 waves, 2x2 MFMA tiles each); a DMA step moves the 256 A rows
+// and 128 B rows, so each wave issues two B instructions instead of four.
+// For outputs whose 256x256 tiles would leave CUs idle or a last round
+// mostly empty (the plan below compares both).
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT, typename OutT1, bool NARROW>
+__device__ __forceinline__ void persistent_body(
     const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
     const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
-    OutT* __restrict__ C, int ldc, int vec_out, int ksteps = 0, int nsplit = 1, PProb p1 = {}) {
+    OutT* __restrict__ C, int ldc, int vec_out, int ksteps, int nsplit, const PProb& p1) {
     constexpr bool GROUPED = !std::is_void<OutT1>::value;
+    static_assert(!NARROW || (!GROUPED && !SPLIT), "narrow tiles: one problem, unsplit");
     using Out1 = typename std::conditional<GROUPED, OutT1, OutT>::type;
-    constexpr int FM = 4, FN = 2;                 // 32x32 MFMA tiles per wave
-    using G0 = EpiGeom<(int)sizeof(OutT)>;
-    using G1 = EpiGeom<(int)sizeof(Out1)>;
+    constexpr int FM = NARROW ? 2 : 4, FN = 2;    // 32x32 MFMA tiles per wave
+    constexpr int BN = NARROW ? 128 : kPBN;       // tile columns
+    constexpr int WR = 32 * FM;                   // rows of a wave's part
+    constexpr int NDA = 4, NDB = NARROW ? 2 : 4;  // A and B DMA instructions per wave and step
+    using G0 = EpiGeom<(int)sizeof(OutT), FM>;
+    using G1 = EpiGeom<(int)sizeof(Out1), FM>;
     constexpr int SLAB = G0::SLAB > G1::SLAB ? G0::SLAB : G1::SLAB;
     // after an epilogue, a wait that leaves the smaller store count in flight
     // (only where the wave's whole 128x64 quarter was in range: every store
@@ -543,7 +553,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = w >> 2, wn = w & 3;
+    const int wm = NARROW ? w >> 1 : w >> 2, wn = NARROW ? w & 1 : w & 3;
     uint8_t* const slab = lds + 2 * kPStage + kPBiasSlots * kPBiasSlot + w * SLAB;
     // a 2-byte bias of odd length: its last element, which the dword bias DMA
     // cannot deliver (it shares a dword with the end of the buffer), read
@@ -551,7 +561,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     uint32_t bias_tail = 0;
     if (HAS_BIAS && sizeof(BiasT) == 2 && (N & 1))
         bias_tail = __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint16_t*>(bias)[N - 1]);
-    const int tiles_m = (M + kPBM - 1) / kPBM, tiles_n = (N + kPBN - 1) / kPBN;
+    const int tiles_m = (M + kPBM - 1) / kPBM, tiles_n = (N + BN - 1) / BN;
     const int ntiles = tiles_m * tiles_n;
     const int nk = (K + kPKB - 1) / kPKB;
     const int P = gridDim.x;
@@ -593,7 +603,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const int gsize = min(tm_ - first_m, kGroupM);
         const int in_group = lt - group * per_group;
         m0 = (first_m + in_group % gsize) * kPBM;
-        n0 = (in_group / gsize) * kPBN;
+        n0 = (in_group / gsize) * BN;
     };
     int S = 0;  // DMA steps of this block
     for (int r = 0; r < my_tiles; ++r) {
@@ -629,7 +639,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const int lda_ = q1 ? p1.lda : lda, ldb_ = q1 ? p1.ldb : ldb, K_ = q1 ? p1.K : K;
         const int kstep = d_kb + d_k;
         const int k0 = kstep * kPKB + dch0, k1 = kstep * kPKB + dch1;
-        const uint32_t ra = (uint32_t)(d_m0 + w * 32 + drow), rb = (uint32_t)(d_n0 + w * 32 + drow);
+        const uint32_t ra = (uint32_t)(d_m0 + w * 32 + drow), rb = (uint32_t)(d_n0 + w * 8 * NDB + drow);
         oa0 = (live && k0 < K_) ? ra * (uint32_t)lda_ + (uint32_t)k0 : kOOB;
         oa1 = (live && k1 < K_) ? (ra + 8u) * (uint32_t)lda_ + (uint32_t)k1 : kOOB;
         ob0 = (live && k0 < K_) ? rb * (uint32_t)ldb_ + (uint32_t)k0 : kOOB;
@@ -647,9 +657,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                 ra_, (__attribute__((address_space(3))) void*)(base + (w * 4 + d) * 1024), 16,
                 ((d & 1) ? oa1 : oa0) + (uint32_t)(d >> 1) * a16, 0, 0, 0);
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < NDB; ++d)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rb_, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
+                rb_, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * NDB + d) * 1024), 16,
                 ((d & 1) ? ob1 : ob0) + (uint32_t)(d >> 1) * b16, 0, 0, 0);
         if (HAS_BIAS)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -658,20 +668,21 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
                                                           w * 256),
                 4, obias, 0, 0, 0);
     };
-    // instruction k (0..8) of dissue(): A rows (4), B rows (4), bias
+    // instruction k (0..NDA+NDB) of dissue(): A rows (4), B rows (NDB), bias
     auto dissue_one = [&](int k) __attribute__((always_inline)) {
         uint8_t* base = lds + ((uint32_t)d_g & 1u) * kPStage;
         const bool q1 = GROUPED && d_p;
-        if (k < 4) {
+        if (k < NDA) {
             const uint32_t a16 = 16u * (uint32_t)(q1 ? p1.lda : lda);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 q1 ? rA1 : rA, (__attribute__((address_space(3))) void*)(base + (w * 4 + k) * 1024), 16,
                 ((k & 1) ? oa1 : oa0) + (uint32_t)(k >> 1) * a16, 0, 0, 0);
-        } else if (k < 8) {
-            const int d = k - 4;
+        } else if (k < NDA + NDB) {
+            const int d = k - NDA;
             const uint32_t b16 = 16u * (uint32_t)(q1 ? p1.ldb : ldb);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                q1 ? rB1 : rB, (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * 4 + d) * 1024), 16,
+                q1 ? rB1 : rB,
+                (__attribute__((address_space(3))) void*)(base + kPBM * kPKB + (w * NDB + d) * 1024), 16,
                 ((d & 1) ? ob1 : ob0) + (uint32_t)(d >> 1) * b16, 0, 0, 0);
         } else if (HAS_BIAS && d_k == 0) {  // a tile's bias, once, with its first step
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -747,9 +758,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         const uint8_t* sA = lds + (((uint32_t)nxt >> 1) & 1u) * kPStage;
         const uint8_t* sB = sA + kPBM * kPKB;
         const int e = nxt & 1;
-        u32x4 part[12];  // read r: fragment r/2 (A0-A3, B0, B1), 16-byte half r%2
+        constexpr int NR = 2 * (FM + FN);  // 16-byte fragment reads per half-step
+        u32x4 part[NR];  // read r: fragment r/2 (A0..A(FM-1), B0, B1), 16-byte half r%2
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
+        for (int x = 0; x < FM * FN; ++x) {
             const int i = x >> 1, j = x & 1;
             if (decltype(zero)::value) {
                 const v16f z = {};
@@ -760,14 +772,18 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
             }
             if (x < 4) {
 #pragma unroll
-                for (int r = 3 * x; r < 3 * x + 3; ++r) {
+                for (int r = (NR / 4) * x; r < (NR / 4) * (x + 1); ++r) {
                     const int f = r >> 1, h = r & 1;
-                    const uint8_t* p = f < 4 ? sA + (wm * 128 + f * 32) * kPKB : sB + (wn * 64 + (f - 4) * 32) * kPKB;
+                    const uint8_t* p =
+                        f < FM ? sA + (wm * WR + f * 32) * kPKB : sB + (wn * 64 + (f - FM) * 32) * kPKB;
                     part[r] = *reinterpret_cast<const u32x4*>(p + foff[e][h]);
                 }
             }
             if (decltype(odd)::value) {
-                if (x == 0) {
+                if (NARROW) {  // seven instructions over four MFMAs: 2, 2, 2, 1
+                    dissue_one(2 * x);
+                    if (2 * x + 1 <= NDA + NDB) dissue_one(2 * x + 1);
+                } else if (x == 0) {
                     dissue_one(0);
                     dissue_one(1);
                 } else {
@@ -777,12 +793,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int f = 0; f < 6; ++f) {
+        for (int f = 0; f < FM + FN; ++f) {
             const u32x4 lo = part[2 * f], hi = part[2 * f + 1];
             v8i r;
             r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
             r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
-            if (f < 4) na[f] = r; else nb[f - 4] = r;
+            if (f < FM) na[f] = r; else nb[f - FM] = r;
         }
         ++c_h;
         if (decltype(odd)::value) dadvance();
@@ -804,7 +820,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         constexpr int SR = EpiGeom<ES>::SR, SROW = EpiGeom<ES>::SROW;
         constexpr int NPASS = EpiGeom<ES>::NPASS, SPP = EpiGeom<ES>::SPP;
         const int el = fresh_lane(), efr = el & 31;
-        const int rowb = tm0 + wm * 128;
+        const int rowb = tm0 + wm * WR;
         const int colw = tn0 + wn * 64;
         const int h4 = (el >> 5) * 4;
         const uint8_t* bsl = lbias + ((uint32_t)tile % kPBiasSlots) * kPBiasSlot;
@@ -941,10 +957,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         dissue();
         dadvance();
     }
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(HAS_BIAS ? 9 : 8));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(NDA + NDB + (HAS_BIAS ? 1 : 0)));
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa0[i] = rd(lds + (wm * 128 + i * 32) * kPKB, 0);
+    for (int i = 0; i < FM; ++i) fa0[i] = rd(lds + (wm * WR + i * 32) * kPKB, 0);
 #pragma unroll
     for (int j = 0; j < FN; ++j) fb0[j] = rd(lds + kPBM * kPKB + (wn * 64 + j * 32) * kPKB, 0);
 
@@ -966,6 +982,24 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
         epilogue(tile);
     }
     __builtin_amdgcn_s_waitcnt(0);  // every DMA has landed before the block's LDS is released
+}
+
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT = false, typename OutT1 = void>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
+    const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
+    const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
+    OutT* __restrict__ C, int ldc, int vec_out, int ksteps = 0, int nsplit = 1, PProb p1 = {}) {
+    persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, SPLIT, OutT1, false>(A, lda, B, ldb, M, N, K, sa, sb, bias, C,
+                                                                        ldc, vec_out, ksteps, nsplit, p1);
+}
+
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_narrow_kernel(
+    const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
+    const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
+    OutT* __restrict__ C, int ldc, int vec_out) {
+    persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, false, void, true>(A, lda, B, ldb, M, N, K, sa, sb, bias, C, ldc,
+                                                                      vec_out, 0, 1, PProb{});
 }
 
 // out[m,n] = (sum_s P[s][m][n]) * sa * sb + bias[n], slices in order; four
@@ -1124,6 +1158,7 @@ static bool persistent_ok(const GemmArgs& g) {
 // panels at unrelated K offsets and L2 reuse was lost.)
 struct PSplit {
     int S, L;
+    double cost;  // rounds cost model, in K steps of a 256x256 tile
 };
 
 static PSplit persistent_split_plan(int M, int N, int K, size_t ws_bytes, int cus) {
@@ -1131,8 +1166,8 @@ static PSplit persistent_split_plan(int M, int N, int K, size_t ws_bytes, int cu
     const double red_steps_per_byte = 2.0 / 10e6;
     const int nk = (K + kPKB - 1) / kPKB;
     const int64_t tiles = (int64_t)((M + kPBM - 1) / kPBM) * ((N + kPBN - 1) / kPBN);
-    PSplit best{1, nk};
-    double best_cost = (double)((tiles + cus - 1) / cus) * (nk + kOverheadSteps);
+    PSplit best{1, nk, (double)((tiles + cus - 1) / cus) * (nk + kOverheadSteps)};
+    double best_cost = best.cost;
     for (int s = 2; s <= 8; ++s) {
         const int span = (nk + s - 1) / s;
         if (span < 4) break;
@@ -1143,7 +1178,7 @@ static PSplit persistent_split_plan(int M, int N, int K, size_t ws_bytes, int cu
             rounds * (span + kOverheadSteps) + (double)(se + 1) * M * N * sizeof(float) * red_steps_per_byte;
         if (cost < best_cost * 0.97) {
             best_cost = cost;
-            best = PSplit{se, span};
+            best = PSplit{se, span, cost};
         }
     }
     return best;
@@ -1161,9 +1196,33 @@ static void launch_persistent(const GemmArgs& g, int grid) {
             g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, static_cast<OutT*>(g.C), g.ldc, vec_out);
 }
 
+template <int FA, int FB, typename OutT, typename BiasT>
+static void launch_persistent_narrow(const GemmArgs& g, int grid) {
+    const int vec_out = epi_store_mode(g.C, (int64_t)g.ldc * (int64_t)sizeof(OutT));
+    if (g.bias)
+        gemm_nt_persistent_narrow_kernel<FA, FB, OutT, BiasT, true><<<grid, 512, 0, g.st>>>(
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, static_cast<const BiasT*>(g.bias),
+            static_cast<OutT*>(g.C), g.ldc, vec_out);
+    else
+        gemm_nt_persistent_narrow_kernel<FA, FB, OutT, BiasT, false><<<grid, 512, 0, g.st>>>(
+            g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, nullptr, static_cast<OutT*>(g.C), g.ldc, vec_out);
+}
+
+// Narrow (256x128) tiles in the rounds cost model: a K step costs
+// kNarrowStep of a 256x256 step, a tile kNarrowOverhead steps beyond them.
+// Measured (bf16 output, 20 launches each): where both tilings run one
+// round, narrow tiles took 0.75-0.77 of the time (GPT-2 small attn/mlp
+// projections at 8192 tokens: about 0.74 per step and 2.5 per tile).  The
+// smaller constants here also send the GPT-2 small c_attn and c_fc shapes,
+// whose 256x256 plans end in a partly empty round, to narrow tiles (0-4%
+// faster there), while the GPT-2 XL shapes at 16384 tokens keep 256x256
+// tiles (narrow ones 13-40% slower).
+constexpr double kNarrowStep = 0.6, kNarrowOverhead = 2.0;
+
 // The kernel one NT GEMM call runs (df_fp8_gemm_nt_plan reports it): the
 // persistent kernel when its offsets fit (split into K-slice units when the
-// output has fewer tiles than CUs and a workspace allows it), otherwise the
+// output has fewer tiles than CUs and a workspace allows it; its 256x128
+// tiles when the rounds cost model puts them 3% below), otherwise the
 // tiled kernels -- LDS-DMA when both operands fit a 32-bit buffer range,
 // register-staged beyond -- with 256x256 or 128x128 blocks and split-K from
 // plan_gemm.  Every launch below follows this plan.
@@ -1178,11 +1237,24 @@ static NtPlan nt_plan(const GemmArgs& g) {
     const int cus = device_cu_count();
     const size_t ws = g.ws ? g.ws_bytes : 0;
     if (cus > 0 && persistent_ok(g)) {
-        const int64_t tiles = (int64_t)((g.M + kPBM - 1) / kPBM) * ((g.N + kPBN - 1) / kPBN);
-        if (tiles >= cus) return NtPlan{DF_GEMM_KERNEL_PERSISTENT, 1, 0, cus};
-        const PSplit ps = persistent_split_plan(g.M, g.N, g.K, ws, cus);
-        if (ps.S == 1) return NtPlan{DF_GEMM_KERNEL_PERSISTENT, 1, 0, (int)tiles};
-        return NtPlan{DF_GEMM_KERNEL_PERSISTENT, ps.S, ps.L, (int)std::min<int64_t>(tiles * ps.S, cus)};
+        const int tm = (g.M + kPBM - 1) / kPBM, nk = (g.K + kPKB - 1) / kPKB;
+        const int64_t tiles = (int64_t)tm * ((g.N + kPBN - 1) / kPBN);
+        const int64_t tiles_nw = (int64_t)tm * ((g.N + 127) / 128);
+        NtPlan wide;
+        double wcost;
+        if (tiles >= cus) {
+            wide = NtPlan{DF_GEMM_KERNEL_PERSISTENT, 1, 0, cus};
+            wcost = (double)((tiles + cus - 1) / cus) * (nk + 3.0);
+        } else {
+            const PSplit ps = persistent_split_plan(g.M, g.N, g.K, ws, cus);
+            wide = ps.S == 1 ? NtPlan{DF_GEMM_KERNEL_PERSISTENT, 1, 0, (int)tiles}
+                             : NtPlan{DF_GEMM_KERNEL_PERSISTENT, ps.S, ps.L, (int)std::min<int64_t>(tiles * ps.S, cus)};
+            wcost = ps.cost;
+        }
+        const double ncost = (double)((tiles_nw + cus - 1) / cus) * (nk * kNarrowStep + kNarrowOverhead);
+        if (ncost < wcost * 0.97)
+            return NtPlan{DF_GEMM_KERNEL_PERSISTENT_NARROW, 1, 0, (int)std::min<int64_t>(tiles_nw, cus)};
+        return wide;
     }
     const GemmPlan gp = plan_gemm(g.M, g.N, g.K, ws);
     const bool dma_ok = (int64_t)g.M * g.lda < (1ll << 31) && (int64_t)g.N * g.ldb < (1ll << 31);
@@ -1200,6 +1272,10 @@ static NtPlan nt_plan(const GemmArgs& g) {
 template <int FA, int FB, typename OutT, typename BiasT>
 static void launch_shape(const GemmArgs& g) {
     const NtPlan p = nt_plan(g);
+    if (p.kind == DF_GEMM_KERNEL_PERSISTENT_NARROW) {
+        launch_persistent_narrow<FA, FB, OutT, BiasT>(g, p.grid);
+        return;
+    }
     if (p.kind == DF_GEMM_KERNEL_PERSISTENT) {
         if (p.split == 1) {
             launch_persistent<FA, FB, OutT, BiasT>(g, p.grid);

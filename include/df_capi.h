@@ -298,7 +298,9 @@ int df_fp8_gemm_nt(int fmt_a, const uint8_t* A, int lda,
  * DF_GEMM_KERNEL_*, *split the K slices (1 = unsplit).  The persistent
  * kernel takes every call whose operands fit its 32-bit buffer offsets
  * (M*lda and N*ldb below 2^31, lda and ldb below 2^23) and whose bias is
- * 4-byte aligned; the tiled kernels take the rest, with LDS-DMA operand
+ * 4-byte aligned, with 256x256 tiles or, where its rounds cost model
+ * prefers them, 256x128 tiles (PERSISTENT_NARROW); the tiled kernels take
+ * the rest, with LDS-DMA operand
  * loads while M*lda and N*ldb stay below 2^31 and register-staged loads
  * beyond.  Same plan as the reference-facing calls below; no reference
  * counterpart (the reference has one kernel per GEMM). */
@@ -307,7 +309,8 @@ enum {
     DF_GEMM_KERNEL_TILED_DMA_256 = 1,
     DF_GEMM_KERNEL_TILED_DMA_128 = 2,
     DF_GEMM_KERNEL_TILED_REG_256 = 3,
-    DF_GEMM_KERNEL_TILED_REG_128 = 4
+    DF_GEMM_KERNEL_TILED_REG_128 = 4,
+    DF_GEMM_KERNEL_PERSISTENT_NARROW = 5
 };
 int df_fp8_gemm_nt_plan(int M, int N, int K, int lda, int ldb, const void* bias, size_t ws_bytes,
                         int* kernel, int* split);

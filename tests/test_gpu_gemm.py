@@ -197,6 +197,9 @@ def test_config3_forward_bf16(dev, K, N):
     _, sw = df.absmax_scale(Wd, Fmt.E4M3)
     xq, _ = df.quantize_2d(Xd, sx, Fmt.E4M3)
     wq, _ = df.quantize_2d(Wd, sw, Fmt.E4M3)
+    # at these shapes the plan takes the persistent kernel's 256x128 tiles
+    wsb = int(df.lib().df_fp8_gemm_workspace_bytes(M, N, K))
+    assert df.gemm_plan(M, N, K, xq.stride(0), wq.stride(0), bd, wsb)[0] == df.GemmKernel.PERSISTENT_NARROW
     Y32 = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd)
     Y16 = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=bd, out_dtype=torch.bfloat16)
     check_bf16_image(Y32, Y16)
@@ -211,6 +214,35 @@ def test_config3_forward_bf16(dev, K, N):
     ref = orc.fc_forward(orc.dequantize(cx, s_x, 0), orc.dequantize(cw, s_w, 0), orc.bf16_to_f32(bb))
     err = orc.rel_err(Y32.cpu().numpy()[idx], ref)
     assert err <= TOL, f"config3 {K}->{N}: {err:.3e}"
+
+
+# (M, N, K) whose plan takes the persistent kernel's 256x128 tiles, with
+# ragged edges: rows and columns ending inside a wave's 64x64 part, an
+# odd-length bf16 bias, outputs whose row pitch is not 16-byte aligned.
+NARROW_CASES = [(1000, 999, 640), (1000, 1000, 768), (300, 130, 1024), (2048, 640, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", NARROW_CASES)
+def test_narrow_tiles_match_oracle(dev, M, N, K):
+    """256x128 tiles (fully_connected_layer.cu:14-35 restated by the
+    oracle): fp32 output on every row against the oracle, bf16 output as
+    its RNE image, bf16 bias."""
+    seed = synth.SEED_BASE + 700 + M + N + K
+    A = synth.normal((M, K), 1.0, seed=seed)
+    B = synth.normal((N, K), 0.02, seed=seed + 1)
+    bb = synth.f32_to_bf16_bits(synth.normal((N,), 0.1, seed=seed + 2))
+    aq, _, sa, Ad = quant_operand(A, Fmt.E4M3, dev)
+    bq, _, sb, Bd = quant_operand(B, Fmt.E4M3, dev)
+    bd = torch.from_numpy(bb.view(np.int16)).to(dev).view(torch.bfloat16)
+    for ws_bytes in (0, int(df.lib().df_fp8_gemm_workspace_bytes(M, N, K))):
+        kind = df.gemm_plan(M, N, K, aq.stride(0), bq.stride(0), bd, ws_bytes)[0]
+        assert kind == df.GemmKernel.PERSISTENT_NARROW, f"plan {kind!r} (workspace {ws_bytes})"
+    Y = df.gemm_nt(aq, Fmt.E4M3, bq, Fmt.E4M3, K, sa, sb, bias=bd)
+    Y16 = df.gemm_nt(aq, Fmt.E4M3, bq, Fmt.E4M3, K, sa, sb, bias=bd, out_dtype=torch.bfloat16)
+    check_bf16_image(Y, Y16)
+    ref = orc.fc_forward(Ad, Bd, orc.bf16_to_f32(bb))
+    err = orc.rel_err(Y.cpu().numpy(), ref)
+    assert err <= TOL, f"narrow M={M} N={N} K={K}: rel err {err:.3e}"
 
 
 @pytest.mark.parametrize("K,N", GPT2_XL)
