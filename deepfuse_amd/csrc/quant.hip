@@ -475,6 +475,8 @@ __global__ __launch_bounds__(kThreads) void dequantize_bf16_kernel(const uint8_t
 // partial sum per column (rows in fixed order), written to
 // colpart[tile_row][col] for a deterministic second pass.
 constexpr int kT2 = 128;
+// rows of a quantize_2d_kernel tile (quantize_2d_batch_kernel keeps kT2)
+constexpr int kT2R = 128;
 
 template <typename InT> struct Ld;
 template <> struct Ld<float> {
@@ -588,7 +590,8 @@ __device__ __forceinline__ float ln_apply(float x, float mean, float rstd, bool 
 // absmax see.
 // The tile pass proper, instantiated for both division forms (FAST: see
 // qdiv_t); the kernel below owns the LDS and picks the form once per block.
-template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bool FAST, bool NT = AMAX && !LN>
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bool FAST, bool NT = AMAX && !LN,
+          int TR = kT2>
 __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, int cols, int ldx, bool vec_ok,
                                          const QDiv& d, uint8_t* __restrict__ q, int ldq, uint8_t* __restrict__ qt,
                                          int ldqt, float* __restrict__ colpart, uint32_t* __restrict__ amaxpart,
@@ -597,9 +600,10 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     constexpr int E = Ld<InT>::E;      // elements per 16-byte load
     constexpr int TPR = kT2 / E;       // threads per tile row
     constexpr int RG = kThreads / TPR; // row groups
-    constexpr int RPT = kT2 / RG;      // rows per thread (8 for bf16, 16 for fp32)
-    constexpr int TSTRIDE = kT2 + 16;  // LDS tile row (bytes), [column][row]
-    const int r0 = by * kT2, c0 = bx * kT2;  // tile (bx, by) of a grid nbx tiles wide
+    constexpr int RPT = TR / RG;       // rows per thread (8 for bf16, 16 for fp32 at TR = 128)
+    static_assert(RPT % 4 == 0 && RPT <= 32, "4x4 byte transposes");
+    constexpr int TSTRIDE = TR + 16;   // LDS tile row (bytes), [column][row]
+    const int r0 = by * TR, c0 = bx * kT2;  // tile (bx, by) of a grid nbx tiles wide
     const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
     const int c = c0 + tc;
     const bool full = vec_ok && c + E <= cols;
@@ -608,7 +612,7 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     // aligned), so no line is assembled from several non-temporal partial
     // writes; other layouts take plain stores.
     const bool q_lines = ((reinterpret_cast<uintptr_t>(q) | (uint32_t)ldq) & 127u) == 0;
-    const bool qt_lines = ((reinterpret_cast<uintptr_t>(qt) | (uint32_t)ldqt) & 127u) == 0;
+    const bool qt_lines = TR % 128 == 0 && ((reinterpret_cast<uintptr_t>(qt) | (uint32_t)ldqt) & 127u) == 0;
     uint32_t codes[RPT][E / 4];
     float cs[E];
     uint32_t am = 0;
@@ -676,7 +680,7 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
             }
         }
     };
-    if (full && r0 + kT2 <= rows) {
+    if (full && r0 + TR <= rows) {
         // every row of this thread is in range and 16-byte loadable: issue
         // all RPT loads before using any, so they are in flight together
         u32x4 raw[RPT];
@@ -723,11 +727,17 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
         for (int e = 0; e < E; ++e) {
             const uint32_t* w = wcol[e];
             uint8_t* dst = tile + (tc + e) * TSTRIDE + rg * RPT;
-            if (RPT == 16)
-                *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[RPT / 4 > 1 ? 1 : 0], w[RPT / 4 > 2 ? 2 : 0],
-                                                       w[RPT / 4 > 3 ? 3 : 0]};
-            else
+            if (RPT >= 16) {
+#pragma unroll
+                for (int h = 0; h < RPT / 16; ++h)
+                    *reinterpret_cast<u32x4*>(dst + 16 * h) =
+                        u32x4{w[4 * h], w[4 * h + 1 < RPT / 4 ? 4 * h + 1 : 0], w[4 * h + 2 < RPT / 4 ? 4 * h + 2 : 0],
+                              w[4 * h + 3 < RPT / 4 ? 4 * h + 3 : 0]};
+            } else if (RPT == 8) {
                 *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[RPT / 4 > 1 ? 1 : 0]};
+            } else {
+                *reinterpret_cast<uint32_t*>(dst) = w[0];
+            }
         }
     }
     if (COLSUM) {
@@ -736,10 +746,11 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     }
     __syncthreads();
     if (CODES && qt) {
+        constexpr int CPC = TR / 16;  // 16-byte chunks per column
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kT2 * CPC / kThreads; ++k) {
             const int idx = threadIdx.x + kThreads * k;
-            const int col = idx >> 3, rc = (idx & 7) * 16;
+            const int col = idx / CPC, rc = (idx % CPC) * 16;
             if (c0 + col < cols && r0 + rc < ldqt) {
                 u32x4* dst = reinterpret_cast<u32x4*>(qt + (int64_t)(c0 + col) * ldqt + r0 + rc);
                 const u32x4 v = *reinterpret_cast<const u32x4*>(tile + col * TSTRIDE + rc);
@@ -926,16 +937,17 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
                                                                 uint32_t* __restrict__ amaxpart = nullptr,
                                                                 LnArgs ln = LnArgs()) {
     constexpr int RG = kThreads / (kT2 / Ld<InT>::E);
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2 + 16)];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2R + 16)];
     __shared__ float csum[COLSUM ? RG : 1][kT2];
     const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
     if (!CODES || d.fast)
-        q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, true>(x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart,
-                                                          amaxpart, ln, tile, csum, blockIdx.x, blockIdx.y, gridDim.x);
+        q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, true, AMAX && !LN, kT2R>(
+            x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart, amaxpart, ln, tile, csum, blockIdx.x,
+            blockIdx.y, gridDim.x);
     else
-        q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, false>(x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart,
-                                                           amaxpart, ln, tile, csum, blockIdx.x, blockIdx.y,
-                                                           gridDim.x);
+        q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, false, AMAX && !LN, kT2R>(
+            x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart, amaxpart, ln, tile, csum, blockIdx.x,
+            blockIdx.y, gridDim.x);
 }
 
 // ---- several 2-D tensors in three launches (every Linear's weights after
@@ -1337,14 +1349,15 @@ extern "C" int df_dequantize_e5m2_bf16(const uint8_t* q, int64_t n, const float*
 
 extern "C" size_t df_quantize_2d_workspace_bytes(int rows, int cols) {
     if (rows <= 0 || cols <= 0) return 0;
-    return (size_t)((rows + kT2 - 1) / kT2) * (size_t)cols * sizeof(float);
+    return (size_t)((rows + kT2R - 1) / kT2R) * (size_t)cols * sizeof(float);
 }
 
-// Tile grid of a 2-D quantize: covers the codes' padded extents.
-static dim3 q2d_grid(int rows, int cols, const uint8_t* q, int ldq, const uint8_t* qt, int ldqt) {
+// Tile grid of a 2-D quantize (tiles of tr rows and kT2 columns): covers the
+// codes' padded extents.
+static dim3 q2d_grid(int rows, int cols, const uint8_t* q, int ldq, const uint8_t* qt, int ldqt, int tr) {
     const int row_ext = qt ? (rows > ldqt ? rows : ldqt) : rows;
     const int col_ext = q ? (cols > ldq ? cols : ldq) : cols;
-    return dim3((col_ext + kT2 - 1) / kT2, (row_ext + kT2 - 1) / kT2);
+    return dim3((col_ext + kT2 - 1) / kT2, (row_ext + tr - 1) / tr);
 }
 
 // Delayed-scaling workspace: column-sum partials (when asked for), then one
@@ -1352,7 +1365,7 @@ static dim3 q2d_grid(int rows, int cols, const uint8_t* q, int ldq, const uint8_
 static size_t delayed_ws_layout(int rows, int cols, int ldq, int ldqt, bool colsum, size_t* amax_off) {
     const size_t cs = colsum ? df_quantize_2d_workspace_bytes(rows, cols) : 0;
     const size_t off = (cs + 15) & ~(size_t)15;
-    const dim3 g = q2d_grid(rows, cols, (const uint8_t*)1, ldq, ldqt > 0 ? (const uint8_t*)1 : nullptr, ldqt);
+    const dim3 g = q2d_grid(rows, cols, (const uint8_t*)1, ldq, ldqt > 0 ? (const uint8_t*)1 : nullptr, ldqt, kT2R);
     if (amax_off) *amax_off = off;
     return off + (size_t)g.x * g.y * sizeof(uint32_t);
 }
@@ -1393,7 +1406,7 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
         DF_CHECK(ws_bytes >= df_quantize_2d_workspace_bytes(rows, cols), DF_ERR_WORKSPACE,
                  "%s: workspace %zu bytes < %zu", name, ws_bytes, df_quantize_2d_workspace_bytes(rows, cols));
     }
-    const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt);
+    const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt, kT2R);
     hipStream_t st = as_stream(stream);
     if (grid.x == 0 || grid.y == 0) {
         if (colsum && cols > 0) {
@@ -1442,7 +1455,7 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
     }
 #undef DF_Q2D
     if (colsum)
-        colsum_reduce_kernel<<<(cols + 63) / 64, kThreads, 0, st>>>(part, rows == 0 ? 0 : (rows + kT2 - 1) / kT2,
+        colsum_reduce_kernel<<<(cols + 63) / 64, kThreads, 0, st>>>(part, rows == 0 ? 0 : (rows + kT2R - 1) / kT2R,
                                                                     cols, colsum);
     if (delayed)
         amax_history_kernel<<<1, kThreads, 0, st>>>(amaxpart, (int)(grid.x * grid.y), fmt, history, hist_len,
@@ -1590,7 +1603,7 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
                  "%s: tensor %d: q needs ldq >= cols, a multiple of 16, and 16-byte alignment", name, t);
         DF_CHECK(!qqt || (ldqt && ldqt[t] >= rows[t] && ldqt[t] % 16 == 0 && aligned16(qqt)), DF_ERR_ALIGN,
                  "%s: tensor %d: qt needs ldqt >= rows, a multiple of 16, and 16-byte alignment", name, t);
-        DF_CHECK(q2d_grid(rows[t], cols[t], qq, qq ? ldq[t] : 0, qqt, qqt ? ldqt[t] : 0).y <= 65535, DF_ERR_INVALID,
+        DF_CHECK(q2d_grid(rows[t], cols[t], qq, qq ? ldq[t] : 0, qqt, qqt ? ldqt[t] : 0, kT2).y <= 65535, DF_ERR_INVALID,
                  "%s: tensor %d: rows=%d too large", name, t, rows[t]);
     }
     hipStream_t st = as_stream(stream);
@@ -1619,7 +1632,7 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
             const int share = total > 0 ? (int)((double)budget * (double)n / (double)total) : 0;
             B.blk_first[i] = bf;
             bf += 1 + std::max(0, std::min(want - 1, share));
-            const dim3 g = q2d_grid(rows[t], cols[t], B.q[i], B.ldq[i], B.qt[i], B.ldqt[i]);
+            const dim3 g = q2d_grid(rows[t], cols[t], B.q[i], B.ldq[i], B.qt[i], B.ldqt[i], kT2);
             B.tile_first[i] = tf;
             B.tiles_x[i] = g.x > 0 ? (int)g.x : 1;
             tf += (int)(g.x * g.y);
@@ -1678,7 +1691,7 @@ extern "C" int df_quantize_2d_batch_absmax(int in_dtype, int count, const void* 
 static size_t ln_ws_layout(int rows, int cols, int ldq, int ldqt, size_t* part_off) {
     const size_t st = ((size_t)rows * sizeof(float2) + 15) & ~(size_t)15;
     const size_t stat_parts = (size_t)((rows + 3) / 4);
-    const dim3 g = q2d_grid(rows, cols, (const uint8_t*)1, ldq, ldqt > 0 ? (const uint8_t*)1 : nullptr, ldqt);
+    const dim3 g = q2d_grid(rows, cols, (const uint8_t*)1, ldq, ldqt > 0 ? (const uint8_t*)1 : nullptr, ldqt, kT2R);
     const size_t tile_parts = (size_t)g.x * g.y;
     if (part_off) *part_off = st;
     return st + (stat_parts > tile_parts ? stat_parts : tile_parts) * sizeof(uint32_t) + 16;
@@ -1777,7 +1790,7 @@ static int layernorm_impl(const char* name, int mode, int dtype, const void* x, 
     la.y = y;
     la.ldy = ldy;
     la.y_vec = y && aligned16(y) && ((int64_t)ldy * esz) % 16 == 0;
-    const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt);
+    const dim3 grid = q2d_grid(rows, cols, q, ldq, qt, ldqt, kT2R);
     DF_CHECK(grid.y <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
 #define DF_LNT(T, F, CODES, AMAX)                                                                              \
     quantize_2d_kernel<T, F, false, CODES, AMAX, true><<<grid, kThreads, 0, st>>>(                             \
