@@ -1200,6 +1200,35 @@ def config3_bench(torch, df, synth, dev, stream, M=8192, reps=20, vendor=False):
     ms = timed(forward_batched)
     res["forward_with_quantize_weights_batched"] = {"ms": round(ms, 4),
                                                     "tflops": round(tot_flops / (ms * 1e-3) / 1e12, 1)}
+
+    # the same forward with X at delayed scaling (df_quantize_2d_delayed: the
+    # scale from a 16-entry amax history, the absmax measured in the same
+    # pass; two scale slots alternate), the weights batched just-in-time
+    H = 16
+    dws_b = max(df.lib().df_quantize_2d_delayed_workspace_bytes(M, l["K"], l["K"], 0, 0) for l in lin)
+    dws = torch.empty(max(dws_b, 16), dtype=torch.uint8, device=dev)
+    for l in lin:
+        l["hist"] = torch.empty(H, dtype=torch.float32, device=dev)
+        l["dsc"] = torch.empty(3, dtype=torch.float32, device=dev)
+        d = l["dsc"].data_ptr()
+        df.call("df_absmax_bf16", l["X"].data_ptr(), l["X"].numel(), d + 8, aws.data_ptr(), aws.numel(), stream)
+        df.call("df_amax_history_init", d + 8, E4, l["hist"].data_ptr(), H, d, stream)
+
+    def forward_delayed(parity):
+        df.call("df_quantize_2d_batch", BF, nl, *wargs, stream)
+        for i, l in enumerate(lin):
+            d = l["dsc"].data_ptr()
+            used, nxt = d + 4 * parity, d + 4 * (parity ^ 1)
+            df.call("df_quantize_2d_delayed", BF, l["X"].data_ptr(), M, l["K"], l["K"], E4, used, nxt,
+                    l["hist"].data_ptr(), H, l["Xq"].data_ptr(), l["K"], None, 0, None, dws.data_ptr(), dws.numel(),
+                    stream)
+            df.call("df_fp8_gemm_fwd", l["Xq"].data_ptr(), l["K"], l["Wq"].data_ptr(), l["K"], M, l["N"], l["K"],
+                    used, wsc.data_ptr() + 4 * i, BF, l["b"].data_ptr(), BF, l["Y"].data_ptr(), l["N"],
+                    gws.data_ptr(), gws.numel(), stream)
+
+    ms = timed(lambda: (forward_delayed(0), forward_delayed(1))) / 2
+    res["forward_with_quantize_delayed"] = {"ms": round(ms, 4), "tflops": round(tot_flops / (ms * 1e-3) / 1e12, 1),
+                                            "history": H, "weights": "batched, just-in-time"}
     return res
 
 
