@@ -542,9 +542,10 @@ __device__ __forceinline__ void persistent_body(
     using G1 = EpiGeom<(int)sizeof(Out1), FM>;
     constexpr int SLAB = G0::SLAB > G1::SLAB ? G0::SLAB : G1::SLAB;
     // after an epilogue, a wait that leaves the smaller store count in flight
-    // (only where the wave's whole 128x64 quarter was in range: every store
-    // of an edge quarter sits behind a branch on its lanes' range, so such a
-    // wave may have issued fewer, down to none, and then waits for vmcnt(0))
+    // (only where the wave's whole part -- 128x64, or 64x64 in narrow tiles
+    // -- was in range: every store of an edge part sits behind a branch on
+    // its lanes' range, so such a wave may have issued fewer, down to none,
+    // and then waits for vmcnt(0))
     constexpr int NSTMIN = G0::NST < G1::NST ? G0::NST : G1::NST;
     constexpr int W_AFTER = NSTMIN > 63 ? 63 : NSTMIN;
     constexpr uint32_t kOOB = 0x80000000u;
@@ -738,7 +739,9 @@ __device__ __forceinline__ void persistent_body(
     // Issue order, frozen by scheduling barriers: MFMA x (row block x/2,
     // column block x%2), then, for x < 4, three of the twelve fragment
     // reads, then (odd half-steps) this MFMA's share of the nine DMA
-    // instructions -- two after MFMA 0, one after each later one.  The reads
+    // instructions -- two after MFMA 0, one after each later one (narrow
+    // tiles: four MFMAs, two of the eight reads and two, two, two and one
+    // of the seven DMA instructions under each).  The reads
     // all sit under the first four MFMAs, so they have landed by the end of
     // the half-step and the wait before the next barrier costs nothing; the
     // DMA is spread over the whole half-step instead of leaving as one burst
@@ -806,8 +809,8 @@ __device__ __forceinline__ void persistent_body(
 
     // Stores one finished tile: scale, bias, conversion to T, the slab pass
     // and the 16-byte row-segment stores (tile: this block's unit index, for
-    // the bias slot).  Returns whether the wave's 128x64 quarter lay wholly
-    // inside the output, i.e. whether it issued all its stores.
+    // the bias slot).  Returns whether the wave's part lay wholly inside the
+    // output, i.e. whether it issued all its stores.
     // always inlined: when both problems store the same type this lambda is
     // called from two places, and an outlined copy would take acc by
     // reference, i.e. through scratch memory
