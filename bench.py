@@ -47,7 +47,7 @@ import time
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 M_TOKENS = 16384
-SINGLE_KERNEL_FAMILIES = ("gemm_fwd", "gemm_dx")
+SINGLE_KERNEL_FAMILIES = ("gemm_fwd", "gemm_bwd", "gemm_dx")
 XL_LINEARS = [("qkv", 1600, 4800), ("attn_proj", 1600, 1600), ("fc", 1600, 6400), ("proj", 6400, 1600)]
 SMALL_LINEARS = [("qkv", 768, 2304), ("attn_proj", 768, 768), ("fc", 768, 3072), ("proj", 3072, 768)]
 
@@ -221,6 +221,16 @@ def main():
                iarr([l["Wq"].stride(0) for l in layers]), parr([l["Wt"] for l in layers]),
                iarr([l["Wt"].stride(0) for l in layers]), qb_ws.data_ptr(), qb_ws.numel())
 
+    # The grouped backward of a Linear is one kernel launch when its plan
+    # keeps dW unsplit (family gemm_bwd) and two when dW runs in K slices
+    # (the persistent kernel + the ordered slice reduce: gemm_bwd_split).
+    bwd_family = []
+    for l in layers:
+        g_, s_ = ctypes.c_int(), ctypes.c_int()
+        df.call("df_fp8_gemm_bwd_plan", M, l["N"], l["K"], gws_bytes, ctypes.byref(g_), ctypes.byref(s_))
+        bwd_family.append("gemm_bwd" if g_.value and s_.value == 1 else
+                          "gemm_bwd_split" if g_.value else "gemm_bwd_separate")
+
     def step(tm, grouped=not args.separate_backward):
         if not args.per_linear_weights:
             tm.run("weights_batch", df.call, "df_quantize_2d_batch", BF, nl, *qb_args, cur())
@@ -239,7 +249,7 @@ def main():
             quant(tm, l["dY"], M, N, E5, sdy_am, sdy, l["dYq"], l["dYt"], "grad", db=l["db"])
             if grouped:
                 # dX and dW in one launch (df_fp8_gemm_bwd)
-                tm.run("gemm_bwd", df.call, "df_fp8_gemm_bwd", l["dYq"].data_ptr(), l["dYq"].stride(0),
+                tm.run(bwd_family[i], df.call, "df_fp8_gemm_bwd", l["dYq"].data_ptr(), l["dYq"].stride(0),
                        l["Wt"].data_ptr(), l["Wt"].stride(0), l["dYt"].data_ptr(), l["dYt"].stride(0),
                        l["Xt"].data_ptr(), l["Xt"].stride(0), M, N, K, sdy, sw, sx, BF, l["dX"].data_ptr(), K,
                        F32, l["dW"].data_ptr(), K, gws.data_ptr(), gws_bytes, cur())
@@ -252,13 +262,13 @@ def main():
                    gws.data_ptr(), gws_bytes, cur())
 
     # algorithmic work per step: 2*M*N*K per GEMM on unpadded shapes
-    families = ("gemm_fwd", "gemm_dx", "gemm_dw") if args.separate_backward else ("gemm_fwd", "gemm_bwd")
-    gemm_flops = {k: 0 for k in families}
+    gemm_flops = {}
     qbytes = {}
-    for (_, K, N) in XL_LINEARS:
+    for i, (_, K, N) in enumerate(XL_LINEARS):
         f = 2 * M * N * K
-        for k in gemm_flops:
-            gemm_flops[k] += 2 * f if k == "gemm_bwd" else f
+        fams = ("gemm_fwd", "gemm_dx", "gemm_dw") if args.separate_backward else ("gemm_fwd", bwd_family[i])
+        for k in fams:
+            gemm_flops[k] = gemm_flops.get(k, 0) + (f if k in ("gemm_fwd", "gemm_dx", "gemm_dw") else 2 * f)
         for tag, r, c in (("act", M, K), ("weight", N, K), ("grad", M, N)):
             if tag == "weight" and not args.per_linear_weights:
                 # absmax read + quantize read + both code layouts written
@@ -348,11 +358,13 @@ def main():
 
     # dominant kernel = the largest summed time among the families whose
     # C-ABI call is exactly one kernel launch: gemm_fwd (the persistent
-    # kernel, e4m3 x e4m3 -> bf16 + bias) and gemm_dx (persistent, e5m2 x e4m3
-    # -> bf16).  gemm_dw is several kernels (K-slice partial tiles + their
-    # ordered reduction on the split outputs) and each quantize family two or three
-    # (absmax passes, 2-D quantize, column-sum fold); they are reported in
-    # `kernels` but a per-launch roofline needs one kernel.
+    # kernel, e4m3 x e4m3 -> bf16 + bias), gemm_bwd (the grouped dX + dW
+    # persistent launch of the Linears whose dW stays unsplit) and, under
+    # --separate-backward, gemm_dx.  gemm_bwd_split and gemm_dw are several
+    # kernels (K-slice partial tiles + their ordered reduction) and each
+    # quantize family two or three (absmax passes, 2-D quantize, column-sum
+    # fold); they are reported in `kernels` but a per-launch roofline needs
+    # one kernel.
     dom = max((k for k in SINGLE_KERNEL_FAMILIES if k in per), key=lambda k: per[k][0])
     tot_ms, cnt = per[dom]
     avg_ms = tot_ms / cnt
@@ -368,7 +380,7 @@ def main():
         roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                 "avg_launch_ms": round(avg_ms, 4), "work_per_launch": work_per_launch}
-    roof["traffic"] = measured_traffic(roof["kernel"])
+    roof["traffic"], roof["traffic_source"] = measured_traffic(roof["kernel"])
     kernels = {}
     for k, (t, c) in sorted(per.items()):
         d = {"ms_per_step": round(t / args.steps, 4), "launches_per_step": c // args.steps}
@@ -429,14 +441,21 @@ def main():
 def measured_traffic(kernel_family):
     """HBM bytes per launch of a kernel family from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE runs (profiles/hbm_traffic.json, written from
-    those runs with the copy-kernel scale factor applied), or None."""
+    those runs with the copy-kernel scale factor applied), and where that
+    figure comes from (the file, the tree the runs measured, their
+    commands); (None, None) without it.  rocprofv3 cannot count inside the
+    process it measures, so the figure is as fresh as the last profile
+    run."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
     try:
         with open(path) as fh:
             data = json.load(fh)
-        return data["families"][kernel_family]["bytes_per_launch"]
+        fam = data["families"][kernel_family]
+        src = {"file": "profiles/hbm_traffic.json", "tree": data.get("tree"), "kernel": fam["kernel"],
+               "commands": [data["command_fetch"], data["command_write"]]}
+        return fam["bytes_per_launch"], src
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
 
 
 # The profiling runs behind profiles/ (from the repository root on one
@@ -490,8 +509,22 @@ EXTRA_STATS = (
 # K-split>.
 TRAFFIC_FAMILIES = {
     "gemm_fwd": ("gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true, false, void>",),
+    "gemm_bwd": ("gemm_nt_persistent_kernel<1, 0, float, float, false, false, unsigned short>",),
     "gemm_dx": ("gemm_nt_persistent_kernel<1, 0, unsigned short, float, false, false, void>",),
 }
+
+
+def _tree_id():
+    """The git commit of this tree (with -dirty for uncommitted changes),
+    recorded beside profile summaries; None outside a git checkout."""
+    import subprocess
+
+    try:
+        r = subprocess.run(["git", "describe", "--always", "--dirty", "--abbrev=12"], capture_output=True, text=True,
+                           cwd=os.path.dirname(os.path.abspath(__file__)), timeout=20)
+        return r.stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
+        return None
 
 
 def _short_kernel(name):
@@ -557,7 +590,7 @@ def config4_summaries(out_dir, prof):
         k = names[0]
         fams[fam] = {"kernel": k, "bytes_per_launch": int(round(fetch[k][0] * 1024 * fscale + write[k][0] * 1024 * wscale)),
                      "fetch_KiB": fetch[k][0], "write_KiB": write[k][0]}
-    data = {"command_fetch": PROFILE_COMMANDS["fetch"], "command_write": PROFILE_COMMANDS["write"],
+    data = {"tree": _tree_id(), "command_fetch": PROFILE_COMMANDS["fetch"], "command_write": PROFILE_COMMANDS["write"],
             "calibration": {"kernel": copy, "bytes": 1 << 30, "fetch_KiB": copy_f, "write_KiB": copy_w,
                             "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
             "families": fams}

@@ -115,7 +115,7 @@ _SIGS = {
     "df_streamer_wait": (_c_int, [_vp, _c_int, _vp]),
     "df_streamer_release": (_c_int, [_vp, _c_int, _vp]),
     "df_streamer_slot": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
-    "df_streamer_copy_stream": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "df_streamer_copy_stream": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
     "df_amax_history_init": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp]),
     "df_quantize_2d_delayed_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "df_quantize_2d_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp,
@@ -427,10 +427,14 @@ class WeightStreamer:
     def release(self, slot: int, stream: int | None = None):
         call("df_streamer_release", self.handle, slot, _stream() if stream is None else stream)
 
-    def copy_stream(self) -> int:
-        st = _vp()
-        call("df_streamer_copy_stream", self.handle, ctypes.byref(st))
-        return st.value or 0
+    def copy_streams(self) -> tuple[int, int]:
+        """The two copy streams (load i runs on stream i % 2)."""
+        out = []
+        for which in (0, 1):
+            st = _vp()
+            call("df_streamer_copy_stream", self.handle, which, ctypes.byref(st))
+            out.append(st.value or 0)
+        return out[0], out[1]
 
     def close(self):
         if self.handle is not None:

@@ -132,10 +132,11 @@ extern "C" int df_streamer_destroy(df_streamer_s* s) {
     return DF_OK;
 }
 
-extern "C" int df_streamer_copy_stream(df_streamer_s* s, void** stream) {
+extern "C" int df_streamer_copy_stream(df_streamer_s* s, int which, void** stream) {
     clear_error();
     DF_CHECK(s && stream, DF_ERR_INVALID, "df_streamer_copy_stream: NULL argument");
-    *stream = s->copy[0];
+    DF_CHECK(which == 0 || which == 1, DF_ERR_INVALID, "df_streamer_copy_stream: which=%d is not 0 or 1", which);
+    *stream = s->copy[which];
     return DF_OK;
 }
 
@@ -159,7 +160,14 @@ extern "C" int df_streamer_load(df_streamer_s* s, const void* host_src, size_t b
     // made to wait on the GPU for an event of the compute stream delays the
     // compute stream's own work (measured: 81.5 ms instead of 65.5 ms for a
     // 96-layer sweep whose kernels alone take 57.6 ms).
-    if (s->state[k] == kReleased) DF_HIP(hipEventSynchronize(s->released[k]), "df_streamer_load");
+    if (s->state[k] == kReleased) {
+        DF_HIP(hipEventSynchronize(s->released[k]), "df_streamer_load");
+        // the slot's previous copy ran on the other copy stream, so stream
+        // order does not keep it ahead of this one; a caller that waited on
+        // it before releasing the slot has made it complete already (then
+        // this returns at once), one that did not is covered here
+        DF_HIP(hipEventSynchronize(s->loaded[k]), "df_streamer_load");
+    }
     uint8_t* dst = s->dev + (size_t)k * s->slot_bytes;
     hipStream_t cs = s->copy[s->loads++ & 1u];
     if (bytes) DF_HIP(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, cs), "df_streamer_load");

@@ -247,6 +247,9 @@ tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerN
                          wt ? Op : 0, nullptr);
         sx_used_ = sw_used_ = nullptr;
     }
+    // a training forward has just written W^T codes of the current weights
+    // (at the scale sw), so a load() before it no longer leaves them stale
+    if (wt) wt_stale_ = false;
     const size_t gb = df_fp8_gemm_workspace_bytes(N, out_features_, in_features_);
     CHECK_DF_EX(df_fp8_gemm_fwd(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sw, dt, this->bias_.data(), dt,
                                 output.data(), out_features_, gemm_ws_.get(gb), gb, st()));
@@ -285,6 +288,7 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
                          Op, nullptr);
         wt = wtn;
         wt_stale_ = false;
+        sw_used_ = nullptr;  // these codes are at the just-in-time scale sc + 1
     }
     if (history_len_ > 0 && sx_used_) {
         sdy = quantize_delayed(ddy_, grad_output.data(), N, out_features_, DF_FMT_E5M2, dyq, Op, dyt, Np, db);

@@ -27,7 +27,7 @@ import ctypes
 
 import numpy as np
 
-from . import DType, Fmt, WeightStreamer, call, lib, round16, synth
+from . import DType, Fmt, WeightStreamer, _in_dtype, call, lib, round16, synth
 
 XL_LINEARS = [("qkv", 1600, 4800), ("attn_proj", 1600, 1600), ("fc", 1600, 6400), ("proj", 6400, 1600)]
 
@@ -49,6 +49,8 @@ class StreamedStack:
         self.linears = list(linears)
         self.keep = keep_outputs
         self.out_dtype = out_dtype if out_dtype is not None else torch.bfloat16
+        if self.out_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"StreamedStack: out_dtype must be float32 or bfloat16, got {self.out_dtype}")
         r16 = round16
         self.fwd_off, self.bwd_off = [], []
         o1 = o2 = 0
@@ -171,7 +173,7 @@ class StreamedStack:
         return (2 * l + direction) * self.blob
 
     def _dt(self, t):
-        return int(DType.FLOAT32) if t.dtype == self.torch.float32 else int(DType.BFLOAT16)
+        return int(_in_dtype(t))
 
     # ------------------------------------------------------------ layers --
     def fwd_layer(self, l, base):

@@ -392,7 +392,9 @@ int df_streamer_load(df_streamer* s, const void* host_src, size_t bytes, int* sl
 int df_streamer_wait(df_streamer* s, int slot, void* stream);
 int df_streamer_release(df_streamer* s, int slot, void* stream);
 int df_streamer_slot(df_streamer* s, int slot, void** dev_ptr);
-int df_streamer_copy_stream(df_streamer* s, void** stream);  /* the first of the two copy streams */
+/* copy stream `which` (0 or 1): load i is enqueued on copy stream i % 2, so
+ * a caller that synchronizes with the copies needs both */
+int df_streamer_copy_stream(df_streamer* s, int which, void** stream);
 
 /* ---- consumer side of the fp32 gradients: global-norm clipping and Adam ----
  * Lists of fp32 tensors: the pointer arrays and `sizes` are HOST arrays of

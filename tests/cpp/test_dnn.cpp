@@ -956,6 +956,37 @@ TEST_F(FullyConnectedLayerTest, DelayedScalingUsesHistoryScale) {
     EXPECT_EQ(h[1], dfo_absmax_f32(x1.data(), (int64_t)x1.size()));
 }
 
+// load() between two training forwards of a delayed-scaling layer: the
+// second forward writes the W^T codes of the loaded weights at the delayed
+// W scale (the history still holds the old weights' absmax), and the
+// backward's dX must use those codes with that same scale.
+TEST_F(FullyConnectedLayerTest, DelayedScalingForwardAfterLoadKeepsWtScale) {
+    const int N = 16, in_f = 64, out_f = 24;
+    FullyConnectedLayer<float> layer(in_f, out_f, true), other(in_f, out_f, true);
+    const auto w_old = uniform((size_t)out_f * in_f, -0.3f, 0.3f, 111);
+    const auto w_new = uniform((size_t)out_f * in_f, -0.1f, 0.1f, 112);
+    layer.parameters()[0]->upload(w_old.data());
+    other.parameters()[0]->upload(w_new.data());
+    layer.set_delayed_scaling(16);
+    tensor<float> x({N, in_f}), gy({N, out_f});
+    const auto xh = uniform((size_t)N * in_f, -1.0f, 1.0f, 113), gh = uniform((size_t)N * out_f, -0.01f, 0.01f, 114);
+    x.upload(xh.data());
+    gy.upload(gh.data());
+    layer.forward(x);
+    std::stringstream ss;
+    other.save(ss);
+    layer.load(ss);
+    layer.forward(x);
+    const auto dx = download(layer.backward(gy));
+    // oracle: W (loaded) at the delayed scale of the old weights' absmax; dY
+    // at its own scale (the first backward seeds its history)
+    const float sw = dfo_scale(dfo_absmax_f32(w_old.data(), (int64_t)w_old.size()), DFO_E4M3);
+    const auto wd = fp8_values_at(w_new, sw, DFO_E4M3), gd = fp8_values(gh, DFO_E5M2);
+    std::vector<float> e((size_t)N * in_f);
+    dfo_fc_backward_input(gd.data(), wd.data(), e.data(), N, in_f, out_f, 4);
+    EXPECT_LE(rel_err(dx, e), 1e-4);
+}
+
 // ---- LayerNormLayer (dnn/layers/layer_norm_layer.cu) and the fused producer ----
 TEST_F(LayerNormLayerTest, ForwardMatchesOracle) {
     const int rows = 37, C = 100;

@@ -78,9 +78,13 @@ def test_noalloc_rejects_oversized(dev):
     assert need > LIMIT
     hist = torch.zeros(4, dtype=torch.float32, device=dev)
     sc = torch.ones(1, dtype=torch.float32, device=dev)
-    fake = 0x100000  # never dereferenced: the call fails its size check first
-    rc = _fn()(int(DType.BFLOAT16), fake, rows, cols, cols, int(Fmt.E5M2), sc.data_ptr(), sc.data_ptr(),
-               hist.data_ptr(), 4, fake, cols, None, 0, fake, None)
+    # x and q are NULL and colsum is a real (tiny) buffer, so the size is
+    # that of the column-sum partials: the size check refuses the call
+    # first, and were it to pass, the NULL-pointer checks would still refuse
+    # it with no launch
+    cs = torch.zeros(4, dtype=torch.float32, device=dev)
+    rc = _fn()(int(DType.BFLOAT16), None, rows, cols, cols, int(Fmt.E5M2), sc.data_ptr(), sc.data_ptr(),
+               hist.data_ptr(), 4, None, cols, None, 0, cs.data_ptr(), None)
     assert rc == -5
     msg = df.lib().df_last_error_string().decode()
     assert str(LIMIT) in msg and "df_quantize_2d_delayed_noalloc" in msg
