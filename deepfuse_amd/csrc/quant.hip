@@ -478,6 +478,24 @@ constexpr int kT2 = 128;
 // rows of a quantize_2d_kernel tile (quantize_2d_batch_kernel keeps kT2)
 constexpr int kT2R = 128;
 
+// LDS layout of a tile's transposed codes: column col holds the 128 codes
+// of its rows as sixteen 8-byte slots (slot s = rows 8s..8s+7).  Columns
+// are paired into 256-byte units, and the 32 slots of a pair are permuted
+// by an even XOR key taken from the column's thread group (col / E, E =
+// the columns one thread loads), so
+//  - the 8- or 16-byte writes of one instruction (one column per thread
+//    group, the row slots of the block's row groups) spread over all 64
+//    banks instead of landing 16 to a bank (a column stride that is a
+//    multiple of the bank period did that), and
+//  - a 16-byte chunk (slots 2j, 2j+1) stays contiguous and aligned, so the
+//    read-back of 16 rows of one column is one ds_read_b128, and the 16
+//    lanes reading one column pair hit distinct banks.
+template <int E>
+__device__ __forceinline__ int tslot(int col, int s) {
+    const int key = ((col / E) & 15) << 1;
+    return (col >> 1) * 256 + (((((col & 1) << 4) | s) ^ key) << 3);
+}
+
 template <typename InT> struct Ld;
 template <> struct Ld<float> {
     static constexpr int E = 4;
@@ -602,7 +620,7 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
     constexpr int RG = kThreads / TPR; // row groups
     constexpr int RPT = TR / RG;       // rows per thread (8 for bf16, 16 for fp32 at TR = 128)
     static_assert(RPT % 4 == 0 && RPT <= 32, "4x4 byte transposes");
-    constexpr int TSTRIDE = TR + 16;   // LDS tile row (bytes), [column][row]
+    static_assert(TR == 128 && (RPT == 8 || RPT == 16), "the tslot layout holds 128-row tiles, 8 or 16 rows a thread");
     const int r0 = by * TR, c0 = bx * kT2;  // tile (bx, by) of a grid nbx tiles wide
     const int tc = (threadIdx.x % TPR) * E, rg = threadIdx.x / TPR;
     const int c = c0 + tc;
@@ -726,18 +744,13 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const uint32_t* w = wcol[e];
-            uint8_t* dst = tile + (tc + e) * TSTRIDE + rg * RPT;
-            if (RPT >= 16) {
-#pragma unroll
-                for (int h = 0; h < RPT / 16; ++h)
-                    *reinterpret_cast<u32x4*>(dst + 16 * h) =
-                        u32x4{w[4 * h], w[4 * h + 1 < RPT / 4 ? 4 * h + 1 : 0], w[4 * h + 2 < RPT / 4 ? 4 * h + 2 : 0],
-                              w[4 * h + 3 < RPT / 4 ? 4 * h + 3 : 0]};
-            } else if (RPT == 8) {
-                *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[RPT / 4 > 1 ? 1 : 0]};
-            } else {
-                *reinterpret_cast<uint32_t*>(dst) = w[0];
-            }
+            // rows rg*RPT.. of column tc+e: slot rg (8 rows) or slots 2rg,
+            // 2rg+1 (16 rows, one aligned 16-byte chunk)
+            uint8_t* dst = tile + tslot<E>(tc + e, rg * (RPT / 8));
+            if (RPT == 16)
+                *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1 % (RPT / 4)], w[2 % (RPT / 4)], w[3 % (RPT / 4)]};
+            else
+                *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1 % (RPT / 4)]};
         }
     }
     if (COLSUM) {
@@ -753,7 +766,7 @@ __device__ __forceinline__ void q2d_tile(const InT* __restrict__ x, int rows, in
             const int col = idx / CPC, rc = (idx % CPC) * 16;
             if (c0 + col < cols && r0 + rc < ldqt) {
                 u32x4* dst = reinterpret_cast<u32x4*>(qt + (int64_t)(c0 + col) * ldqt + r0 + rc);
-                const u32x4 v = *reinterpret_cast<const u32x4*>(tile + col * TSTRIDE + rc);
+                const u32x4 v = *reinterpret_cast<const u32x4*>(tile + tslot<E>(col, rc >> 3));
                 if (NT && qt_lines)
                     st_nt<true>(dst, v);
                 else
@@ -937,7 +950,7 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
                                                                 uint32_t* __restrict__ amaxpart = nullptr,
                                                                 LnArgs ln = LnArgs()) {
     constexpr int RG = kThreads / (kT2 / Ld<InT>::E);
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2R + 16)];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * kT2R];
     __shared__ float csum[COLSUM ? RG : 1][kT2];
     const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
     if (!CODES || d.fast)
@@ -1018,7 +1031,7 @@ __global__ __launch_bounds__(kThreads) void scale_batch_kernel(const float* __re
 template <typename InT, int FMT, bool NT>
 __global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const BatchArgs B,
                                                                       const float* __restrict__ scale) {
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * (kT2 + 16)];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * kT2];
     __shared__ float csum[1][kT2];
     const int t = batch_owner(B.tile_first, B.count, blockIdx.x);
     const int lt = blockIdx.x - B.tile_first[t];
