@@ -485,9 +485,8 @@ PROFILE_COMMANDS = {
     "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-producer --no-delayed --no-config3"),
-    "stats_streaming": ("rocprofv3 --kernel-trace --memory-copy-trace --stats --output-format csv "
-                        "-d gpurun_out/prof_streaming -o bench -- python3 bench.py --steps 2 --warmup 1 "
-                        "--no-cpu-baseline --no-conversion --no-optimizer --no-producer --no-delayed --no-config3"),
+    "streaming": ("python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-optimizer "
+                  "--no-producer --no-delayed --no-config3"),
     "stats_producer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_producer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-optimizer --no-delayed --no-config3"),
@@ -650,7 +649,7 @@ def summarize_profiles():
             fh.write("\n".join(lines) + "\n")
         extra.append(fname)
     if streaming_summary(out_dir, prof):
-        extra.append("streaming_h2d_copies_config5.md")
+        extra.append("streaming_config5.md")
     if config3_summary(out_dir, prof):
         extra.append("gemm_config3_kernels.md")
     print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)}, extra {extra})")
@@ -835,49 +834,48 @@ def mfma_summary(out_dir, prof):
 
 
 def streaming_summary(out_dir, prof):
-    """profiles/streaming_h2d_copies_config5.md from the stats_streaming run:
-    the weight copies of config 5 (the host-to-device stream that carries
-    2 x layers copies per step, all the same size) and their rate, with the
-    copy size taken from the same run's bench line."""
-    import csv
-    path = os.path.join(out_dir, "prof_streaming", "bench_memory_copy_trace.csv")
-    # the run's stdout (its bench line), saved as gpurun_out/prof_stats_streaming.log
-    log = os.path.join(out_dir, "prof_stats_streaming.log")
+    """profiles/streaming_config5.md from the streaming run's bench line
+    (gpurun_out/prof_streaming.log, the stdout of PROFILE_COMMANDS
+    ["streaming"]): the step, compute and copy times of config 5, every
+    copy timed by HIP events on its copy stream (rocprofv3's memory-copy
+    trace dropped completion callbacks on this leg, so it is not used)."""
+    log = os.path.join(out_dir, "prof_streaming.log")
     if not os.path.exists(log):
-        log = os.path.join(out_dir, "prof_streaming.log")
-    if not (os.path.exists(path) and os.path.exists(log)):
         return False
     line = [l for l in open(log) if l.startswith('{"metric"')]
     if not line:
         return False
     st = json.loads(line[-1])["streaming"]
-    with open(path) as fh:
-        rows = [r for r in csv.DictReader(fh) if r["Direction"] == "MEMORY_COPY_HOST_TO_DEVICE"]
-    by_stream = {}
-    for r in rows:
-        by_stream.setdefault(r["Stream_Id"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    # the streamer's two copy streams carry the layer copies, the longest
-    # copies of the run: every copy over half the longest stream median
-    per = st["copies_per_step"]
-    top = max(sorted(v)[len(v) // 2] for v in by_stream.values())
-    sids = sorted(k for k, v in by_stream.items() if sorted(v)[len(v) // 2] > 0.5 * top)
-    sid = ", ".join(sids)
-    durs = sorted(d for k in sids for d in by_stream[k] if d > 0.5 * top)
-    nbytes = st["copy_bytes"]
-    med = durs[len(durs) // 2]
-    lines = ["# rocprofv3 memory-copy trace -- config 5 weight streaming (48-layer GPT-2 XL Linear stack, 8192 tokens)",
-             "", "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["stats_streaming"],
-             "", f"The streamer's copy streams (stream ids {sid}) carry {len(durs)} host-to-device copies of "
-             f"{nbytes / 1e6:.2f} MB (one layer's e4m3 weight codes, W for the forward sweep, W^T for the backward; "
-             f"{per} per step): the warm-up step, the timed steps and the copies-alone pass.", "",
+    if "copies_alone" not in st:
+        return False
+    ca, cs, ss = st["copies_alone"], st["copies_streamed"], st["steady_state"]
+    lines = ["# Config 5 weight streaming: step, compute and copy times (HIP events)", "",
+             "Command (from the repository root, on one MI355X; stdout to gpurun_out/prof_streaming.log):", "",
+             "    " + PROFILE_COMMANDS["streaming"], "",
+             st["workload"] + ".  Every copy is one layer's e4m3 weight codes "
+             f"({st['copy_bytes'] / 1e6:.2f} MB; W for the forward sweep, W^T for the backward), "
+             f"{st['copies_per_step']} per step, timed by HIP events recorded on its copy stream right before and "
+             "after it (df_streamer_set_timing).  A copy's own duration runs from its stream reaching it to its "
+             "end; with the streamer's two copy streams two copies share the link for most of that time, so the "
+             "link's rate is the bytes over the time any copy was in flight (busy).", "",
              "| quantity | value |", "|---|---|",
-             f"| copies | {len(durs)} |",
-             f"| median / min / max copy | {med:.1f} / {durs[0]:.1f} / {durs[-1]:.1f} us |",
-             f"| rate at the median copy | {nbytes / (med * 1e-6) / 1e9:.1f} GB/s |",
-             f"| same run, bench line: streamed step / compute alone / copies alone | {st['ms_per_step']} / "
-             f"{st['compute_alone_ms']} / {st['h2d_alone_ms']} ms (overlap {st['overlap']}) |",
-             f"| same run, bench line: copies alone rate | {st['h2d_gbs']} GB/s |"]
-    with open(os.path.join(prof, "streaming_h2d_copies_config5.md"), "w") as fh:
+             f"| streamed step | {st['ms_per_step']} ms ({st['value']} TFLOP/s) |",
+             f"| compute alone (weights resident) / the same under concurrent copies | {st['compute_alone_ms']} / "
+             f"{st.get('compute_under_copies_ms')} ms |",
+             f"| compute alone: forward sweep / backward sweep | {st['compute_fwd_sweep_ms']} / "
+             f"{st['compute_bwd_sweep_ms']} ms |",
+             f"| copies alone | {st['h2d_alone_ms']} ms ({st['h2d_gbs']} GB/s) |",
+             f"| overlap = max(compute, copies) / streamed | {st['overlap']} |",
+             f"| flow-shop bound of the entry order (per-entry copy and compute times) | {st['flowshop_bound_ms']} ms "
+             f"(streamed step at {st['overlap_vs_flowshop_bound']} of it) |",
+             f"| steady state: {ss['micro_batches']} passes, same weights, {ss['slots']} slots | {ss['ms_per_pass']} ms "
+             f"per pass (overlap {ss['overlap']}) |", "",
+             "| copies | count | median copy | its rate | sum of durations | busy | link rate | copies in flight |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, c in (("alone", ca), ("in the streamed step", cs)):
+        lines.append(f"| {name} | {c['copies']} | {c['median_copy_ms']} ms | {c['median_copy_gbs']} GB/s | "
+                     f"{c['sum_copy_ms']} ms | {c['busy_ms']} ms | {c['busy_gbs']} GB/s | {c['copies_in_flight_avg']} |")
+    with open(os.path.join(prof, "streaming_config5.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
     return True
 
@@ -1464,7 +1462,50 @@ def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
     return res
 
 
-def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, steps=2):
+def _copy_stats(log, nbytes):
+    """Summary of a streamer copy log [(start, end) ms]: per-copy duration
+    (its copy stream reaching it to its end), time the link was busy (union
+    of the copies' intervals) and the rates that follow."""
+    if not log:
+        return None
+    dur = sorted(b - a for a, b in log)
+    ivs = sorted(log)
+    busy, cur_a, cur_b = 0.0, ivs[0][0], ivs[0][1]
+    for a, b in ivs[1:]:
+        if a > cur_b:
+            busy += cur_b - cur_a
+            cur_a, cur_b = a, b
+        else:
+            cur_b = max(cur_b, b)
+    busy += cur_b - cur_a
+    span = max(b for _, b in log) - min(a for a, _ in log)
+    n = len(log)
+    med = dur[n // 2]
+    return {"copies": n, "bytes_each": nbytes, "median_copy_ms": round(med, 4),
+            "median_copy_gbs": round(nbytes / (med * 1e-3) / 1e9, 2),
+            "sum_copy_ms": round(sum(dur), 3), "busy_ms": round(busy, 3), "span_ms": round(span, 3),
+            "busy_gbs": round(n * nbytes / (busy * 1e-3) / 1e9, 2),
+            "copies_in_flight_avg": round(sum(dur) / busy, 3) if busy > 0 else None}
+
+
+def flowshop_bound(copy_ms, compute_ms):
+    """Shortest time a fixed sequence of entries can take when entry j's
+    copy (copy_ms[j], on one link, in order) must end before its compute
+    (compute_ms[j], on the GPU, in order) starts, with unlimited buffering:
+    max over k of (copies 0..k) + (computes k..end) -- the two-machine flow
+    shop's makespan for that order."""
+    best, pre = 0.0, 0.0
+    suf = [0.0] * (len(compute_ms) + 1)
+    for j in range(len(compute_ms) - 1, -1, -1):
+        suf[j] = suf[j + 1] + compute_ms[j]
+    for k in range(len(copy_ms)):
+        pre += copy_ms[k]
+        best = max(best, pre + suf[k])
+    return best
+
+
+def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, steps=2, micro_batches=3,
+                    steady_slots=12):
     """Config 5: a 48-layer GPT-2 XL Linear stack (4 Linears per layer) at
     `tokens` tokens, forward then backward, with every layer's e4m3 weight
     codes in pinned host memory: the forward sweep streams W [N, K] per layer,
@@ -1472,13 +1513,21 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
     a ring of `slots` device slots filled on the streamer's copy streams while
     earlier layers compute (deepfuse_amd.stack.StreamedStack, the same code
     tests/test_gpu_stream.py checks).  Per layer and Linear the step
-    quantizes the activation (e4m3, row copy + the transposed copy cached for
-    dW) and the upstream gradient (e5m2, both copies, db fused), and runs the
-    forward, dX and dW GEMMs; dW is kept per layer (fp32).
+    quantizes the layer's own activation (e4m3, row copy + the transposed copy
+    cached for dW) and upstream gradient (e5m2, both copies, db fused), and
+    runs the forward, dX and dW GEMMs; dW is kept per layer (fp32).
 
     Also timed: the same step with all weights resident in HBM (compute
-    alone) and the 2*layers weight copies alone on the copy streams (PCIe
-    alone); overlap = max(compute, copies) / streamed."""
+    alone, with a HIP event per layer entry) and the 2*layers weight copies
+    alone on the copy streams (PCIe alone), every copy timed by HIP events on
+    its copy stream (df_streamer_set_timing).  overlap = max(compute,
+    copies) / streamed; bound = the flow-shop makespan of the entry order from
+    the measured per-entry copy and compute times (the forward sweep is
+    PCIe-bound and the backward compute-bound, so one step cannot reach
+    max(compute, copies)); steady state = micro_batches passes back to back
+    with the same weights, loads running ahead across passes through
+    steady_slots slots; compute under copies = the resident step while the
+    2*layers copies run on the copy streams beside it."""
     from deepfuse_amd.stack import StreamedStack
 
     stack = StreamedStack(torch, dev, layers=layers, tokens=tokens)
@@ -1498,6 +1547,17 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
         streamer = df.WeightStreamer(slots, stack.blob)
         stack.streamed_step(streamer)  # warm-up
         stream_ms, stream_wall = timed(lambda: stack.streamed_step(streamer), steps)
+        # one more streamed step with every copy timed on its copy stream
+        streamer.set_timing(True)
+        stack.streamed_step(streamer)
+        torch.cuda.synchronize()
+        stream_copies = _copy_stats(streamer.copy_log(), stack.blob)
+        streamer.set_timing(False)
+        # steady state: micro_batches passes with the same weights
+        steady = df.WeightStreamer(steady_slots, stack.blob)
+        stack.streamed_step(steady)
+        mb_ms, _ = timed(lambda: stack.streamed_step(steady, micro_batches), 1)
+        steady.close()
 
         # PCIe alone: the same 2*layers loads with no kernels; the idle
         # compute stream waits for each slot's copy and releases it (the
@@ -1511,6 +1571,7 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
                 streamer.release(slot, cur)
 
         torch.cuda.synchronize()
+        streamer.set_timing(True)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -1518,12 +1579,46 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
         e1.record()
         torch.cuda.synchronize()
         h2d_ms = e0.elapsed_time(e1)
+        alone_log = streamer.copy_log()
+        alone_copies = _copy_stats(alone_log, stack.blob)
         streamer.close()
+        # per-entry copy time when the copies run back to back: the gap
+        # between consecutive copy ends (the first: its own duration)
+        ends = [b for _, b in alone_log]
+        copy_each = [ends[0] - alone_log[0][0]] + [ends[j] - ends[j - 1] for j in range(1, len(ends))]
 
-        # compute alone: weights resident in HBM (one device copy of the blobs)
+        # compute alone: weights resident in HBM (one device copy of the
+        # blobs), a HIP event before every entry
         dev_w = stack.resident_weights()
         stack.resident_step(dev_w)
         compute_ms, compute_wall = timed(lambda: stack.resident_step(dev_w), steps)
+        torch.cuda.synchronize()
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(stack.seq) + 1)]
+        for j, (d, l) in enumerate(stack.seq):
+            evs[j].record()
+            stack.resident_entry(dev_w, d, l)
+        evs[-1].record()
+        torch.cuda.synchronize()
+        compute_each = [evs[j].elapsed_time(evs[j + 1]) for j in range(len(stack.seq))]
+        # the resident step with the 2*layers copies running beside it (the
+        # copies wait on and release their slots on a side stream, so the
+        # compute stream never waits for them): what concurrent copies cost
+        # the kernels themselves
+        side = torch.cuda.Stream()
+        beside = df.WeightStreamer(slots, stack.blob)
+        torch.cuda.synchronize()
+        c0 = torch.cuda.Event(enable_timing=True)
+        c1 = torch.cuda.Event(enable_timing=True)
+        c0.record()
+        stack.resident_step(dev_w)
+        c1.record()
+        for d, l in stack.seq:
+            slot, _ = beside.load(stack.host_ptr + stack.host_offset(l, d), stack.blob)
+            beside.wait(slot, side.cuda_stream)
+            beside.release(slot, side.cuda_stream)
+        torch.cuda.synchronize()
+        beside.close()
+        under_copies_ms = c0.elapsed_time(c1)
         # the same resident step replayed from a HIP graph: no host launch gaps
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -1531,21 +1626,36 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
         graph.replay()
         compute_graph_ms, _ = timed(graph.replay, steps)
         del graph, dev_w
+        bound_ms = flowshop_bound(copy_each, compute_each)
         h2d_bytes = 2 * layers * stack.blob
         step_flops = stack.step_flops
+        half = len(stack.seq) // 2
         return {
             "workload": f"config 5: {layers}-layer GPT-2 XL Linear stack, {tokens} tokens, fwd+bwd, e4m3 weights "
-                        f"streamed from pinned host memory through {slots} device slots",
+                        f"streamed from pinned host memory through {slots} device slots; every layer has its own "
+                        f"activations and gradients",
             "value": round(step_flops / (stream_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "ms_per_step": round(stream_ms, 3), "host_ms_per_step": round(stream_wall, 3),
             "step_gemm_flops": step_flops,
             "compute_alone_ms": round(compute_ms, 3), "compute_alone_host_ms": round(compute_wall, 3),
             "compute_alone_tflops": round(step_flops / (compute_ms * 1e-3) / 1e12, 2),
             "compute_alone_graph_ms": round(compute_graph_ms, 3),
+            "compute_under_copies_ms": round(under_copies_ms, 3),
+            "compute_fwd_sweep_ms": round(sum(compute_each[:half]), 3),
+            "compute_bwd_sweep_ms": round(sum(compute_each[half:]), 3),
             "h2d_alone_ms": round(h2d_ms, 3), "h2d_gbs": round(h2d_bytes / (h2d_ms * 1e-3) / 1e9, 2),
             "h2d_bytes_per_step": h2d_bytes, "copy_bytes": stack.blob, "copies_per_step": 2 * layers,
+            "copies_alone": alone_copies, "copies_streamed": stream_copies,
             "bound": "pcie" if h2d_ms > compute_ms else "compute",
             "overlap": round(max(h2d_ms, compute_ms) / stream_ms, 4),
+            "flowshop_bound_ms": round(bound_ms, 3), "overlap_vs_flowshop_bound": round(bound_ms / stream_ms, 4),
+            "steady_state": {"micro_batches": micro_batches, "slots": steady_slots,
+                             "ms_per_pass": round(mb_ms / micro_batches, 3),
+                             "tflops": round(step_flops / (mb_ms / micro_batches * 1e-3) / 1e12, 2),
+                             "overlap": round(max(h2d_ms, compute_ms) / (mb_ms / micro_batches), 4),
+                             "note": "passes with the same weights (gradient accumulation), loads running ahead "
+                                     "across pass boundaries; each pass overwrites dW as the reference's backward "
+                                     "does"},
             "steps": steps,
         }
     finally:

@@ -116,6 +116,8 @@ _SIGS = {
     "df_streamer_release": (_c_int, [_vp, _c_int, _vp]),
     "df_streamer_slot": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
     "df_streamer_copy_stream": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp)]),
+    "df_streamer_set_timing": (_c_int, [_vp, _c_int]),
+    "df_streamer_copy_log": (_c_int, [_vp, _vp, _vp, _c_int, ctypes.POINTER(_c_int)]),
     "df_amax_history_init": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp]),
     "df_quantize_2d_delayed_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "df_quantize_2d_delayed": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp,
@@ -426,6 +428,20 @@ class WeightStreamer:
 
     def release(self, slot: int, stream: int | None = None):
         call("df_streamer_release", self.handle, slot, _stream() if stream is None else stream)
+
+    def set_timing(self, on: bool = True):
+        """Record HIP events around every later copy (see copy_log)."""
+        call("df_streamer_set_timing", self.handle, 1 if on else 0)
+
+    def copy_log(self) -> list[tuple[float, float]]:
+        """(start, end) in ms of every timed copy since the last call, in load
+        order (waits for them to finish); clears the log."""
+        n = ctypes.c_int()
+        call("df_streamer_copy_log", self.handle, None, None, 0, ctypes.byref(n))
+        cap = n.value
+        a, b = (ctypes.c_float * max(cap, 1))(), (ctypes.c_float * max(cap, 1))()
+        call("df_streamer_copy_log", self.handle, a, b, cap, ctypes.byref(n))
+        return [(a[i], b[i]) for i in range(min(cap, n.value))]
 
     def copy_streams(self) -> tuple[int, int]:
         """The two copy streams (load i runs on stream i % 2)."""

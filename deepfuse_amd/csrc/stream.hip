@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <new>
+#include <vector>
 
 #include "df_common.hpp"
 
@@ -55,6 +56,18 @@ struct df_streamer_s {
     hipEvent_t released[dfk::kMaxSlots] = {};
     int state[dfk::kMaxSlots] = {};
     int next = 0;
+    // timing mode: events recorded on the copy stream right before and after
+    // each copy; a slot's pair is read into the log once that copy is known
+    // to be complete (its slot is loaded again, or the log is read)
+    bool timing = false;
+    hipEvent_t t_start[dfk::kMaxSlots] = {};
+    hipEvent_t t_end[dfk::kMaxSlots] = {};
+    bool t_pending[dfk::kMaxSlots] = {};
+    size_t t_bytes[dfk::kMaxSlots] = {};
+    hipEvent_t t_origin = nullptr;  // recorded just before the first timed copy since the log was read
+    bool have_origin = false;
+    std::vector<float> log_start, log_end;
+    std::vector<size_t> log_bytes;
 };
 
 using namespace dfk;
@@ -90,7 +103,10 @@ static void destroy_streamer(df_streamer_s* s) {
     for (int i = 0; i < kMaxSlots; ++i) {
         if (s->loaded[i]) (void)hipEventDestroy(s->loaded[i]);
         if (s->released[i]) (void)hipEventDestroy(s->released[i]);
+        if (s->t_start[i]) (void)hipEventDestroy(s->t_start[i]);
+        if (s->t_end[i]) (void)hipEventDestroy(s->t_end[i]);
     }
+    if (s->t_origin) (void)hipEventDestroy(s->t_origin);  // its own event (created with the timing pairs)
     for (hipStream_t c : s->copy)
         if (c) (void)hipStreamDestroy(c);
     if (s->dev) (void)hipFree(s->dev);
@@ -148,6 +164,62 @@ extern "C" int df_streamer_slot(df_streamer_s* s, int slot, void** dev_ptr) {
     return DF_OK;
 }
 
+// Moves slot k's timed copy into the log (start and end in ms after the
+// origin event, which was recorded just before the first timed copy since
+// the log was last read); waits for that copy to complete.
+static int log_slot(df_streamer_s* s, int k, const char* what) {
+    if (!s->t_pending[k]) return DF_OK;
+    DF_HIP(hipEventSynchronize(s->t_end[k]), what);
+    DF_HIP(hipEventSynchronize(s->t_origin), what);  // it may sit on the other copy stream
+    float a = 0.0f, b = 0.0f;
+    DF_HIP(hipEventElapsedTime(&a, s->t_origin, s->t_start[k]), what);
+    DF_HIP(hipEventElapsedTime(&b, s->t_origin, s->t_end[k]), what);
+    s->log_start.push_back(a);
+    s->log_end.push_back(b);
+    s->log_bytes.push_back(s->t_bytes[k]);
+    s->t_pending[k] = false;
+    return DF_OK;
+}
+
+extern "C" int df_streamer_set_timing(df_streamer_s* s, int on) {
+    clear_error();
+    DF_CHECK(s, DF_ERR_INVALID, "df_streamer_set_timing: streamer is NULL");
+    if (on && !s->t_origin) {
+        DF_HIP(hipEventCreate(&s->t_origin), "df_streamer_set_timing");
+        for (int i = 0; i < s->slots; ++i) {
+            DF_HIP(hipEventCreate(&s->t_start[i]), "df_streamer_set_timing");
+            DF_HIP(hipEventCreate(&s->t_end[i]), "df_streamer_set_timing");
+        }
+    }
+    s->timing = on != 0;
+    return DF_OK;
+}
+
+extern "C" int df_streamer_copy_log(df_streamer_s* s, float* start_ms, float* end_ms, int capacity, int* count) {
+    clear_error();
+    DF_CHECK(s && count && (capacity == 0 || (start_ms && end_ms)), DF_ERR_INVALID,
+             "df_streamer_copy_log: NULL argument");
+    DF_CHECK(capacity >= 0, DF_ERR_INVALID, "df_streamer_copy_log: capacity < 0");
+    // every timed copy still in flight completes first, in load order
+    for (int j = 0; j < s->slots; ++j) {
+        const int k = (s->next + j) % s->slots;
+        if (int rc = log_slot(s, k, "df_streamer_copy_log")) return rc;
+    }
+    const int n = (int)s->log_start.size();
+    for (int i = 0; i < n && i < capacity; ++i) {
+        start_ms[i] = s->log_start[i];
+        end_ms[i] = s->log_end[i];
+    }
+    *count = n;
+    if (capacity >= n) {  // every entry handed out: start a new log
+        s->log_start.clear();
+        s->log_end.clear();
+        s->log_bytes.clear();
+        s->have_origin = false;
+    }
+    return DF_OK;
+}
+
 extern "C" int df_streamer_load(df_streamer_s* s, const void* host_src, size_t bytes, int* slot, void** dev_ptr) {
     clear_error();
     DF_CHECK(s && host_src && slot, DF_ERR_INVALID, "df_streamer_load: NULL argument");
@@ -168,10 +240,21 @@ extern "C" int df_streamer_load(df_streamer_s* s, const void* host_src, size_t b
         // this returns at once), one that did not is covered here
         DF_HIP(hipEventSynchronize(s->loaded[k]), "df_streamer_load");
     }
+    if (int rc = log_slot(s, k, "df_streamer_load")) return rc;
     uint8_t* dst = s->dev + (size_t)k * s->slot_bytes;
     hipStream_t cs = s->copy[s->loads++ & 1u];
+    if (s->timing) {
+        if (!s->have_origin) DF_HIP(hipEventRecord(s->t_origin, cs), "df_streamer_load");
+        s->have_origin = true;
+        DF_HIP(hipEventRecord(s->t_start[k], cs), "df_streamer_load");
+    }
     if (bytes) DF_HIP(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, cs), "df_streamer_load");
     DF_HIP(hipEventRecord(s->loaded[k], cs), "df_streamer_load");
+    if (s->timing) {
+        DF_HIP(hipEventRecord(s->t_end[k], cs), "df_streamer_load");
+        s->t_pending[k] = true;
+        s->t_bytes[k] = bytes;
+    }
     s->state[k] = kLoaded;
     s->next = (k + 1) % s->slots;
     *slot = k;

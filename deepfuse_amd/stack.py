@@ -14,8 +14,10 @@ Per layer and Linear, forward: absmax + 2-D quantize of the activation X
 (e4m3, the row copy and the transposed copy that this layer's dW reads) and
 Y = Xq . Wq^T * sx * sw + b; backward: absmax + 2-D quantize of the upstream
 gradient dY (e5m2, both copies, db fused), then dX and dW in one grouped
-launch (df_fp8_gemm_bwd).  Every layer reads the same seeded activations and
-gradients; the weights differ per layer.
+launch (df_fp8_gemm_bwd).  Every layer has its own seeded activations and
+gradients (made on the device from per-layer seeds: 183 MB of X and 236 MB
+of dY per layer at 8192 tokens), so no layer finds its inputs still in the
+256 MB Infinity Cache from another layer; the weights differ per layer too.
 
 Used by bench.py's streaming leg and by tests/test_gpu_stream.py, so the
 test runs exactly the launches the bench times.  torch is only the device
@@ -35,10 +37,12 @@ XL_LINEARS = [("qkv", 1600, 4800), ("attn_proj", 1600, 1600), ("fc", 1600, 6400)
 class StreamedStack:
     """The stack's weights (pinned host codes), inputs and output buffers.
 
-    keep_outputs=False (the bench): Y and dX of a Linear are overwritten by
-    every layer, dW is kept per layer.  keep_outputs=True (the tests): Y, dX
-    and dW are kept per layer, so a whole step can be compared afterwards.
-    out_dtype is the dtype of Y and dX (bf16 in the bench); dW is fp32."""
+    keep_outputs=False (the bench): Y and dX of a Linear and the row codes
+    of X and dY are overwritten by every layer; dW and the transposed X
+    codes (which dW reads in the backward sweep) are kept per layer.
+    keep_outputs=True (the tests): Y, dX, dW and every code buffer are kept
+    per layer, so a whole step can be compared afterwards.  out_dtype is the
+    dtype of Y and dX (bf16 in the bench); dW is fp32."""
 
     def __init__(self, torch, dev, layers=48, tokens=8192, linears=XL_LINEARS, keep_outputs=False,
                  out_dtype=None):
@@ -78,14 +82,24 @@ class StreamedStack:
     def weight_seed(self, l, i):
         return synth.SEED_BASE + 5000 + 10 * l + i
 
+    def act_seed(self, l, i):
+        return synth.SEED_BASE + 7000 + 10 * l + i
+
+    def grad_seed(self, l, i):
+        return synth.SEED_BASE + 9000 + 10 * l + i
+
+    def _normal_bf16(self, shape, std, seed):
+        """N(0, std) in bf16, generated on the device from `seed`."""
+        torch = self.torch
+        gen = torch.Generator(device=self.dev)
+        gen.manual_seed(seed)
+        return (torch.randn(shape, generator=gen, device=self.dev) * std).to(torch.bfloat16)
+
     def weight_bf16(self, l, i):
         """Layer l's Linear i weights W [N, K] (bf16, regenerated on the
         device from their seed)."""
-        torch = self.torch
         _, K, N = self.linears[i]
-        gen = torch.Generator(device=self.dev)
-        gen.manual_seed(self.weight_seed(l, i))
-        return (torch.randn((N, K), generator=gen, device=self.dev) * 0.02).to(torch.bfloat16)
+        return self._normal_bf16((N, K), 0.02, self.weight_seed(l, i))
 
     def _build(self):
         torch, dev, M = self.torch, self.dev, self.M
@@ -115,29 +129,35 @@ class StreamedStack:
         def to_bf16(a):
             return torch.from_numpy(synth.f32_to_bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
 
-        self.acts, self.grads, self.bias = [], [], []
-        for i, (_, K, N) in enumerate(self.linears):
-            seed = self.input_seed(i)
-            self.acts.append(to_bf16(synth.normal((M, K), 1.0, seed=seed)))
-            self.grads.append(to_bf16(synth.normal((M, N), 1e-3, seed=seed + 3)))
-            self.bias.append(to_bf16(synth.normal((N,), 0.02, seed=seed + 2)))
+        # per layer and Linear: its activation X ~ N(0, 1) and upstream
+        # gradient dY ~ N(0, 1e-3), bf16 (the bias is one per Linear)
+        self.acts = [[self._normal_bf16((M, K), 1.0, self.act_seed(l, i)) for i, (_, K, N) in enumerate(self.linears)]
+                     for l in range(self.layers)]
+        self.grads = [[self._normal_bf16((M, N), 1e-3, self.grad_seed(l, i))
+                       for i, (_, K, N) in enumerate(self.linears)] for l in range(self.layers)]
+        self.bias = [to_bf16(synth.normal((N,), 0.02, seed=self.input_seed(i) + 2))
+                     for i, (_, K, N) in enumerate(self.linears)]
         Mp = r16(M)
         self.Mp = Mp
         nl = self.layers if self.keep else 1
-        self.xq = [torch.empty((M, r16(K)), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
+        self.xq = [[torch.empty((M, r16(K)), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
+                   for _ in range(nl)]
         self.xt = [[torch.empty((K, Mp), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
                    for _ in range(self.layers)]
-        self.dyq = [torch.empty((M, r16(N)), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
-        self.dyt = [torch.empty((N, Mp), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
+        self.dyq = [[torch.empty((M, r16(N)), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
+                    for _ in range(nl)]
+        self.dyt = [[torch.empty((N, Mp), dtype=torch.uint8, device=dev) for _, K, N in self.linears]
+                    for _ in range(nl)]
         self.Y = [[torch.empty((M, N), dtype=self.out_dtype, device=dev) for _, K, N in self.linears]
                   for _ in range(nl)]
         self.dX = [[torch.empty((M, K), dtype=self.out_dtype, device=dev) for _, K, N in self.linears]
                    for _ in range(nl)]
         self.dW = [[torch.empty((N, K), dtype=torch.float32, device=dev) for _, K, N in self.linears]
                    for _ in range(self.layers)]
-        self.db = [torch.empty((N,), dtype=torch.float32, device=dev) for _, K, N in self.linears]
-        # per Linear: absmax X, scale X, absmax dY, scale dY
-        self.sc = torch.empty((L, 4), dtype=torch.float32, device=dev)
+        self.db = [[torch.empty((N,), dtype=torch.float32, device=dev) for _, K, N in self.linears]
+                   for _ in range(nl)]
+        # per layer and Linear: absmax X, scale X, absmax dY, scale dY
+        self.sc = torch.empty((self.layers, L, 4), dtype=torch.float32, device=dev)
         self.cws = torch.empty(max(lib().df_quantize_2d_workspace_bytes(M, N) for _, _, N in self.linears),
                                dtype=torch.uint8, device=dev)
         gws_b = max(max(lib().df_fp8_gemm_workspace_bytes(M, n, k), lib().df_fp8_gemm_bwd_workspace_bytes(M, n, k))
@@ -168,6 +188,11 @@ class StreamedStack:
     def sw_ptr(self, l, i):
         return self.sw.data_ptr() + 4 * (l * len(self.linears) + i)
 
+    def sc_ptr(self, l, i):
+        """Device address of layer l's Linear i scale record (absmax X,
+        scale X, absmax dY, scale dY)."""
+        return self.sc.data_ptr() + 16 * (l * len(self.linears) + i)
+
     def host_offset(self, l, direction):
         """Byte offset of layer l's codes (direction 0: W, 1: W^T) in host memory."""
         return (2 * l + direction) * self.blob
@@ -182,16 +207,16 @@ class StreamedStack:
         BF, E4 = int(DType.BFLOAT16), int(Fmt.E4M3)
         o = l if self.keep else 0
         for i, (_, K, N) in enumerate(self.linears):
-            s = self.sc[i].data_ptr()
-            x = self.acts[i]
+            s = self.sc_ptr(l, i)
+            x, xq = self.acts[l][i], self.xq[o][i]
             call("df_absmax_scale_bf16", x.data_ptr(), x.numel(), E4, s, s + 4, self.ws.data_ptr(), self.ws.numel(),
                  cur)
-            call("df_quantize_2d", BF, x.data_ptr(), M, K, K, E4, s + 4, self.xq[i].data_ptr(),
-                 self.xq[i].stride(0), self.xt[l][i].data_ptr(), self.Mp, cur)
+            call("df_quantize_2d", BF, x.data_ptr(), M, K, K, E4, s + 4, xq.data_ptr(), xq.stride(0),
+                 self.xt[l][i].data_ptr(), self.Mp, cur)
             Y = self.Y[o][i]
-            call("df_fp8_gemm_fwd", self.xq[i].data_ptr(), self.xq[i].stride(0), base + self.fwd_off[i],
-                 round16(K), M, N, K, s + 4, self.sw_ptr(l, i), BF, self.bias[i].data_ptr(), self._dt(Y),
-                 Y.data_ptr(), N, self.gws.data_ptr(), self.gws.numel(), cur)
+            call("df_fp8_gemm_fwd", xq.data_ptr(), xq.stride(0), base + self.fwd_off[i], round16(K), M, N, K, s + 4,
+                 self.sw_ptr(l, i), BF, self.bias[i].data_ptr(), self._dt(Y), Y.data_ptr(), N, self.gws.data_ptr(),
+                 self.gws.numel(), cur)
 
     def bwd_layer(self, l, base):
         """Backward of layer l with its W^T codes at device address `base`."""
@@ -199,32 +224,35 @@ class StreamedStack:
         BF, F32, E5 = int(DType.BFLOAT16), int(DType.FLOAT32), int(Fmt.E5M2)
         o = l if self.keep else 0
         for i, (_, K, N) in enumerate(self.linears):
-            s = self.sc[i].data_ptr()
-            g = self.grads[i]
+            s = self.sc_ptr(l, i)
+            g, dyq, dyt = self.grads[l][i], self.dyq[o][i], self.dyt[o][i]
             call("df_absmax_scale_bf16", g.data_ptr(), g.numel(), E5, s + 8, s + 12, self.ws.data_ptr(),
                  self.ws.numel(), cur)
-            call("df_quantize_2d_colsum", BF, g.data_ptr(), M, N, N, E5, s + 12, self.dyq[i].data_ptr(),
-                 self.dyq[i].stride(0), self.dyt[i].data_ptr(), self.Mp, self.db[i].data_ptr(),
-                 self.cws.data_ptr(), self.cws.numel(), cur)
-            # dX and dW in one launch; the activation scale of layer l's
-            # forward is the one cached with xt[l]: every layer quantizes the
-            # same activations, so sc[i][1] still holds it
+            call("df_quantize_2d_colsum", BF, g.data_ptr(), M, N, N, E5, s + 12, dyq.data_ptr(), dyq.stride(0),
+                 dyt.data_ptr(), self.Mp, self.db[o][i].data_ptr(), self.cws.data_ptr(), self.cws.numel(), cur)
+            # dX and dW in one launch; dW reads the transposed X codes that
+            # layer l's forward cached in xt[l], at that pass's scale s + 4
             dX = self.dX[o][i]
-            call("df_fp8_gemm_bwd", self.dyq[i].data_ptr(), self.dyq[i].stride(0), base + self.bwd_off[i],
-                 round16(N), self.dyt[i].data_ptr(), self.Mp, self.xt[l][i].data_ptr(), self.Mp, M, N, K, s + 12,
-                 self.sw_ptr(l, i), s + 4, self._dt(dX), dX.data_ptr(), K, F32, self.dW[l][i].data_ptr(), K,
-                 self.gws.data_ptr(), self.gws.numel(), cur)
+            call("df_fp8_gemm_bwd", dyq.data_ptr(), dyq.stride(0), base + self.bwd_off[i], round16(N), dyt.data_ptr(),
+                 self.Mp, self.xt[l][i].data_ptr(), self.Mp, M, N, K, s + 12, self.sw_ptr(l, i), s + 4, self._dt(dX),
+                 dX.data_ptr(), K, F32, self.dW[l][i].data_ptr(), K, self.gws.data_ptr(), self.gws.numel(), cur)
 
     # ------------------------------------------------------------- steps --
-    def streamed_step(self, streamer: WeightStreamer):
+    def streamed_step(self, streamer: WeightStreamer, micro_batches: int = 1):
         """One fwd+bwd step with the weights streamed through `streamer`
         (slots >= 3, slot_bytes >= self.blob).  The load of entry idx +
         slots - 2 is issued right after entry idx's launches: it blocks the
         host until entry idx - 2 has finished, so entries idx - 1 and idx
-        stay queued on the compute stream."""
+        stay queued on the compute stream.
+
+        micro_batches > 1: that many fwd+bwd passes back to back with the
+        same weights (gradient accumulation: the weights change only after
+        the last one), the loads running ahead across pass boundaries, so
+        the next pass's first W loads overlap this pass's backward.  Each
+        pass recomputes the same outputs here (same inputs)."""
         ahead = streamer.slots - 2
-        assert ahead >= 1
-        seq = self.seq
+        assert ahead >= 1 and micro_batches >= 1
+        seq = self.seq * micro_batches
         pending = [streamer.load(self.host_ptr + self.host_offset(ll, dd), self.blob) for dd, ll in seq[:ahead]]
         for idx, (d, l) in enumerate(seq):
             slot, base = pending.pop(0)

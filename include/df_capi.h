@@ -395,6 +395,18 @@ int df_streamer_slot(df_streamer* s, int slot, void** dev_ptr);
 /* copy stream `which` (0 or 1): load i is enqueued on copy stream i % 2, so
  * a caller that synchronizes with the copies needs both */
 int df_streamer_copy_stream(df_streamer* s, int which, void** stream);
+/* Timing of the copies (new; no counterpart in the reference): with timing
+ * on, each load records a HIP event on its copy stream right before and
+ * right after the copy.  df_streamer_copy_log waits for every timed copy,
+ * writes up to `capacity` (start, end) pairs in load order -- ms after an
+ * event recorded just before the first timed copy since the log was last
+ * read -- sets *count to the number logged, and clears the log when all of them
+ * fit in `capacity` (capacity 0: a query of the count).  A copy's
+ * start is when its copy stream reached it (the previous copy on that
+ * stream had finished); with two streams, two copies can share the link
+ * between those marks. */
+int df_streamer_set_timing(df_streamer* s, int on);
+int df_streamer_copy_log(df_streamer* s, float* start_ms, float* end_ms, int capacity, int* count);
 
 /* ---- consumer side of the fp32 gradients: global-norm clipping and Adam ----
  * Lists of fp32 tensors: the pointer arrays and `sizes` are HOST arrays of

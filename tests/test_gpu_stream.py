@@ -148,7 +148,8 @@ C5_LAYERS, C5_TOKENS, C5_SLOTS = 48, 8192, 6
 @pytest.fixture(scope="module")
 def config5(dev):
     """One streamed step and one resident step of the config-5 stack, every
-    layer's Y, dX (bf16, as the bench) and dW (fp32) kept from each."""
+    layer's Y, dX (bf16, as the bench) and dW (fp32) kept from each.  Each
+    layer has its own activations and gradients."""
     stack = StreamedStack(torch, dev, layers=C5_LAYERS, tokens=C5_TOKENS, keep_outputs=True)
     try:
         streamer = df.WeightStreamer(C5_SLOTS, stack.blob)
@@ -173,11 +174,36 @@ def test_config5_streamed_equals_resident(config5):
             assert torch.equal(Ys[l][i], stack.Y[l][i]), f"Y layer {l} {name}"
             assert torch.equal(dXs[l][i], stack.dX[l][i]), f"dX layer {l} {name}"
             assert torch.equal(dWs[l][i], stack.dW[l][i]), f"dW layer {l} {name}"
-    # dW = dY^T . X does not involve W, and every layer reads the same
-    # activations and gradients: equal across layers
-    for l in range(1, C5_LAYERS):
-        for i in range(len(stack.linears)):
-            assert torch.equal(dWs[l][i], dWs[0][i]), f"dW layer {l} differs from layer 0"
+    # the layers' inputs differ, so their dW do (dW = dY^T . X does not
+    # involve W; equal dW would mean the layers read the same inputs)
+    for i, (name, K, N) in enumerate(stack.linears):
+        assert not torch.equal(dWs[1][i], dWs[0][i]), f"dW of layers 0 and 1 equal ({name})"
+
+
+def test_config5_micro_batches_stream_across_passes(config5):
+    """Two passes with the same weights and the loads running ahead across
+    the pass boundary (stack.streamed_step(streamer, 2)), with copy timing
+    on: the outputs of the second pass are bit-identical to the resident
+    step's, and every one of the 2 x 96 copies is logged in load order."""
+    stack, _, _ = config5
+    ref = stack.new_outputs()  # the resident step's outputs
+    streamer = df.WeightStreamer(C5_SLOTS, stack.blob)
+    try:
+        streamer.set_timing(True)
+        stack.streamed_step(streamer, micro_batches=2)
+        torch.cuda.synchronize()
+        log = streamer.copy_log()
+        assert len(log) == 2 * len(stack.seq)
+        assert all(b >= a for a, b in log)
+        assert streamer.copy_log() == []  # the first read cleared it
+    finally:
+        streamer.close()
+    Ys, dXs, dWs = ref
+    for l in range(C5_LAYERS):
+        for i, (name, K, N) in enumerate(stack.linears):
+            assert torch.equal(Ys[l][i], stack.Y[l][i]), f"Y layer {l} {name}"
+            assert torch.equal(dXs[l][i], stack.dX[l][i]), f"dX layer {l} {name}"
+            assert torch.equal(dWs[l][i], stack.dW[l][i]), f"dW layer {l} {name}"
 
 
 def _bits(t):
@@ -209,19 +235,24 @@ def test_config5_layer_matches_oracle(config5, layer):
     sw = stack.sw.cpu().numpy()
     for i, (name, K, N) in enumerate(stack.linears):
         seed = stack.input_seed(i)
-        xb = synth.f32_to_bf16_bits(synth.normal((M, K), 1.0, seed=seed))
-        gb = synth.f32_to_bf16_bits(synth.normal((M, N), 1e-3, seed=seed + 3))
+        # this layer's own inputs (seeded on the device; the bf16 bits are
+        # the values every check below starts from)
+        xb = _bits(stack.acts[layer][i])
+        gb = _bits(stack.grads[layer][i])
         bb = synth.f32_to_bf16_bits(synth.normal((N,), 0.02, seed=seed + 2))
         wb = _bits(stack.weight_bf16(layer, i))
         s_x, s_dy, s_w = (orc.scale(orc.absmax(xb), orc.E4M3), orc.scale(orc.absmax(gb), orc.E5M2),
                           orc.scale(orc.absmax(wb), orc.E4M3))
-        assert (sc[i, 1], sc[i, 3], sw[layer, i]) == (np.float32(s_x), np.float32(s_dy), np.float32(s_w)), name
+        assert (sc[layer, i, 1], sc[layer, i, 3], sw[layer, i]) == \
+            (np.float32(s_x), np.float32(s_dy), np.float32(s_w)), name
         cx, cdy, cw = orc.quantize(xb, s_x, orc.E4M3), orc.quantize(gb, s_dy, orc.E5M2), orc.quantize(wb, s_w, orc.E4M3)
         r16 = df.round16
-        assert np.array_equal(stack.xq[i].cpu().numpy()[:, :K], cx), f"X codes {name}"
+        xq = stack.xq[layer][i]
+        assert np.array_equal(xq.cpu().numpy()[:, :K], cx), f"X codes {name}"
         assert np.array_equal(stack.xt[layer][i].cpu().numpy()[:, :M], np.ascontiguousarray(cx.T)), f"X^T {name}"
-        assert np.array_equal(stack.dyq[i].cpu().numpy()[:, :N], cdy), f"dY codes {name}"
-        assert np.array_equal(stack.dyt[i].cpu().numpy()[:, :M], np.ascontiguousarray(cdy.T)), f"dY^T {name}"
+        dyq = stack.dyq[layer][i]
+        assert np.array_equal(dyq.cpu().numpy()[:, :N], cdy), f"dY codes {name}"
+        assert np.array_equal(stack.dyt[layer][i].cpu().numpy()[:, :M], np.ascontiguousarray(cdy.T)), f"dY^T {name}"
         host = stack.host.numpy()
         fo = stack.host_offset(layer, 0) + stack.fwd_off[i]
         bo = stack.host_offset(layer, 1) + stack.bwd_off[i]
@@ -234,8 +265,8 @@ def test_config5_layer_matches_oracle(config5, layer):
         idx = _band_rows(M, seed)
         # Y: fp32 output of the same forward GEMM on the same codes
         Y32 = torch.empty((M, N), dtype=torch.float32, device=dev)
-        df.call("df_fp8_gemm_fwd", stack.xq[i].data_ptr(), stack.xq[i].stride(0),
-                dev_w.data_ptr() + fo, r16(K), M, N, K, stack.sc[i].data_ptr() + 4, stack.sw_ptr(layer, i),
+        df.call("df_fp8_gemm_fwd", xq.data_ptr(), xq.stride(0),
+                dev_w.data_ptr() + fo, r16(K), M, N, K, stack.sc_ptr(layer, i) + 4, stack.sw_ptr(layer, i),
                 int(df.DType.BFLOAT16), stack.bias[i].data_ptr(), int(df.DType.FLOAT32), Y32.data_ptr(), N,
                 stack.gws.data_ptr(), stack.gws.numel(), st)
         assert np.array_equal(_bits(Ys[layer][i]), synth.f32_to_bf16_bits(Y32.cpu().numpy())), f"Y bf16 {name}"
@@ -245,8 +276,8 @@ def test_config5_layer_matches_oracle(config5, layer):
         # dX: fp32 output of the dX GEMM (the grouped launch's dX is the
         # separate call's, bit for bit)
         dX32 = torch.empty((M, K), dtype=torch.float32, device=dev)
-        df.call("df_fp8_gemm_bwd_dx", stack.dyq[i].data_ptr(), stack.dyq[i].stride(0), dev_w.data_ptr() + bo,
-                r16(N), M, N, K, stack.sc[i].data_ptr() + 12, stack.sw_ptr(layer, i), int(df.DType.FLOAT32),
+        df.call("df_fp8_gemm_bwd_dx", dyq.data_ptr(), dyq.stride(0), dev_w.data_ptr() + bo,
+                r16(N), M, N, K, stack.sc_ptr(layer, i) + 12, stack.sw_ptr(layer, i), int(df.DType.FLOAT32),
                 dX32.data_ptr(), K, stack.gws.data_ptr(), stack.gws.numel(), st)
         assert np.array_equal(_bits(dXs[layer][i]), synth.f32_to_bf16_bits(dX32.cpu().numpy())), f"dX bf16 {name}"
         ref = orc.fc_backward_input(dYd[idx], Wd)
@@ -258,4 +289,4 @@ def test_config5_layer_matches_oracle(config5, layer):
         err = orc.rel_err(dWs[layer][i].cpu().numpy()[np.ix_(o_idx, i_idx)], refw)
         assert err <= 1e-4, f"layer {layer} {name} dW: {err:.3e}"
         # db from the same pass as the dY codes (fc_backward_bias, :91-106)
-        assert orc.rel_err(stack.db[i].cpu().numpy(), orc.fc_backward_bias(orc.bf16_to_f32(gb))) <= 1e-4
+        assert orc.rel_err(stack.db[layer][i].cpu().numpy(), orc.fc_backward_bias(orc.bf16_to_f32(gb))) <= 1e-4
