@@ -83,6 +83,8 @@ def parse():
                    help="run only the config-2 conversion leg and print its JSON (profiling runs)")
     p.add_argument("--config3-only", action="store_true",
                    help="run only the config-3 leg and print its JSON (profiling runs)")
+    p.add_argument("--tile-timeline", action="store_true",
+                   help="run only the per-tile timeline of the four config-4 forward GEMMs and print its JSON")
     p.add_argument("--summarize-profiles", action="store_true",
                    help="no GPU work: turn the rocprofv3 output of PROFILE_COMMANDS into the summaries under "
                         "profiles/")
@@ -160,6 +162,9 @@ def main():
         return
     if args.config3_only:
         print(json.dumps({"config3": config3_bench(torch, df, synth, dev, cur(), vendor=args.vendor_compare)}))
+        return
+    if args.tile_timeline:
+        print(json.dumps({"tile_timeline": tile_timeline_bench(torch, df, dev, cur())}))
         return
 
     def to_bf16(a):
@@ -487,6 +492,17 @@ PROFILE_COMMANDS = {
                        "--no-producer --no-delayed --no-config3"),
     "streaming": ("python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-optimizer "
                   "--no-producer --no-delayed --no-config3"),
+    "timeline": "python3 bench.py --tile-timeline",
+    "pmc_sq1": ("timeout -s KILL 180 rocprofv3 --pmc SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_LDS SQ_VALU_MFMA_BUSY_CYCLES --kernel-trace --output-format csv "
+                "-d gpurun_out/pmc_sq1 -o bench -- python3 bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph"),
+    "pmc_sq2": ("timeout -s KILL 180 rocprofv3 --pmc SQ_VMEM_TA_ADDR_FIFO_FULL SQ_VMEM_TA_CMD_FIFO_FULL SQ_LDS_BANK_CONFLICT SQ_LDS_DATA_FIFO_FULL SQ_INSTS_LDS SQ_WAIT_INST_LDS SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR --kernel-trace --output-format csv "
+                "-d gpurun_out/pmc_sq2 -o bench -- python3 bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph"),
+    "pmc_tatd": ("timeout -s KILL 180 rocprofv3 --pmc TA_TA_BUSY_sum TA_ADDR_STALLED_BY_TC_CYCLES_sum TD_TD_BUSY_sum TD_TC_STALL_sum GRBM_GUI_ACTIVE GRBM_COUNT --kernel-trace --output-format csv "
+                "-d gpurun_out/pmc_tatd -o bench -- python3 bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph"),
+    "pmc_tcp": ("timeout -s KILL 180 rocprofv3 --pmc TCP_PENDING_STALL_CYCLES_sum TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum TCP_UTCL1_TRANSLATION_MISS_sum TCC_HIT_sum TCC_MISS_sum --kernel-trace --output-format csv "
+                "-d gpurun_out/pmc_tcp -o bench -- python3 bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph"),
+    "pmc_ea": ("timeout -s KILL 180 rocprofv3 --pmc TCC_EA0_WRREQ_sum TCC_EA0_RDREQ_sum TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum --kernel-trace --output-format csv "
+                "-d gpurun_out/pmc_ea -o bench -- python3 bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph"),
     "stats_producer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_producer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-optimizer --no-delayed --no-config3"),
@@ -650,6 +666,10 @@ def summarize_profiles():
         extra.append(fname)
     if streaming_summary(out_dir, prof):
         extra.append("streaming_config5.md")
+    if timeline_summary(out_dir, prof):
+        extra.append("gemm_tile_timeline_config4.md")
+    if limiter_summary(out_dir, prof):
+        extra.append("limiters_config4.md")
     if config3_summary(out_dir, prof):
         extra.append("gemm_config3_kernels.md")
     print(f"wrote profiles/ summaries ({len(rows)} kernels, traffic families {sorted(fams)}, extra {extra})")
@@ -876,6 +896,112 @@ def streaming_summary(out_dir, prof):
         lines.append(f"| {name} | {c['copies']} | {c['median_copy_ms']} ms | {c['median_copy_gbs']} GB/s | "
                      f"{c['sum_copy_ms']} ms | {c['busy_ms']} ms | {c['busy_gbs']} GB/s | {c['copies_in_flight_avg']} |")
     with open(os.path.join(prof, "streaming_config5.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return True
+
+
+def timeline_summary(out_dir, prof):
+    """profiles/gemm_tile_timeline_config4.md from the timeline run's JSON
+    (gpurun_out/prof_timeline.log, the stdout of PROFILE_COMMANDS["timeline"])."""
+    log = os.path.join(out_dir, "prof_timeline.log")
+    if not os.path.exists(log):
+        return False
+    line = [l for l in open(log) if l.startswith('{"tile_timeline"')]
+    if not line:
+        return False
+    tl = json.loads(line[-1])["tile_timeline"]
+    lines = ["# Per-tile timeline of the persistent GEMM -- config-4 forward GEMMs (M = 16384, bf16 bias and output)",
+             "", "Command (from the repository root, on one MI355X; stdout to gpurun_out/prof_timeline.log):", "",
+             "    " + PROFILE_COMMANDS["timeline"], "",
+             "df_fp8_gemm_fwd_timeline runs the forward's persistent kernel with wave 0 of every block stamping the "
+             "GPU's 100 MHz real-time counter at the block's start and at each of its tiles' start, epilogue start "
+             "and epilogue end (the shortest of three runs per shape).  Main loop = a tile's DMA steps and MFMAs "
+             "(the next tile's first two DMA steps are issued inside it); epilogue = scale, bias, bf16 conversion, "
+             "LDS slab passes and stores; gap = epilogue end to the next tile's start; prologue = block start to "
+             "its first tile.  Medians over tiles or blocks, microseconds.", "",
+             "| GEMM | N | K | K steps | tiles / blocks | main loop | per K step | epilogue | gap | epilogue share "
+             "| block prologue | first / last block end | kernel span |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for name, d in tl["shapes"].items():
+        lines.append(f"| {name} | {d['N']} | {d['K']} | {d['k_steps']} | {d['tiles']} / {d['blocks']} | "
+                     f"{d['tile_main_loop_us']} | {d['main_loop_per_k_step_us']} | {d['tile_epilogue_us']} | "
+                     f"{d['gap_to_next_tile_us']} | {d['epilogue_share_of_tile']} | {d['block_prologue_us']} | "
+                     f"{d['block_end_first_us']} / {d['block_end_last_us']} | {d['kernel_span_us']} |")
+    with open(os.path.join(prof, "gemm_tile_timeline_config4.md"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return True
+
+
+# kernel families of the limiter summary: (label, kernel name prefix)
+LIMITER_KERNELS = (
+    ("gemm_fwd", "void dfk::gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true, false, void>"),
+    ("gemm_bwd (dW unsplit)", "void dfk::gemm_nt_persistent_kernel<1, 0, float, float, false, false, unsigned short>"),
+    ("quantize X", "void dfk::quantize_2d_kernel<unsigned short, 0, false, true, false, false>"),
+    ("quantize dY + db", "void dfk::quantize_2d_kernel<unsigned short, 1, true, true, false, false>"),
+)
+
+
+def limiter_summary(out_dir, prof):
+    """profiles/limiters_config4.md from the pmc_* runs: per kernel family,
+    counter averages per dispatch and the fractions that name what bounds
+    it.  Normalisation: cycles per dispatch = GRBM_GUI_ACTIVE / 8 (one count
+    per XCD); per-CU blocks (TA, TD, TCP) over 256 CUs, L2 channels (TCC)
+    over 8 x 16; SQ wave counters as fractions of SQ_WAVE_CYCLES."""
+    import csv
+
+    vals = {}
+    for key in ("sq1", "sq2", "tatd", "tcp", "ea"):
+        path = os.path.join(out_dir, "pmc_" + key, "bench_counter_collection.csv")
+        if not os.path.exists(path):
+            return False
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                for label, pre in LIMITER_KERNELS:
+                    if r["Kernel_Name"].startswith(pre):
+                        vals.setdefault(label, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    avg = {lab: {c: sum(v) / len(v) for c, v in d.items()} for lab, d in vals.items()}
+    labs = [lab for lab, _ in LIMITER_KERNELS if lab in avg]
+    lines = ["# What bounds the config-4 GEMM main loop and 2-D quantize -- rocprofv3 counters", "",
+             "Commands (five counter runs of the same eager config-4 steps, from the repository root):", ""]
+    lines += ["    " + PROFILE_COMMANDS["pmc_" + k] for k in ("sq1", "sq2", "tatd", "tcp", "ea")]
+    lines += ["", "Kernels: " + "; ".join(f"{lab} = `{pre[len('void dfk::'):]}`" for lab, pre in LIMITER_KERNELS
+                                          if lab in avg) + ".",
+              "", "Per kernel family, averages per dispatch.  cycles = GRBM_GUI_ACTIVE / 8; per-CU fractions divide "
+              "the counter's sum over the 256 CUs by 256 x cycles; L2 fractions divide by 128 channels x cycles; "
+              "wave fractions divide by SQ_WAVE_CYCLES.", "",
+              "| quantity | " + " | ".join(labs) + " |", "|---|" + "---|" * len(labs)]
+
+    def row(name, fn, fmt="{:.3f}"):
+        cells = []
+        for lab in labs:
+            try:
+                cells.append(fmt.format(fn(avg[lab])))
+            except (KeyError, ZeroDivisionError, TypeError):
+                cells.append("-")
+        lines.append(f"| {name} | " + " | ".join(cells) + " |")
+
+    cyc = lambda a: a["GRBM_GUI_ACTIVE"] / 8
+    row("cycles per dispatch", cyc, "{:.0f}")
+    row("MFMA busy (of 1024 SIMDs)", lambda a: a["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc(a) * 1024))
+    row("waves waiting on a dependency (s_waitcnt, barrier)", lambda a: a["SQ_WAIT_ANY"] / a["SQ_WAVE_CYCLES"])
+    row("waves with an instruction ready but not issued", lambda a: a["SQ_WAIT_INST_ANY"] / a["SQ_WAVE_CYCLES"])
+    row("VMEM issue blocked: TA command FIFO full (per CU)", lambda a: a["SQ_VMEM_TA_CMD_FIFO_FULL"] / (256 * cyc(a)))
+    row("VMEM issue blocked: TA address FIFO full (per CU)", lambda a: a["SQ_VMEM_TA_ADDR_FIFO_FULL"] / (256 * cyc(a)))
+    row("TA busy", lambda a: a["TA_TA_BUSY_sum"] / (256 * cyc(a)))
+    row("TD busy", lambda a: a["TD_TD_BUSY_sum"] / (256 * cyc(a)))
+    row("TD stalled on the L1 (TC)", lambda a: a["TD_TC_STALL_sum"] / (256 * cyc(a)))
+    row("L1 (TCP) stalled on data pending from L2", lambda a: a["TCP_PENDING_STALL_CYCLES_sum"] / (256 * cyc(a)))
+    row("L2 read latency seen by L1 (cycles)",
+        lambda a: a["TCP_TCC_READ_REQ_LATENCY_sum"] / a["TCP_TCC_READ_REQ_sum"], "{:.0f}")
+    row("L2 hit rate", lambda a: a["TCC_HIT_sum"] / (a["TCC_HIT_sum"] + a["TCC_MISS_sum"]))
+    row("TLB (UTCL1) misses per dispatch", lambda a: a["TCP_UTCL1_TRANSLATION_MISS_sum"], "{:.0f}")
+    row("LDS bank-conflict cycles per LDS instruction", lambda a: a["SQ_LDS_BANK_CONFLICT"] / a["SQ_INSTS_LDS"])
+    row("DRAM read credit stall (per L2 channel)", lambda a: a["TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum"] / (128 * cyc(a)))
+    row("DRAM write credit stall (per L2 channel)",
+        lambda a: a["TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum"] / (128 * cyc(a)))
+    row("fabric read requests per dispatch", lambda a: a["TCC_EA0_RDREQ_sum"], "{:.0f}")
+    row("fabric write requests per dispatch", lambda a: a["TCC_EA0_WRREQ_sum"], "{:.0f}")
+    with open(os.path.join(prof, "limiters_config4.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
     return True
 
@@ -1462,6 +1588,84 @@ def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
     return res
 
 
+def tile_timeline_bench(torch, df, dev, stream, M=M_TOKENS, reps=3):
+    """Where a persistent-kernel tile's time goes: the four config-4 forward
+    GEMMs (bf16 bias and output) through df_fp8_gemm_fwd_timeline, the same
+    kernel body with wave 0 of every block stamping the 100 MHz real-time
+    counter at the block's start and at each tile's start, epilogue start
+    and epilogue end.  Operands: device-seeded X ~ N(0, 1), W ~ N(0, 0.02)
+    codes.  Per shape (the run with the shortest kernel span of `reps`):
+    per tile, the main loop (its DMA steps and MFMAs), the epilogue and the
+    gap to the block's next tile; per block, the prologue (start to first
+    tile) and the end; the main loop per 128-byte K step."""
+    import ctypes
+
+    gen = torch.Generator(device=dev)
+    out = {"clock": "s_memrealtime, 100 MHz", "M": M, "shapes": {}}
+    for i, (name, K, N) in enumerate(XL_LINEARS):
+        gen.manual_seed(8100 + i)
+        X = (torch.randn((M, K), generator=gen, device=dev)).to(torch.bfloat16)
+        W = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        b = (torch.randn((N,), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        _, sx = df.absmax_scale(X, df.Fmt.E4M3)
+        _, sw = df.absmax_scale(W, df.Fmt.E4M3)
+        xq, _ = df.quantize_2d(X, sx, df.Fmt.E4M3, want_qt=False)
+        wq, _ = df.quantize_2d(W, sw, df.Fmt.E4M3, want_qt=False)
+        del X, W
+        Y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        tiles = ((M + 255) // 256) * ((N + 255) // 256)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        spb = 1 + 3 * -(-tiles // cus)  # the kernel's grid is min(tiles, CUs)
+        stamps = torch.zeros(cus * spb, dtype=torch.int64, device=dev)
+        grid = ctypes.c_int()
+        best = None
+        for _ in range(reps + 1):
+            stamps.zero_()
+            df.call("df_fp8_gemm_fwd_timeline", xq.data_ptr(), xq.stride(0), wq.data_ptr(), wq.stride(0), M, N, K,
+                    sx.data_ptr(), sw.data_ptr(), b.data_ptr(), Y.data_ptr(), N, stamps.data_ptr(), spb,
+                    ctypes.byref(grid), stream)
+            torch.cuda.synchronize()
+            st = stamps[:grid.value * spb].view(grid.value, spb).cpu().numpy().astype("int64")
+            span = int(st[st > 0].max() - st[:, 0].min())
+            if best is None or span < best[0]:
+                best = (span, st)
+        span, st = best
+        us = 0.01  # one tick = 10 ns
+        nk = -(-K // 128)
+        main, epi, gap, pro, ends = [], [], [], [], []
+        t0 = st[:, 0].min()
+        for blk in st:
+            ntl = 0
+            while 3 + 3 * ntl < spb and blk[1 + 3 * ntl] > 0:
+                ntl += 1
+            if ntl == 0:
+                continue
+            pro.append((blk[1] - blk[0]) * us)
+            for t in range(ntl):
+                s0, e0, e1 = blk[1 + 3 * t], blk[2 + 3 * t], blk[3 + 3 * t]
+                main.append((e0 - s0) * us)
+                epi.append((e1 - e0) * us)
+                if t + 1 < ntl:
+                    gap.append((blk[4 + 3 * t] - e1) * us)
+            ends.append((blk[3 * ntl] - t0) * us)
+
+        def med(v):
+            v = sorted(v)
+            return round(v[len(v) // 2], 3) if v else None
+
+        out["shapes"][name] = {
+            "N": N, "K": K, "k_steps": nk, "tiles": tiles, "blocks": grid.value,
+            "kernel_span_us": round(span * us, 2),
+            "tile_main_loop_us": med(main), "tile_epilogue_us": med(epi), "gap_to_next_tile_us": med(gap),
+            "main_loop_per_k_step_us": round(med(main) / nk, 3) if main else None,
+            "block_prologue_us": med(pro), "block_end_first_us": round(min(ends), 2),
+            "block_end_last_us": round(max(ends), 2),
+            "epilogue_share_of_tile": round(med(epi) / (med(main) + med(epi) + (med(gap) or 0.0)), 4),
+        }
+        del xq, wq, Y, stamps
+    return out
+
+
 def _copy_stats(log, nbytes):
     """Summary of a streamer copy log [(start, end) ms]: per-copy duration
     (its copy stream reaching it to its end), time the link was busy (union
@@ -1649,8 +1853,11 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
             "bound": "pcie" if h2d_ms > compute_ms else "compute",
             "overlap": round(max(h2d_ms, compute_ms) / stream_ms, 4),
             "flowshop_bound_ms": round(bound_ms, 3), "overlap_vs_flowshop_bound": round(bound_ms / stream_ms, 4),
+            "overlap_vs_compute_under_copies": round(max(h2d_ms, under_copies_ms) / stream_ms, 4),
             "steady_state": {"micro_batches": micro_batches, "slots": steady_slots,
                              "ms_per_pass": round(mb_ms / micro_batches, 3),
+                             "overlap_vs_compute_under_copies": round(max(h2d_ms, under_copies_ms) /
+                                                                      (mb_ms / micro_batches), 4),
                              "tflops": round(step_flops / (mb_ms / micro_batches * 1e-3) / 1e12, 2),
                              "overlap": round(max(h2d_ms, compute_ms) / (mb_ms / micro_batches), 4),
                              "note": "passes with the same weights (gradient accumulation), loads running ahead "

@@ -92,6 +92,8 @@ _SIGS = {
     "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_nt_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_sz, _vp, _vp]),
+    "df_fp8_gemm_fwd_timeline": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
+                                          _c_int, _vp, _c_int, ctypes.POINTER(_c_int), _vp]),
     "df_fp8_gemm_fwd": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                  _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_bwd_dx": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,

@@ -526,11 +526,18 @@ template <typename T> struct Tag { using type = T; };
 // and 128 B rows, so each wave issues two B instructions instead of four.
 // For outputs whose 256x256 tiles would leave CUs idle or a last round
 // mostly empty (the plan below compares both).
-template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT, typename OutT1, bool NARROW>
+// TIMELINE (a diagnostic instantiation, df_fp8_gemm_fwd_timeline): lane 0
+// of wave 0 writes the 100 MHz real-time counter to tl[block][...] at the
+// block's start ([0]) and, for its tile t, at the tile's first half-step
+// ([1 + 3t]), before its epilogue ([2 + 3t]) and after it ([3 + 3t]), while
+// 1 + 3t + 2 < tl_per_block; every other instantiation compiles none of it.
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT, typename OutT1, bool NARROW,
+          bool TIMELINE = false>
 __device__ __forceinline__ void persistent_body(
     const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
     const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
-    OutT* __restrict__ C, int ldc, int vec_out, int ksteps, int nsplit, const PProb& p1) {
+    OutT* __restrict__ C, int ldc, int vec_out, int ksteps, int nsplit, const PProb& p1,
+    uint64_t* __restrict__ tl = nullptr, int tl_per_block = 0) {
     constexpr bool GROUPED = !std::is_void<OutT1>::value;
     static_assert(!NARROW || (!GROUPED && !SPLIT), "narrow tiles: one problem, unsplit");
     using Out1 = typename std::conditional<GROUPED, OutT1, OutT>::type;
@@ -555,6 +562,16 @@ __device__ __forceinline__ void persistent_body(
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = NARROW ? w >> 1 : w >> 2, wn = NARROW ? w & 1 : w & 3;
+    // a stamp of the real-time counter (TIMELINE only; a vector store)
+    auto stamp = [&](int idx) {
+        if constexpr (TIMELINE) {
+            if (w == 0 && idx < tl_per_block) {
+                const uint64_t t = __builtin_amdgcn_s_memrealtime();
+                if (lane == 0) tl[(int64_t)blockIdx.x * tl_per_block + idx] = t;
+            }
+        }
+    };
+    stamp(0);
     uint8_t* const slab = lds + 2 * kPStage + kPBiasSlots * kPBiasSlot + w * SLAB;
     // a 2-byte bias of odd length: its last element, which the dword bias DMA
     // cannot deliver (it shares a dword with the end of the buffer), read
@@ -976,13 +993,16 @@ __device__ __forceinline__ void persistent_body(
     for (int tile = 0; tile < my_tiles; ++tile) {
         int up, um0, un0, ukb, unku, uslot;
         tile_mn(tile, up, um0, un0, ukb, unku, uslot);
+        stamp(1 + 3 * tile);
         half(Z{}, EVEN{}, fa0, fb0, fa1, fb1);
         half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
         for (int k = 1; k < unku; ++k) {
             half(NZ{}, EVEN{}, fa0, fb0, fa1, fb1);
             half(NZ{}, ODD{}, fa1, fb1, fa0, fb0);
         }
+        stamp(2 + 3 * tile);
         epilogue(tile);
+        stamp(3 + 3 * tile);
     }
     __builtin_amdgcn_s_waitcnt(0);  // every DMA has landed before the block's LDS is released
 }
@@ -994,6 +1014,16 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_kernel(
     OutT* __restrict__ C, int ldc, int vec_out, int ksteps = 0, int nsplit = 1, PProb p1 = {}) {
     persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, SPLIT, OutT1, false>(A, lda, B, ldb, M, N, K, sa, sb, bias, C,
                                                                         ldc, vec_out, ksteps, nsplit, p1);
+}
+
+// The forward kernel with the per-tile timeline (df_fp8_gemm_fwd_timeline).
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_timeline_kernel(
+    const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
+    const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
+    OutT* __restrict__ C, int ldc, int vec_out, uint64_t* __restrict__ tl, int tl_per_block) {
+    persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, false, void, false, true>(
+        A, lda, B, ldb, M, N, K, sa, sb, bias, C, ldc, vec_out, 0, 1, PProb{}, tl, tl_per_block);
 }
 
 template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
@@ -1481,6 +1511,29 @@ extern "C" int df_fp8_gemm_fwd(const uint8_t* Xq, int ldx, const uint8_t* Wq, in
                                size_t ws_bytes, void* stream) {
     return df_fp8_gemm_nt(DF_FMT_E4M3, Xq, ldx, DF_FMT_E4M3, Wq, ldw, M, N, K, sx_dev, sw_dev,
                           bias_dtype, bias, y_dtype, Y, ldy, ws, ws_bytes, stream);
+}
+
+extern "C" int df_fp8_gemm_fwd_timeline(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw, int M, int N, int K,
+                                        const float* sx_dev, const float* sw_dev, const uint16_t* bias_bf16,
+                                        uint16_t* Y_bf16, int ldy, uint64_t* stamps, int stamps_per_block,
+                                        int* grid_out, void* stream) {
+    clear_error();
+    GemmArgs g;
+    bool empty = false;
+    const int st = nt_args("df_fp8_gemm_fwd_timeline", DF_FMT_E4M3, Xq, ldx, DF_FMT_E4M3, Wq, ldw, M, N, K, sx_dev,
+                           sw_dev, DF_DTYPE_BFLOAT16, bias_bf16, DF_DTYPE_BFLOAT16, Y_bf16, ldy, nullptr, 0, stream, g,
+                           empty);
+    if (st != DF_OK) return st;
+    DF_CHECK(!empty && bias_bf16 && stamps && grid_out && stamps_per_block >= 1, DF_ERR_INVALID,
+             "df_fp8_gemm_fwd_timeline: needs M, N > 0, a bias, a stamp buffer and grid_out");
+    const NtPlan p = nt_plan(g);
+    DF_CHECK(p.kind == DF_GEMM_KERNEL_PERSISTENT && p.split == 1, DF_ERR_UNSUPPORTED,
+             "df_fp8_gemm_fwd_timeline: M=%d N=%d K=%d does not run the unsplit 256x256 persistent kernel", M, N, K);
+    *grid_out = p.grid;
+    gemm_nt_persistent_timeline_kernel<E4M3, E4M3, uint16_t, uint16_t, true><<<p.grid, 512, 0, g.st>>>(
+        g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, bias_bf16, Y_bf16, g.ldc,
+        epi_store_mode(g.C, (int64_t)g.ldc * 2), stamps, stamps_per_block);
+    return launch_status("df_fp8_gemm_fwd_timeline");
 }
 
 extern "C" int df_fp8_gemm_bwd_dx(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, int M,

@@ -321,6 +321,18 @@ int df_fp8_gemm_fwd(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw,
                     int M, int N, int K, const float* sx_dev, const float* sw_dev,
                     int bias_dtype, const void* bias, int y_dtype, void* Y, int ldy,
                     void* ws, size_t ws_bytes, void* stream);
+/* The forward above on its unsplit 256x256 persistent kernel, bf16 bias
+ * and bf16 Y only, with a per-tile timeline (diagnostic; no counterpart in
+ * the reference): stamps[b * stamps_per_block + i] gets the GPU's 100 MHz
+ * real-time counter for block b at its start (i = 0) and, for its t-th
+ * tile, at the tile's first half-step (1 + 3t), before its epilogue
+ * (2 + 3t) and after it (3 + 3t), as far as stamps_per_block reaches;
+ * *grid_out = the blocks launched.  Y is the forward's Y.  Shapes whose plan
+ * is not that kernel are DF_ERR_UNSUPPORTED. */
+int df_fp8_gemm_fwd_timeline(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw, int M, int N, int K,
+                             const float* sx_dev, const float* sw_dev, const uint16_t* bias_bf16,
+                             uint16_t* Y_bf16, int ldy, uint64_t* stamps, int stamps_per_block,
+                             int* grid_out, void* stream);
 /* dX[M,K] = dY_q[M,N] . W[N,K]  (e5m2 x e4m3), given W^T quantized as
  * Wt_q[K, ldwt] (df_quantize_2d's qt).  Replaces fc_backward_input
  * (fully_connected_layer.cu:43-65). */
