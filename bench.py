@@ -487,6 +487,9 @@ PROFILE_COMMANDS = {
              "SQ_INSTS_VALU_MFMA_MOPS_F8 --kernel-trace --output-format csv -d gpurun_out/pmc_mfma -o bench -- "
              "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming --no-optimizer "
              "--no-producer --no-delayed --no-config3 --no-graph"),
+    "mfma_config3": ("timeout -s KILL 180 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES "
+                     "SQ_INSTS_VALU_MFMA_MOPS_F8 --kernel-trace --output-format csv -d gpurun_out/pmc_mfma_config3 "
+                     "-o bench -- python3 bench.py --config3-only"),
     "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-producer --no-delayed --no-config3"),
@@ -647,6 +650,11 @@ def summarize_profiles():
         extra.append("conversion_config2_kernels.md")
     if mfma_summary(out_dir, prof):
         extra.append("gemm_mfma_busy_config4.md")
+    if mfma_summary(out_dir, prof, key="mfma_config3", out_name="gemm_mfma_busy_config3.md",
+                    title="MFMA busy and shader clock of the config-3 GEMMs (GPT-2 small, M = 8192, forward)",
+                    what="The config-3 leg: each Linear's GEMM 1 + 20 times back to back, eager, counters per "
+                         "dispatch (the kernels run one at a time under counter collection)."):
+        extra.append("gemm_mfma_busy_config3.md")
     for key, sub, fname, title, keep in EXTRA_STATS:
         path = os.path.join(out_dir, sub, "bench_kernel_stats.csv")
         if not os.path.exists(path):
@@ -786,23 +794,26 @@ def config3_summary(out_dir, prof):
     return True
 
 
-def mfma_summary(out_dir, prof):
-    """profiles/gemm_mfma_busy_config4.md from the mfma counter run: per
-    GEMM dispatch of the config-4 step, MFMA-busy cycles over the SIMDs'
-    available cycles, and the shader clock the run held.  GRBM_GUI_ACTIVE
-    as collected is the sum over the 8 XCDs (each counts GPU-busy cycles at
-    the shader clock), so busy cycles per XCD = GRBM_GUI_ACTIVE / 8; the
-    1024 SIMDs (256 CUs x 4) each have that many cycles available."""
+def mfma_summary(out_dir, prof, key="mfma", out_name="gemm_mfma_busy_config4.md",
+                 title="MFMA busy and shader clock of the config-4 GEMMs",
+                 what="Two eager config-4 steps after one warm-up."):
+    """profiles/gemm_mfma_busy_config4.md (or, key="mfma_config3", the
+    config-3 file) from an mfma counter run: per GEMM dispatch, MFMA-busy
+    cycles over the SIMDs' available cycles, and the shader clock the run
+    held.  GRBM_GUI_ACTIVE as collected is the sum over the 8 XCDs (each
+    counts GPU-busy cycles at the shader clock), so busy cycles per XCD =
+    GRBM_GUI_ACTIVE / 8; the 1024 SIMDs (256 CUs x 4) each have that many
+    cycles available."""
     import csv
 
-    path = os.path.join(out_dir, "pmc_mfma", "bench_counter_collection.csv")
-    kt_path = os.path.join(out_dir, "pmc_mfma", "bench_kernel_trace.csv")
+    path = os.path.join(out_dir, "pmc_" + key, "bench_counter_collection.csv")
+    kt_path = os.path.join(out_dir, "pmc_" + key, "bench_kernel_trace.csv")
     if not os.path.exists(path):
         return False
     per = {}
     with open(path) as fh:
         for r in csv.DictReader(fh):
-            if "gemm_nt_persistent_kernel" not in r["Kernel_Name"]:
+            if "gemm_nt_persistent" not in r["Kernel_Name"]:
                 continue
             e = per.setdefault(r["Dispatch_Id"], {"name": _short_kernel(r["Kernel_Name"]),
                                                   "full": r["Kernel_Name"], "grid": int(r["Grid_Size"])})
@@ -813,15 +824,15 @@ def mfma_summary(out_dir, prof):
             for r in csv.DictReader(fh):
                 if r["Dispatch_Id"] in per:
                     per[r["Dispatch_Id"]]["t"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-    lines = ["# rocprofv3: MFMA busy and shader clock of the config-4 GEMMs", "",
-             "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS["mfma"], "",
-             "Two eager config-4 steps after one warm-up.  Per dispatch: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+    lines = ["# rocprofv3: " + title, "",
+             "Command (from the repository root, on one MI355X):", "", "    " + PROFILE_COMMANDS[key], "",
+             what + "  Per dispatch: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
              "(GRBM_GUI_ACTIVE / 8 x 1024 SIMDs); clock = GRBM_GUI_ACTIVE / 8 / duration; fp8 flop = "
              "SQ_INSTS_VALU_MFMA_MOPS_F8 x 512 (the MFMA work issued, padding of partial tiles included).  "
              "`<A fmt, B fmt, out, bias type, bias, split, dX out>`: `<0, 0, ...>` forward, `<1, 0, ..., void>` "
              "dX alone, the last argument non-void the grouped dX + dW launch.", "",
-             "| kernel | grid | us | clock GHz | MFMA busy | issued fp8 TFLOP | TFLOP/s issued |",
-             "|---|---|---|---|---|---|---|"]
+             "| kernel | grid | us | clock GHz | MFMA busy | issued fp8 TFLOP | TFLOP/s issued | issued / 5.0 PF |",
+             "|---|---|---|---|---|---|---|---|"]
     # one row per distinct GEMM (kernel and issued work), medians over its dispatches
     groups = {}
     for did in sorted(per, key=int):
@@ -831,8 +842,10 @@ def mfma_summary(out_dir, prof):
             continue
         tmpl = e["full"][e["full"].find("<"):e["full"].find(">(") + 1] if "<" in e["full"] else ""
         tfl = e.get("SQ_INSTS_VALU_MFMA_MOPS_F8", 0.0) * 512 / 1e12
-        g = groups.setdefault((tmpl, round(tfl, 4)), {"grid": e["grid"] // 512, "t": [], "clk": [], "busy": [],
-                                                      "cyc": [], "bcyc": []})
+        g = groups.setdefault((tmpl, round(tfl, 4), e["grid"]), {"grid": e["grid"] // 512, "t": [], "clk": [], "busy": [],
+                                                      "cyc": [], "bcyc": [],
+                                                      "kname": "gemm_nt_persistent_narrow_kernel"
+                                                      if "narrow" in e["name"] else "gemm_nt_persistent_kernel"})
         g["t"].append(e["t"])
         g["clk"].append(gui / e["t"])
         g["busy"].append(e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui * 1024))
@@ -840,15 +853,23 @@ def mfma_summary(out_dir, prof):
         g["bcyc"].append(e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0))
     med = lambda v: sorted(v)[len(v) // 2]
     tot_b = tot_c = 0.0
-    for (tmpl, tfl), g in groups.items():
+    fast_clock = False
+    for (tmpl, tfl, _), g in groups.items():
         t = med(g["t"])
         tot_b += sum(g["bcyc"])
         tot_c += sum(g["cyc"])
-        lines.append(f"| `gemm_nt_persistent_kernel{tmpl}` (x{len(g['t'])}) | {g['grid']} | {t / 1e3:.1f} | "
-                     f"{med(g['clk']):.2f} | {med(g['busy']):.3f} | {tfl:.3f} | {tfl / (t * 1e-9):.0f} |")
+        fast_clock |= med(g["clk"]) > 2.45
+        lines.append(f"| `{g['kname']}{tmpl}` (x{len(g['t'])}) | {g['grid']} | {t / 1e3:.1f} | "
+                     f"{med(g['clk']):.2f} | {med(g['busy']):.3f} | {tfl:.3f} | {tfl / (t * 1e-9):.0f} | "
+                     f"{tfl / (t * 1e-9) / FP8_PEAK_TFLOPS:.3f} |")
     if tot_c:
         lines += ["", f"All GEMM dispatches together: MFMA busy {tot_b / tot_c:.3f} of the SIMD cycles they held."]
-    with open(os.path.join(prof, "gemm_mfma_busy_config4.md"), "w") as fh:
+    if fast_clock:
+        lines += ["", "Some dispatches read a clock above the part's 2.4 GHz maximum: for dispatches this short the "
+                      "busy window GRBM_GUI_ACTIVE counts under counter collection is longer than the kernel's own "
+                      "duration, so their clock and MFMA-busy columns are not reliable; the issued rate (fp8 work "
+                      "issued over the kernel's duration) against the 5.0 PF peak is."]
+    with open(os.path.join(prof, out_name), "w") as fh:
         fh.write("\n".join(lines) + "\n")
     return True
 
