@@ -533,14 +533,20 @@ TRAFFIC_FAMILIES = {
 
 
 def _tree_id():
-    """The git commit of this tree (with -dirty for uncommitted changes),
-    recorded beside profile summaries; None outside a git checkout."""
+    """The git commit of this tree, with -dirty when files outside profiles/
+    (the summaries being written) differ from it; recorded beside profile
+    summaries.  None outside a git checkout."""
     import subprocess
 
+    root = os.path.dirname(os.path.abspath(__file__))
     try:
-        r = subprocess.run(["git", "describe", "--always", "--dirty", "--abbrev=12"], capture_output=True, text=True,
-                           cwd=os.path.dirname(os.path.abspath(__file__)), timeout=20)
-        return r.stdout.strip() or None
+        head = subprocess.run(["git", "rev-parse", "--short=12", "HEAD"], capture_output=True, text=True, cwd=root,
+                              timeout=20).stdout.strip()
+        if not head:
+            return None
+        st = subprocess.run(["git", "status", "--porcelain", "--untracked-files=no", "--", ".", ":(exclude)profiles"],
+                            capture_output=True, text=True, cwd=root, timeout=20).stdout.strip()
+        return head + ("-dirty" if st else "")
     except (OSError, subprocess.SubprocessError):
         return None
 
