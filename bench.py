@@ -1813,10 +1813,12 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
         alone_log = streamer.copy_log()
         alone_copies = _copy_stats(alone_log, stack.blob)
         streamer.close()
-        # per-entry copy time when the copies run back to back: the gap
-        # between consecutive copy ends (the first: its own duration)
-        ends = [b for _, b in alone_log]
-        copy_each = [ends[0] - alone_log[0][0]] + [ends[j] - ends[j - 1] for j in range(1, len(ends))]
+        # per-entry copy time for the bound: one copy's bytes at the better
+        # of the two link rates measured (busy time of the copies alone and
+        # of the streamed step's copies; the link ran at different rates in
+        # the two on some boxes)
+        link_gbs = max(alone_copies["busy_gbs"], stream_copies["busy_gbs"])
+        copy_each = [stack.blob / (link_gbs * 1e9) * 1e3] * len(stack.seq)
 
         # compute alone: weights resident in HBM (one device copy of the
         # blobs), a HIP event before every entry
@@ -1880,6 +1882,7 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
             "bound": "pcie" if h2d_ms > compute_ms else "compute",
             "overlap": round(max(h2d_ms, compute_ms) / stream_ms, 4),
             "flowshop_bound_ms": round(bound_ms, 3), "overlap_vs_flowshop_bound": round(bound_ms / stream_ms, 4),
+            "flowshop_link_gbs": link_gbs,
             "overlap_vs_compute_under_copies": round(max(h2d_ms, under_copies_ms) / stream_ms, 4),
             "steady_state": {"micro_batches": micro_batches, "slots": steady_slots,
                              "ms_per_pass": round(mb_ms / micro_batches, 3),
