@@ -618,6 +618,15 @@ def config4_summaries(out_dir, prof):
             "calibration": {"kernel": copy, "bytes": 1 << 30, "fetch_KiB": copy_f, "write_KiB": copy_w,
                             "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
             "families": fams}
+    # the tree id names the code the counters were read on: summarizing the
+    # same counter output again later keeps the id it was first written with
+    try:
+        with open(os.path.join(prof, "hbm_traffic.json")) as fh:
+            old = json.load(fh)
+        if old.get("families") == fams and old.get("calibration") == data["calibration"]:
+            data["tree"] = old.get("tree")
+    except (OSError, ValueError):
+        pass
     with open(os.path.join(prof, "hbm_traffic.json"), "w") as fh:
         json.dump(data, fh, indent=1)
         fh.write("\n")
