@@ -1352,6 +1352,14 @@ static GroupPlan grouped_plan(const GemmArgs& dw, const GemmArgs& dx, size_t ws_
     constexpr double kOverheadSteps = kUnitOverhead;
     const double red_steps_per_byte = 2.0 / 10e6;
     const int nk0 = (dw.K + kPKB - 1) / kPKB, nk1 = (dx.K + kPKB - 1) / kPKB;
+    // Where df_fp8_gemm_bwd_dx, given this workspace, cuts dX's reduction into
+    // K slices (a small dX with a long reduction), dX is left to that call:
+    // the grouped launch never slices dX, and this keeps dX bit-identical
+    // between the two entry points.
+    GemmArgs dxs = dx;
+    dxs.ws = ws_bytes ? reinterpret_cast<float*>(uintptr_t{16}) : nullptr;  // only its presence is read
+    dxs.ws_bytes = ws_bytes;
+    if (nt_plan(dxs).split > 1) return GroupPlan{false, 1, nk0};
     const int64_t t0 = (int64_t)((dw.M + kPBM - 1) / kPBM) * ((dw.N + kPBN - 1) / kPBN);
     const int64_t t1 = (int64_t)((dx.M + kPBM - 1) / kPBM) * ((dx.N + kPBN - 1) / kPBN);
     // the two launches it replaces

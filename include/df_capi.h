@@ -352,7 +352,9 @@ int df_fp8_gemm_bwd_dw(const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ld
  * GEMM has few output tiles (6400 x 1600: 175 of 256 x 256 for 256 CUs), so
  * its launch alone leaves CUs idle; here one persistent grid takes dW's work
  * units first and deals dX's tiles to the CUs as they free up (a static
- * schedule, no atomics).  dX is bit-identical to df_fp8_gemm_bwd_dx; dW to
+ * schedule, no atomics).  dX is bit-identical to df_fp8_gemm_bwd_dx (where
+ * that call would cut dX's reduction into K slices, the two calls are made
+ * instead of the grouped launch); dW to
  * df_fp8_gemm_bwd_dw whenever both split its K range alike (they may pick
  * different slice counts, which changes dW's fp32 rounding, within the
  * 1e-4 bar either way).  Falls back to the two calls where the grouped
