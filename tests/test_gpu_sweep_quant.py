@@ -17,15 +17,18 @@ Per shape and input type, for both fp8 formats:
   (dnn/layers/fully_connected_layer.cu:91-106), on an input without
   non-finite values;
 - df_quantize_2d_delayed: codes at the scale the history held, then the
-  history and the next scale bit-exact against the oracle's.
+  history and the next scale bit-exact against the oracle's;
+- the LayerNorm producer (fp32, bf16, f16 inputs): y against the oracle and
+  the fused codes equal to the 2-D quantize of that y.
 """
 import numpy as np
 import pytest
 import torch
 
 import deepfuse_amd as df
-from deepfuse_amd import Fmt, synth
+from deepfuse_amd import Fmt
 from oracle import pyoracle as orc
+from test_gpu_layernorm import case as ln_case, host_f32, oracle_y
 from test_gpu_quant2d_wide import check_codes, make, strided
 
 pytestmark = pytest.mark.gpu
@@ -87,6 +90,36 @@ def test_sweep_quantize_2d(dev, rows, cols, kind):
             assert np.array_equal(ds.history.cpu().numpy().view(np.uint32), hist.view(np.uint32)), \
                 f"{what} delayed {p}: history"
             assert ds.scale.cpu().numpy().view(np.uint32)[0] == scale.view(np.uint32), f"{what} delayed {p}: scale"
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_sweep_layernorm_quantize(dev, rows, cols, kind):
+    """The LayerNorm producer on the same shapes, with gamma and beta:
+    y against the oracle's restatement of layer_norm_forward_kernel
+    (dnn/layers/layer_norm_layer.cu:26-63; fp32 within 1e-5 of the unit
+    scale, bf16 / f16 within one step of the type), and for both formats the
+    fused codes bit-identical to the 2-D quantize of that y, at the oracle's
+    scale of absmax(y)."""
+    xd, gd, bd, xh, gh, bh = ln_case(rows, cols, kind, True, dev, 5000 + rows * 7 + cols)
+    y0 = df.layernorm(xd, gd, bd, eps=1e-5)
+    y0h = host_f32(y0)
+    ref = oracle_y(xh, gh, bh, kind)
+    unit = np.abs(gh).max() + 1.0
+    if kind == "f32":
+        assert np.abs(y0h - ref).max() <= 1e-5 * unit, f"{rows}x{cols}: y"
+    else:
+        step = 2 ** -7 if kind == "bf16" else 2 ** -10
+        assert (np.abs(y0h - ref) <= np.abs(ref) * step + 1e-6 * unit).all(), f"{rows}x{cols}: y"
+    for fmt in (Fmt.E4M3, Fmt.E5M2):
+        y, q, qt, s = df.layernorm(xd, gd, bd, eps=1e-5, fmt=fmt, want_y=True, want_q=True, want_qt=True)
+        torch.cuda.synchronize()
+        same = torch.equal(y, y0) if kind == "f32" else torch.equal(y.view(torch.int16), y0.view(torch.int16))
+        assert same, f"{rows}x{cols} fmt={int(fmt)}: fused y"
+        s_exp = np.float32(orc.scale(orc.absmax(np.ascontiguousarray(y0h)), int(fmt)))
+        assert s.cpu().numpy().view(np.uint32)[0] == s_exp.view(np.uint32), f"{rows}x{cols} fmt={int(fmt)}: scale"
+        q0, qt0 = df.quantize_2d(y0, s, fmt, want_q=True, want_qt=True)
+        assert torch.equal(q, q0) and torch.equal(qt, qt0), f"{rows}x{cols} fmt={int(fmt)}: codes"
 
 
 def test_sweep_quant_covers_the_edges():
