@@ -83,6 +83,9 @@ def parse():
                    help="run only the config-2 conversion leg and print its JSON (profiling runs)")
     p.add_argument("--config3-only", action="store_true",
                    help="run only the config-3 leg and print its JSON (profiling runs)")
+    p.add_argument("--config5-compute-only", action="store_true",
+                   help="run only config 5's step once with every layer's weights resident (the streamed step's "
+                        "kernels, no copies) and print its JSON; for the config-5 MFMA counter run")
     p.add_argument("--tile-timeline", action="store_true",
                    help="run only the per-tile timeline of the four config-4 forward GEMMs and print its JSON")
     p.add_argument("--summarize-profiles", action="store_true",
@@ -165,6 +168,9 @@ def main():
         return
     if args.tile_timeline:
         print(json.dumps({"tile_timeline": tile_timeline_bench(torch, df, dev, cur())}))
+        return
+    if args.config5_compute_only:
+        print(json.dumps({"config5_compute": config5_compute_bench(torch, dev, layers=args.stream_layers)}))
         return
 
     def to_bf16(a):
@@ -490,6 +496,9 @@ PROFILE_COMMANDS = {
     "mfma_config3": ("timeout -s KILL 180 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES "
                      "SQ_INSTS_VALU_MFMA_MOPS_F8 --kernel-trace --output-format csv -d gpurun_out/pmc_mfma_config3 "
                      "-o bench -- python3 bench.py --config3-only"),
+    "mfma_config5": ("timeout -s KILL 300 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES "
+                     "SQ_INSTS_VALU_MFMA_MOPS_F8 --kernel-trace --output-format csv -d gpurun_out/pmc_mfma_config5 "
+                     "-o bench -- python3 bench.py --config5-compute-only"),
     "stats_consumer": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_consumer -o bench "
                        "-- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-conversion --no-streaming "
                        "--no-producer --no-delayed --no-config3"),
@@ -670,6 +679,12 @@ def summarize_profiles():
                     what="The config-3 leg: each Linear's GEMM 1 + 20 times back to back, eager, counters per "
                          "dispatch (the kernels run one at a time under counter collection)."):
         extra.append("gemm_mfma_busy_config3.md")
+    if mfma_summary(out_dir, prof, key="mfma_config5", out_name="gemm_mfma_busy_config5.md",
+                    title="MFMA busy and shader clock of the config-5 GEMMs (48-layer GPT-2 XL stack, 8192 tokens)",
+                    what="Config 5's step twice with every layer's weights resident (the streamed step's kernels "
+                         "without the copies; copies do not change which GEMMs run), eager, counters per dispatch "
+                         "(the kernels run one at a time under counter collection)."):
+        extra.append("gemm_mfma_busy_config5.md")
     for key, sub, fname, title, keep in EXTRA_STATS:
         path = os.path.join(out_dir, sub, "bench_kernel_stats.csv")
         if not os.path.exists(path):
@@ -1742,6 +1757,32 @@ def flowshop_bound(copy_ms, compute_ms):
         pre += copy_ms[k]
         best = max(best, pre + suf[k])
     return best
+
+
+def config5_compute_bench(torch, dev, layers=48, tokens=8192):
+    """Config 5's step once (after one warm-up step) with every layer's
+    weights resident in HBM: the kernels of the streamed step, in its order,
+    without the copies.  The config-5 MFMA counter run
+    (PROFILE_COMMANDS["mfma_config5"]) profiles these dispatches."""
+    from deepfuse_amd.stack import StreamedStack
+
+    stack = StreamedStack(torch, dev, layers=layers, tokens=tokens)
+    try:
+        dev_w = stack.resident_weights()
+        stack.resident_step(dev_w)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        stack.resident_step(dev_w)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        del dev_w
+        return {"workload": f"config 5 step, {layers} layers, {tokens} tokens, weights resident",
+                "ms": round(ms, 3), "tflops": round(stack.step_flops / ms / 1e9, 1)}
+    finally:
+        stack.close()
 
 
 def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, steps=2, micro_batches=3,
