@@ -37,8 +37,21 @@ struct Registry {
     }
 };
 
+// SCOPED_TRACE: messages that a failure inside their scope also prints
+inline std::vector<std::string>& traces() {
+    static thread_local std::vector<std::string> t;
+    return t;
+}
+struct ScopedTrace {
+    explicit ScopedTrace(std::string m) { traces().push_back(std::move(m)); }
+    ~ScopedTrace() { traces().pop_back(); }
+    ScopedTrace(const ScopedTrace&) = delete;
+    ScopedTrace& operator=(const ScopedTrace&) = delete;
+};
+
 inline void fail(const char* file, int line, const std::string& msg) {
     std::cout << file << ":" << line << ": Failure\n  " << msg << std::endl;
+    for (const std::string& t : traces()) std::cout << "  (trace: " << t << ")" << std::endl;
     ++Registry::get().failures;
 }
 
@@ -98,6 +111,10 @@ inline int run_all(int argc, char** argv) {
 }
 
 }  // namespace mini_test
+
+#define MT_CAT2(a, b) a##b
+#define MT_CAT(a, b) MT_CAT2(a, b)
+#define SCOPED_TRACE(msg) mini_test::ScopedTrace MT_CAT(mt_trace_, __LINE__)(msg)
 
 #define MT_CLASS(F, N) F##_##N##_Test
 #define TEST_F(F, N)                                                                       \

@@ -724,6 +724,48 @@ TEST_F(FullyConnectedLayerTest, RaggedShapesMatchOracle) {
     EXPECT_LE(rel_err(db, edb), 1e-5);
 }
 
+// Ten (tokens, in, out) triples drawn once from a fixed-seed mt19937: sizes
+// below 1600 mixed with ones next to a 128- or 256-wide tile edge, through the
+// layer's forward and backward (its caches, workspace and launch choices) and
+// against the oracle on the fp8-dequantized operands.
+TEST_F(FullyConnectedLayerTest, SeededShapeSweepMatchesOracle) {
+    std::mt19937 gen(20261205u);
+    auto draw = [&](int cap) {
+        const uint32_t r = gen();
+        if (r & 1u) return 1 + (int)((r >> 1) % (uint32_t)cap);
+        const int edge = ((r >> 1) & 1u ? 128 : 256) * (1 + (int)((r >> 2) % 6u));
+        return std::max(1, edge + (int)((r >> 5) % 3u) - 1);
+    };
+    for (int c = 0; c < 10; ++c) {
+        const int N = draw(1024), in_f = draw(1600), out_f = draw(1024);
+        SCOPED_TRACE("N=" + std::to_string(N) + " in=" + std::to_string(in_f) + " out=" + std::to_string(out_f));
+        FullyConnectedLayer<float> layer(in_f, out_f, true);
+        const auto w = uniform((size_t)out_f * in_f, -0.2f, 0.2f, 300 + c);
+        const auto b = uniform(out_f, -1.0f, 1.0f, 400 + c);
+        layer.parameters()[0]->upload(w.data());
+        layer.parameters()[1]->upload(b.data());
+        const auto x = uniform((size_t)N * in_f, -2.0f, 2.0f, 500 + c);
+        const auto dy = uniform((size_t)N * out_f, -0.01f, 0.01f, 600 + c);
+        tensor<float> input({N, in_f}), grad_out({N, out_f});
+        input.upload(x.data());
+        grad_out.upload(dy.data());
+        const auto y = download(layer.forward(input));
+        const auto dx = download(layer.backward(grad_out));
+        const auto dw = download(*layer.grad_weights());
+        const auto db = download(*layer.grad_bias());
+        const auto xd = fp8_values(x, DFO_E4M3), wd = fp8_values(w, DFO_E4M3), dyd = fp8_values(dy, DFO_E5M2);
+        std::vector<float> ey((size_t)N * out_f), edx((size_t)N * in_f), edw(w.size()), edb(out_f);
+        dfo_fc_forward(xd.data(), wd.data(), b.data(), ey.data(), N, in_f, out_f, 8);
+        dfo_fc_backward_input(dyd.data(), wd.data(), edx.data(), N, in_f, out_f, 8);
+        dfo_fc_backward_weights(dyd.data(), xd.data(), edw.data(), N, in_f, out_f, 8);
+        dfo_fc_backward_bias(dy.data(), edb.data(), N, out_f);
+        EXPECT_LE(rel_err(y, ey), 1e-4);
+        EXPECT_LE(rel_err(dx, edx), 1e-4);
+        EXPECT_LE(rel_err(dw, edw), 1e-4);
+        EXPECT_LE(rel_err(db, edb), 1e-5);
+    }
+}
+
 // bfloat16 layer: operands quantized from bf16, outputs rounded to bf16
 TEST_F(FullyConnectedLayerTest, BFloat16LayerMatchesOracle) {
     const int N = 64, in_f = 96, out_f = 80;
