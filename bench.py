@@ -978,6 +978,15 @@ def timeline_summary(out_dir, prof):
                      f"{d['tile_main_loop_us']} | {d['main_loop_per_k_step_us']} | {d['tile_epilogue_us']} | "
                      f"{d['gap_to_next_tile_us']} | {d['epilogue_share_of_tile']} | {d['block_prologue_us']} | "
                      f"{d['block_end_first_us']} / {d['block_end_last_us']} | {d['kernel_span_us']} |")
+    tails = [(n, d) for n, d in tl["shapes"].items() if d.get("tail_column_main_loop_us")]
+    if tails:
+        lines += ["", "Tiles of the last tile column, whose columns past N are outside the operand buffer (their DMA "
+                  "lanes return zeros without a memory request), against all tiles of the same launch (medians):", "",
+                  "| GEMM | columns in range of the last tile column | its tiles' main loop | all tiles' main loop |",
+                  "|---|---|---|---|"]
+        for n, d in tails:
+            lines.append(f"| {n} | {d['tail_column_valid_cols']} of 256 | {d['tail_column_main_loop_us']} | "
+                         f"{d['tile_main_loop_us']} |")
     with open(os.path.join(prof, "gemm_tile_timeline_config4.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
     return True
@@ -1639,6 +1648,20 @@ def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):
     return res
 
 
+def _tile_column(block, t, grid, tiles_m, tiles_n, group_m=8):
+    """Tile column of block `block`'s t-th tile in the unsplit persistent
+    kernel: the XCD-aware block remap and the grouped tile order of
+    persistent_body (csrc/gemm_fp8.hip), restated on the host."""
+    q, rr = grid >> 3, grid & 7
+    xcd, idx = block & 7, block >> 3
+    bl = xcd * (q + 1) + idx if xcd < rr else rr * (q + 1) + (xcd - rr) * q + idx
+    lt = bl + t * grid
+    per_group = group_m * tiles_n
+    group = lt // per_group
+    gsize = min(tiles_m - group * group_m, group_m)
+    return (lt - group * per_group) // gsize
+
+
 def tile_timeline_bench(torch, df, dev, stream, M=M_TOKENS, reps=3):
     """Where a persistent-kernel tile's time goes: the four config-4 forward
     GEMMs (bf16 bias and output) through df_fp8_gemm_fwd_timeline, the same
@@ -1683,9 +1706,10 @@ def tile_timeline_bench(torch, df, dev, stream, M=M_TOKENS, reps=3):
         span, st = best
         us = 0.01  # one tick = 10 ns
         nk = -(-K // 128)
-        main, epi, gap, pro, ends = [], [], [], [], []
+        main, epi, gap, pro, ends, tail = [], [], [], [], [], []
+        tiles_m, tiles_n = (M + 255) // 256, (N + 255) // 256
         t0 = st[:, 0].min()
-        for blk in st:
+        for b_id, blk in enumerate(st):
             ntl = 0
             while 3 + 3 * ntl < spb and blk[1 + 3 * ntl] > 0:
                 ntl += 1
@@ -1695,6 +1719,8 @@ def tile_timeline_bench(torch, df, dev, stream, M=M_TOKENS, reps=3):
             for t in range(ntl):
                 s0, e0, e1 = blk[1 + 3 * t], blk[2 + 3 * t], blk[3 + 3 * t]
                 main.append((e0 - s0) * us)
+                if N % 256 and _tile_column(b_id, t, grid.value, tiles_m, tiles_n) == tiles_n - 1:
+                    tail.append((e0 - s0) * us)
                 epi.append((e1 - e0) * us)
                 if t + 1 < ntl:
                     gap.append((blk[4 + 3 * t] - e1) * us)
@@ -1712,6 +1738,8 @@ def tile_timeline_bench(torch, df, dev, stream, M=M_TOKENS, reps=3):
             "block_prologue_us": med(pro), "block_end_first_us": round(min(ends), 2),
             "block_end_last_us": round(max(ends), 2),
             "epilogue_share_of_tile": round(med(epi) / (med(main) + med(epi) + (med(gap) or 0.0)), 4),
+            # tiles of the last tile column, which is only N % 256 columns wide (None when N % 256 == 0)
+            "tail_column_main_loop_us": med(tail), "tail_column_valid_cols": N % 256 or None,
         }
         del xq, wq, Y, stamps
     return out
