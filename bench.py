@@ -1509,6 +1509,80 @@ def producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10):
         res[name] = {"ms": round(ms, 4), "bytes_per_elem": bpe, "gbs": round(n * bpe / (ms * 1e-3) / 1e9, 1),
                      "min_bytes_gbs": round(n * 4 / (ms * 1e-3) / 1e9, 1)}
     res["fused_speedup"] = round(res["unfused"]["ms"] / res["fused"]["ms"], 3)
+    res["gemm_producer"] = gemm_producer_bench(torch, df, synth, dev, stream, M=M, C=C, reps=reps)
+    return res
+
+
+def gemm_producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10, rounds=7):
+    """The reference block's fc1 -> fc2 hand-off (transformer_block.cu:79-81:
+    fc1's bf16 Y is fc2's X, so fc2's just-in-time scale is Y's absmax) at the
+    config-4 fc shape (M x 1600 -> M x 6400), up to fc2's codes: fc1 GEMM, then
+    absmax pass over Y, then quantize Y (unfused) against the GEMM that folds
+    |Y| in its epilogue, then quantize Y (fused).  fc2's GEMM is the same in
+    both and is left out.  The absmax pass the fusion removes reads 2 bytes
+    per Y element."""
+    from deepfuse_amd import DType, Fmt
+    BF, E4 = int(DType.BFLOAT16), int(Fmt.E4M3)
+    N = 4 * C
+    xs = torch.from_numpy(synth.normal((M, C), 1.0, seed=1710)).to(dev).to(torch.bfloat16)
+    ws_ = torch.from_numpy(synth.normal((N, C), 0.02, seed=1711)).to(dev).to(torch.bfloat16)
+    _, sx = df.absmax_scale(xs, Fmt.E4M3)
+    _, sw = df.absmax_scale(ws_, Fmt.E4M3)
+    xq, _ = df.quantize_2d(xs, sx, Fmt.E4M3)
+    wq, _ = df.quantize_2d(ws_, sw, Fmt.E4M3)
+    del xs, ws_
+    Kp, Np, Mp = df.round16(C), df.round16(N), df.round16(M)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    q = torch.empty((M, Np), dtype=torch.uint8, device=dev)
+    qt = torch.empty((N, Mp), dtype=torch.uint8, device=dev)
+    sc = torch.empty(4, dtype=torch.float32, device=dev)
+    gws_b = max(int(df.lib().df_fp8_gemm_fwd_absmax_workspace_bytes(M, N, C)),
+                int(df.lib().df_fp8_gemm_workspace_bytes(M, N, C)), int(df.lib().df_absmax_workspace_bytes()))
+    gws = torch.empty(gws_b, dtype=torch.uint8, device=dev)
+    p = sc.data_ptr()
+
+    def gemm():
+        df.call("df_fp8_gemm_fwd", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, C, sx.data_ptr(), sw.data_ptr(),
+                int(DType.FLOAT32), None, BF, y.data_ptr(), N, gws.data_ptr(), gws_b, stream)
+
+    def absmax():
+        df.call("df_absmax_scale_bf16", y.data_ptr(), y.numel(), E4, None, p, gws.data_ptr(), gws_b, stream)
+
+    def fused_gemm():
+        df.call("df_fp8_gemm_fwd_absmax", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, C, sx.data_ptr(),
+                sw.data_ptr(), int(DType.FLOAT32), None, BF, y.data_ptr(), N, E4, None, p, gws.data_ptr(), gws_b,
+                stream)
+
+    def quant():
+        df.call("df_quantize_2d", BF, y.data_ptr(), M, N, N, E4, p, q.data_ptr(), Np, qt.data_ptr(), Mp, stream)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    # the variants in turn, over rounds that rotate their order, median per
+    # variant: back-to-back blocks of one variant drift with the clock
+    variants = (("gemm", gemm), ("absmax_pass", absmax), ("gemm_absmax", fused_gemm), ("quantize", quant),
+                ("unfused", lambda: (gemm(), absmax(), quant())), ("fused", lambda: (fused_gemm(), quant())))
+    for _, fn in variants:
+        fn()
+    times = {name: [] for name, _ in variants}
+    for r in range(rounds):
+        for j in range(len(variants)):
+            name, fn = variants[(j + r) % len(variants)]
+            times[name].append(timed(fn))
+    res = {"shape": [M, C, N], "y_dtype": "bf16", "note": f"median of {rounds} rotated rounds of {reps} calls"}
+    for name, _ in variants:
+        res[name + "_ms"] = round(sorted(times[name])[rounds // 2], 4)
+    res["epilogue_fold_ms"] = round(res["gemm_absmax_ms"] - res["gemm_ms"], 4)  # with the partials' fold
+    res["absmax_pass_gbs"] = round(M * N * 2 / (res["absmax_pass_ms"] * 1e-3) / 1e9, 1)
+    res["saved_ms"] = round(res["unfused_ms"] - res["fused_ms"], 4)
     return res
 
 

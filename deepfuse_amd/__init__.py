@@ -89,6 +89,9 @@ _SIGS = {
     "df_quantize_2d_batch_absmax": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp]),
     "df_fp8_gemm_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
+    "df_fp8_gemm_fwd_absmax_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
+    "df_fp8_gemm_fwd_absmax": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp,
+                                        _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "df_fp8_gemm_nt": (_c_int, [_c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "df_fp8_gemm_nt_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_sz, _vp, _vp]),
@@ -317,6 +320,25 @@ def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dty
          M, N, K, _ptr(sa), _ptr(sb), bias_dt, _ptr(bias), c_dt, _ptr(c), c.stride(0), _ptr(ws),
          ws.numel() if ws is not None else 0, _stream())
     return c
+
+
+def gemm_fwd_absmax(x_q, w_q, K: int, sx, sw, bias=None, out_dtype=None, next_fmt: Fmt = Fmt.E4M3):
+    """Y = X . W^T * sx * sw + bias (df_fp8_gemm_fwd_absmax): returns (Y,
+    absmax of Y as stored, the rule-D1/D2 scale of Y for next_fmt); Y is
+    bf16 (default) or fp32."""
+    torch = _torch()
+    out_dtype = out_dtype or torch.bfloat16
+    M, N = x_q.shape[0], w_q.shape[0]
+    y = torch.empty((M, N), dtype=out_dtype, device=x_q.device)
+    am = torch.empty(1, dtype=torch.float32, device=x_q.device)
+    sc = torch.empty(1, dtype=torch.float32, device=x_q.device)
+    nbytes = int(lib().df_fp8_gemm_fwd_absmax_workspace_bytes(M, N, K))
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x_q.device)
+    bias_dt = int(DType.FLOAT32) if bias is None else int(_in_dtype(bias))
+    call("df_fp8_gemm_fwd_absmax", _ptr(x_q), x_q.stride(0), _ptr(w_q), w_q.stride(0), M, N, K, _ptr(sx), _ptr(sw),
+         bias_dt, _ptr(bias), int(_in_dtype(y)), _ptr(y), y.stride(0), int(next_fmt), _ptr(am), _ptr(sc), _ptr(ws),
+         ws.numel(), _stream())
+    return y, am, sc
 
 
 class GemmKernel(enum.IntEnum):

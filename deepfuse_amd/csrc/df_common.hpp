@@ -49,6 +49,37 @@ __device__ __forceinline__ uint32_t fold_f32(uint32_t m, uint32_t bits) {
     return max(m, a < 0x7F800000u ? a : 0u);
 }
 
+// two bf16 in one dword: widen each to its binary32 pattern
+__device__ __forceinline__ uint32_t fold_bf16x2(uint32_t m, uint32_t w) {
+    const uint32_t hi = w & 0x7FFF0000u;
+    const uint32_t lo = (w << 16) & 0x7FFF0000u;
+    m = max(m, hi < 0x7F800000u ? hi : 0u);
+    return max(m, lo < 0x7F800000u ? lo : 0u);
+}
+
+// The same folds without compares, for code whose VALU slots are scarce (a
+// compare's lane mask read by the next VALU instruction costs wait states).
+// Adding 0x00800000 to a sign-cleared binary32 pattern (0x0080 to each
+// sign-cleared bf16 half of a dword: no carry crosses the halves) maps finite
+// patterns to positive and inf/NaN patterns to negative signed values, so a
+// signed max that starts at 0 skips the latter.  unbias_* turns such an
+// accumulator back into the binary32 pattern fold_f32 / fold_bf16x2 give.
+__device__ __forceinline__ uint32_t fold_f32_biased(uint32_t m, uint32_t bits) {
+    return (uint32_t)max((int)m, (int)((bits & 0x7FFFFFFFu) + 0x00800000u));
+}
+__device__ __forceinline__ uint32_t unbias_f32(uint32_t m) { return (uint32_t)max((int)m - 0x00800000, 0); }
+
+typedef short df_short2 __attribute__((ext_vector_type(2)));
+// two bf16 in one dword, one 16-bit lane each (v_pk_max_i16)
+__device__ __forceinline__ uint32_t fold_bf16x2_biased(uint32_t m, uint32_t w) {
+    const df_short2 u = __builtin_bit_cast(df_short2, (w & 0x7FFF7FFFu) + 0x00800080u);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(df_short2, m), u));
+}
+__device__ __forceinline__ uint32_t unbias_bf16x2(uint32_t m) {
+    const int hi = (int)(int16_t)(m >> 16), lo = (int)(int16_t)(m & 0xFFFFu);
+    return (uint32_t)max(max(hi, lo) - 0x80, 0) << 16;
+}
+
 // ----------------------------------------------------------------- encode --
 // binary32 -> fp8 code in the low byte.  |v| >= max (inf included) saturates,
 // NaN gives sign|0x7F.  Normal targets round the re-biased significand in
@@ -269,6 +300,10 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 int launch_status(const char* what);  // DF_OK or DF_ERR_HIP (checks hipGetLastError)
 int device_cu_count();                 // compute units of the current device (cached; 0 on error)
+// One block folds `nparts` absmax partials (fold_* bit patterns) into
+// absmax_out and/or the rule-D1/D2 scale for `fmt` (quant.hip).
+void launch_absmax_fold(const uint32_t* partial, int nparts, int fmt, float* absmax_out, float* scale_out,
+                        hipStream_t st);
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool aligned128(const void* p) { return ((uintptr_t)p & 127u) == 0; }

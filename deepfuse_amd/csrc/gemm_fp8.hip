@@ -531,15 +531,23 @@ template <typename T> struct Tag { using type = T; };
 // block's start ([0]) and, for its tile t, at the tile's first half-step
 // ([1 + 3t]), before its epilogue ([2 + 3t]) and after it ([3 + 3t]), while
 // 1 + 3t + 2 < tl_per_block; every other instantiation compiles none of it.
+// AMAX_OUT (df_fp8_gemm_fwd_absmax; one problem, unsplit, bf16 or fp32 C):
+// the epilogue also folds |C| over the finite values it stores, as stored
+// (after the conversion to OutT), with the compare-free biased folds, and
+// after its last tile wave w of block bl writes its maximum (a binary32
+// pattern) to amax_part[bl * 8 + w].
 template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT, typename OutT1, bool NARROW,
-          bool TIMELINE = false>
+          bool TIMELINE = false, bool AMAX_OUT = false>
 __device__ __forceinline__ void persistent_body(
     const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
     const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
     OutT* __restrict__ C, int ldc, int vec_out, int ksteps, int nsplit, const PProb& p1,
-    uint64_t* __restrict__ tl = nullptr, int tl_per_block = 0) {
+    uint64_t* __restrict__ tl = nullptr, int tl_per_block = 0, uint32_t* __restrict__ amax_part = nullptr) {
     constexpr bool GROUPED = !std::is_void<OutT1>::value;
     static_assert(!NARROW || (!GROUPED && !SPLIT), "narrow tiles: one problem, unsplit");
+    static_assert(!AMAX_OUT || (!GROUPED && !SPLIT && !NARROW &&
+                                (std::is_same<OutT, uint16_t>::value || std::is_same<OutT, float>::value)),
+                  "output absmax: one problem, unsplit, 256x256 tiles, bf16 or fp32 output");
     using Out1 = typename std::conditional<GROUPED, OutT1, OutT>::type;
     constexpr int FM = NARROW ? 2 : 4, FN = 2;    // 32x32 MFMA tiles per wave
     constexpr int BN = NARROW ? 128 : kPBN;       // tile columns
@@ -745,6 +753,7 @@ __device__ __forceinline__ void persistent_body(
     v16f acc[FM][FN];
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
     int after_epi = 0, c_h = 0;
+    uint32_t am_acc = 0;  // AMAX_OUT: this lane's biased fold of every value it stores
     const float sab = SPLIT ? 1.0f : sa[0] * sb[0];
     const float sab1 = GROUPED ? p1.sa[0] * p1.sb[0] : 0.0f;
 
@@ -945,11 +954,27 @@ __device__ __forceinline__ void persistent_body(
                                 __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
                             else
                                 *reinterpret_cast<u32x4*>(dst) = val;
+                            if constexpr (AMAX_OUT && ES == 2) {
+                                am_acc = fold_bf16x2_biased(am_acc, val.x);
+                                am_acc = fold_bf16x2_biased(am_acc, val.y);
+                                am_acc = fold_bf16x2_biased(am_acc, val.z);
+                                am_acc = fold_bf16x2_biased(am_acc, val.w);
+                            } else if constexpr (AMAX_OUT) {
+                                am_acc = fold_f32_biased(am_acc, val.x); am_acc = fold_f32_biased(am_acc, val.y);
+                                am_acc = fold_f32_biased(am_acc, val.z); am_acc = fold_f32_biased(am_acc, val.w);
+                            }
                         } else {
                             const T* ev = reinterpret_cast<const T*>(&val);
 #pragma unroll
                             for (int x = 0; x < 16 / ES; ++x)
-                                if (scol + x < No) dst[x] = ev[x];
+                                if (scol + x < No) {
+                                    dst[x] = ev[x];
+                                    if constexpr (AMAX_OUT && ES == 2)  // the value in the low half
+                                        am_acc = fold_bf16x2_biased(
+                                            am_acc, (uint32_t)reinterpret_cast<const uint16_t*>(ev)[x]);
+                                    else if constexpr (AMAX_OUT)
+                                        am_acc = fold_f32_biased(am_acc, reinterpret_cast<const uint32_t*>(ev)[x]);
+                                }
                         }
                     }
                 }
@@ -1004,6 +1029,12 @@ __device__ __forceinline__ void persistent_body(
         epilogue(tile);
         stamp(3 + 3 * tile);
     }
+    if constexpr (AMAX_OUT) {  // every block, tiles or none, writes its 8 partials
+        uint32_t m = sizeof(OutT) == 2 ? unbias_bf16x2(am_acc) : unbias_f32(am_acc);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+        if (lane == 0) amax_part[bl * 8 + w] = m;
+    }
     __builtin_amdgcn_s_waitcnt(0);  // every DMA has landed before the block's LDS is released
 }
 
@@ -1024,6 +1055,15 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_timeline_kernel(
     OutT* __restrict__ C, int ldc, int vec_out, uint64_t* __restrict__ tl, int tl_per_block) {
     persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, false, void, false, true>(
         A, lda, B, ldb, M, N, K, sa, sb, bias, C, ldc, vec_out, 0, 1, PProb{}, tl, tl_per_block);
+}
+
+template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_amax_kernel(
+    const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
+    const float* __restrict__ sa, const float* __restrict__ sb, const BiasT* __restrict__ bias,
+    OutT* __restrict__ C, int ldc, int vec_out, uint32_t* __restrict__ amax_part) {
+    persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, false, void, false, false, true>(
+        A, lda, B, ldb, M, N, K, sa, sb, bias, C, ldc, vec_out, 0, 1, PProb{}, nullptr, 0, amax_part);
 }
 
 template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
@@ -1542,6 +1582,72 @@ extern "C" int df_fp8_gemm_fwd_timeline(const uint8_t* Xq, int ldx, const uint8_
         g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, bias_bf16, Y_bf16, g.ldc,
         epi_store_mode(g.C, (int64_t)g.ldc * 2), stamps, stamps_per_block);
     return launch_status("df_fp8_gemm_fwd_timeline");
+}
+
+// Forward GEMM whose Y also yields its absmax (and the next quantize's scale):
+// the unsplit 256x256 persistent kernel folds |Y| in its epilogue into
+// per-block, per-wave partials in ws, and one block folds those.  Other plans
+// run df_fp8_gemm_fwd and then df_absmax_scale_* over Y (two passes, the same
+// results).
+extern "C" size_t df_fp8_gemm_fwd_absmax_workspace_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    // 8 partials per block; the grid is at most one block per tile
+    const size_t parts = (size_t)((M + kPBM - 1) / kPBM) * (size_t)((N + kPBN - 1) / kPBN) * 8 * sizeof(uint32_t);
+    return std::max(std::max(parts, df_absmax_workspace_bytes()), df_fp8_gemm_workspace_bytes(M, N, K));
+}
+
+extern "C" int df_fp8_gemm_fwd_absmax(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw, int M, int N, int K,
+                                      const float* sx_dev, const float* sw_dev, int bias_dtype, const void* bias,
+                                      int y_dtype, void* Y, int ldy, int next_fmt, float* y_absmax_dev,
+                                      float* y_scale_dev, void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    static const char* name = "df_fp8_gemm_fwd_absmax";
+    DF_CHECK(y_dtype == DF_DTYPE_BFLOAT16 || y_dtype == DF_DTYPE_FLOAT32, DF_ERR_UNSUPPORTED,
+             "%s: Y dtype %d (bf16 or fp32 only)", name, y_dtype);
+    DF_CHECK(next_fmt == E4M3 || next_fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad fp8 format %d", name, next_fmt);
+    DF_CHECK(y_absmax_dev || y_scale_dev, DF_ERR_INVALID, "%s: no absmax or scale output", name);
+    DF_CHECK(ldy == N, DF_ERR_INVALID, "%s: Y must be contiguous (ldy=%d, N=%d)", name, ldy, N);
+    GemmArgs g;
+    bool empty = false;
+    int st = nt_args(name, DF_FMT_E4M3, Xq, ldx, DF_FMT_E4M3, Wq, ldw, M, N, K, sx_dev, sw_dev, bias_dtype, bias,
+                     y_dtype, Y, ldy, ws, ws_bytes, stream, g, empty);
+    if (st != DF_OK) return st;
+    DF_CHECK(ws && ws_bytes >= df_absmax_workspace_bytes(), DF_ERR_WORKSPACE,
+             "%s: workspace %zu bytes < %zu", name, ws_bytes, df_absmax_workspace_bytes());
+    const bool bf16_out = y_dtype == DF_DTYPE_BFLOAT16;
+    const NtPlan p = empty ? NtPlan{} : nt_plan(g);
+    if (!empty && p.kind == DF_GEMM_KERNEL_PERSISTENT && p.split == 1 &&
+        ws_bytes >= (size_t)p.grid * 8 * sizeof(uint32_t)) {
+        uint32_t* parts = static_cast<uint32_t*>(ws);
+        const int vec_out = epi_store_mode(g.C, (int64_t)g.ldc * (bf16_out ? 2 : 4));
+        const bool bbf = bias && bias_dtype == DF_DTYPE_BFLOAT16;
+#define DF_AMAX_LAUNCH(OutT, BiasT, HB)                                                                          \
+    gemm_nt_persistent_amax_kernel<E4M3, E4M3, OutT, BiasT, HB><<<p.grid, 512, 0, g.st>>>(                      \
+        g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, static_cast<const BiasT*>(g.bias),                     \
+        static_cast<OutT*>(g.C), g.ldc, vec_out, parts)
+        if (bf16_out) {
+            if (!bias) DF_AMAX_LAUNCH(uint16_t, float, false);
+            else if (bbf) DF_AMAX_LAUNCH(uint16_t, uint16_t, true);
+            else DF_AMAX_LAUNCH(uint16_t, float, true);
+        } else {
+            if (!bias) DF_AMAX_LAUNCH(float, float, false);
+            else if (bbf) DF_AMAX_LAUNCH(float, uint16_t, true);
+            else DF_AMAX_LAUNCH(float, float, true);
+        }
+#undef DF_AMAX_LAUNCH
+        if ((st = launch_status(name)) != DF_OK) return st;
+        // each of the grid's blocks wrote its 8 partials
+        launch_absmax_fold(parts, p.grid * 8, next_fmt, y_absmax_dev, y_scale_dev, g.st);
+        return launch_status(name);
+    }
+    st = df_fp8_gemm_fwd(Xq, ldx, Wq, ldw, M, N, K, sx_dev, sw_dev, bias_dtype, bias, y_dtype, Y, ldy, ws, ws_bytes,
+                         stream);
+    if (st != DF_OK) return st;
+    const int64_t n = (int64_t)M * N;
+    return bf16_out ? df_absmax_scale_bf16(static_cast<const uint16_t*>(Y), n, next_fmt, y_absmax_dev, y_scale_dev,
+                                           ws, ws_bytes, stream)
+                    : df_absmax_scale_f32(static_cast<const float*>(Y), n, next_fmt, y_absmax_dev, y_scale_dev, ws,
+                                          ws_bytes, stream);
 }
 
 extern "C" int df_fp8_gemm_bwd_dx(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, int M,

@@ -22,14 +22,7 @@ constexpr int kThreads = 256;
 constexpr int kMaxReduceBlocks = 2048;  // partials in the absmax workspace
 
 // ------------------------------------------------------------------ absmax --
-// (fold_f32, the binary32 fold, is in df_common.hpp)
-// two bf16 in one dword: widen each to its binary32 pattern
-__device__ __forceinline__ uint32_t fold_bf16x2(uint32_t m, uint32_t w) {
-    const uint32_t hi = w & 0x7FFF0000u;
-    const uint32_t lo = (w << 16) & 0x7FFF0000u;
-    m = max(m, hi < 0x7F800000u ? hi : 0u);
-    return max(m, lo < 0x7F800000u ? lo : 0u);
-}
+// (fold_f32 and fold_bf16x2, the binary32 and bf16-pair folds, are in df_common.hpp)
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t m) {
     __shared__ uint32_t red[kThreads / 64];
@@ -201,6 +194,11 @@ __global__ __launch_bounds__(kThreads) void absmax_stage2(const uint32_t* __rest
         if (absmax_out) absmax_out[0] = am;
         if (scale_out) scale_out[0] = scale_from_absmax(am, fmt);
     }
+}
+
+void launch_absmax_fold(const uint32_t* partial, int nparts, int fmt, float* absmax_out, float* scale_out,
+                        hipStream_t st) {
+    absmax_stage2<<<1, kThreads, 0, st>>>(partial, nparts, fmt, absmax_out, scale_out);
 }
 
 __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* __restrict__ scale) {

@@ -333,6 +333,24 @@ int df_fp8_gemm_fwd_timeline(const uint8_t* Xq, int ldx, const uint8_t* Wq, int 
                              const float* sx_dev, const float* sw_dev, const uint16_t* bias_bf16,
                              uint16_t* Y_bf16, int ldy, uint64_t* stamps, int stamps_per_block,
                              int* grid_out, void* stream);
+/* The forward GEMM of df_fp8_gemm_fwd whose Y also gives the absmax the next
+ * Linear's just-in-time scale needs (new; no counterpart in the reference,
+ * whose TransformerBlock feeds fc1's output straight into fc2,
+ * dnn/layers/transformer_block.cu:79-81).  Y (bf16 or fp32, contiguous:
+ * ldy == N) is bit-identical to df_fp8_gemm_fwd's.  *y_absmax_dev gets the
+ * absmax over the finite values of Y as stored, and *y_scale_dev the rule-D1/D2
+ * scale for next_fmt, exactly what df_absmax_scale_bf16 / _f32 give on Y
+ * (either output may be NULL, not both).  On the unsplit 256x256 plan the
+ * kernel folds |Y| in its epilogue and one block folds the partials, so Y
+ * is not read again; other plans run the two passes.  ws:
+ * df_fp8_gemm_fwd_absmax_workspace_bytes(M, N, K) for the fused kernel; at
+ * least df_absmax_workspace_bytes() runs the two passes.  Calls that overlap
+ * on one workspace race. */
+size_t df_fp8_gemm_fwd_absmax_workspace_bytes(int M, int N, int K);
+int df_fp8_gemm_fwd_absmax(const uint8_t* Xq, int ldx, const uint8_t* Wq, int ldw, int M, int N, int K,
+                           const float* sx_dev, const float* sw_dev, int bias_dtype, const void* bias,
+                           int y_dtype, void* Y, int ldy, int next_fmt, float* y_absmax_dev,
+                           float* y_scale_dev, void* ws, size_t ws_bytes, void* stream);
 /* dX[M,K] = dY_q[M,N] . W[N,K]  (e5m2 x e4m3), given W^T quantized as
  * Wt_q[K, ldwt] (df_quantize_2d's qt).  Replaces fc_backward_input
  * (fully_connected_layer.cu:43-65). */

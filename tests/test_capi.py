@@ -72,6 +72,16 @@ def test_argument_errors():
     assert g(0, FAKE, 16, 0, FAKE, 16, 4, 5, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1  # ldc < N
     assert g(0, FAKE, 16, 0, FAKE, 16, -1, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1
     assert g(0, FAKE, 16, 0, FAKE, 16, 0, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == 0  # M = 0
+    # forward GEMM with Y's absmax: bf16 / fp32 Y only, a known format, an output, contiguous Y
+    fa = df.lib().df_fp8_gemm_fwd_absmax
+    bf, f32 = int(DType.BFLOAT16), int(DType.FLOAT32)
+    assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, int(DType.HALF), FAKE, 4, 0, FAKE, FAKE, FAKE,
+              4096, None) == -2
+    assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, bf, FAKE, 4, 7, FAKE, FAKE, FAKE, 4096, None) == -2
+    assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, bf, FAKE, 4, 0, None, None, FAKE, 4096, None) == -1
+    assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, f32, FAKE, 8, 0, FAKE, None, FAKE, 4096, None) == -1
+    assert "contiguous" in err()
+    assert df.lib().df_fp8_gemm_fwd_absmax_workspace_bytes(16384, 6400, 1600) >= 64 * 25 * 8 * 4
     # tensor utilities
     assert status("df_fill", FAKE, 4, 3, ctypes.byref(ctypes.c_int(0)), None) == -2
     assert status("df_add", 99, FAKE, FAKE, FAKE, 4, None) == -2
