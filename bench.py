@@ -66,6 +66,9 @@ def parse():
     p.add_argument("--no-config3", action="store_true", help="skip the GPT-2 small forward leg (config 3)")
     p.add_argument("--per-linear-weights", action="store_true",
                    help="quantize each weight in its own calls instead of one df_quantize_2d_batch per step")
+    p.add_argument("--separate-absmax", action="store_true",
+                   help="absmax pass and 2-D quantize as two calls (df_absmax_scale_bf16, df_quantize_2d*) "
+                        "instead of df_quantize_2d_jit")
     p.add_argument("--separate-backward", action="store_true",
                    help="time the backward as separate dX and dW launches instead of df_fp8_gemm_bwd")
     p.add_argument("--vendor-compare", action="store_true",
@@ -209,7 +212,15 @@ def main():
     BF, F32 = int(DType.BFLOAT16), int(DType.FLOAT32)
     E4, E5 = int(Fmt.E4M3), int(Fmt.E5M2)
 
+    jws_bytes = max(L.df_quantize_2d_jit_workspace_bytes(M, n, 1) for _, _, n in XL_LINEARS)
+    jws = torch.empty(jws_bytes, dtype=torch.uint8, device=dev)
+
     def quant(tm, x, rows, cols, fmt, am, sc, q, qt, tag, db=None):
+        if not args.separate_absmax:  # absmax and codes in one call (df_quantize_2d_jit)
+            tm.run("quantize2d_" + tag, df.call, "df_quantize_2d_jit", BF, x.data_ptr(), rows, cols, fmt, am, sc,
+                   q.data_ptr(), q.stride(0), qt.data_ptr(), qt.stride(0), None if db is None else db.data_ptr(),
+                   jws.data_ptr(), jws_bytes, cur())
+            return
         tm.run("absmax_" + tag, df.call, "df_absmax_scale_bf16", x.data_ptr(), x.numel(), fmt, am, sc,
                ws.data_ptr(), ws.numel(), cur())
         if db is None:
@@ -285,7 +296,9 @@ def main():
                 # absmax read + quantize read + both code layouts written
                 qbytes["weights_batch"] = qbytes.get("weights_batch", 0) + 2 * r * c + 2 * r * c + 2 * r * c
                 continue
-            qbytes["absmax_" + tag] = qbytes.get("absmax_" + tag, 0) + 2 * r * c
+            # absmax read (2 bytes per value) + quantize read + both code layouts written
+            absmax_fam = "absmax_" + tag if args.separate_absmax else "quantize2d_" + tag
+            qbytes[absmax_fam] = qbytes.get(absmax_fam, 0) + 2 * r * c
             qbytes["quantize2d_" + tag] = qbytes.get("quantize2d_" + tag, 0) + 2 * r * c + 2 * r * c
 
     step_flops = sum(gemm_flops.values())

@@ -82,6 +82,9 @@ _SIGS = {
     "df_quantize_2d_workspace_bytes": (_c_sz, [_c_int, _c_int]),
     "df_quantize_2d_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int,
                                        _vp, _c_int, _vp, _vp, _c_sz, _vp]),
+    "df_quantize_2d_jit_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
+    "df_quantize_2d_jit": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp,
+                                    _vp, _c_sz, _vp]),
     "df_colsum": (_c_int, [_c_int, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_sz, _vp]),
     "df_quantize_2d_batch_workspace_bytes": (_c_sz, []),
     "df_quantize_2d_batch": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -292,6 +295,26 @@ def quantize_2d(x, scale, fmt: Fmt, want_q=True, want_qt=False, colsum=False):
     call("df_quantize_2d_colsum", int(_in_dtype(x)), _ptr(x), rows, cols, x.stride(0), int(fmt),
          _ptr(scale), _ptr(q), ldq, _ptr(qt), ldqt, _ptr(cs), _ptr(ws), ws.numel(), _stream())
     return q, qt, cs
+
+
+def quantize_2d_jit(x, fmt: Fmt, want_q=True, want_qt=False, colsum=False):
+    """absmax, scale and the 2-D quantize at that scale in one call
+    (df_quantize_2d_jit): returns (absmax, scale, q, qt), plus the fp32
+    column sums when colsum=True; x is contiguous."""
+    torch = _torch()
+    if not x.is_contiguous():
+        raise ValueError("quantize_2d_jit: x must be contiguous")
+    rows, cols = x.shape
+    am = torch.empty(1, dtype=torch.float32, device=x.device)
+    sc = torch.empty(1, dtype=torch.float32, device=x.device)
+    q = torch.empty((rows, round16(cols)), dtype=torch.uint8, device=x.device) if want_q else None
+    qt = torch.empty((cols, round16(rows)), dtype=torch.uint8, device=x.device) if want_qt else None
+    cs = torch.empty(cols, dtype=torch.float32, device=x.device) if colsum else None
+    ws = _scratch(x.device, int(lib().df_quantize_2d_jit_workspace_bytes(rows, cols, int(colsum))), "jit")
+    call("df_quantize_2d_jit", int(_in_dtype(x)), _ptr(x), rows, cols, int(fmt), _ptr(am), _ptr(sc), _ptr(q),
+         q.shape[1] if q is not None else 0, _ptr(qt), qt.shape[1] if qt is not None else 0, _ptr(cs), _ptr(ws),
+         ws.numel(), _stream())
+    return (am, sc, q, qt, cs) if colsum else (am, sc, q, qt)
 
 
 def gemm_workspace(M: int, N: int, K: int, device):

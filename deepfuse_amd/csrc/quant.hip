@@ -20,6 +20,10 @@ namespace dfk {
 
 constexpr int kThreads = 256;
 constexpr int kMaxReduceBlocks = 2048;  // partials in the absmax workspace
+// absmax blocks of df_quantize_2d_jit: every tile block folds their
+// partials, so fewer than kMaxReduceBlocks (512: 2 KiB per tile block, and
+// still enough blocks for the absmax pass to stream at full rate)
+constexpr int kJitParts = 512;
 
 // ------------------------------------------------------------------ absmax --
 // (fold_f32 and fold_bf16x2, the binary32 and bf16-pair folds, are in df_common.hpp)
@@ -199,6 +203,35 @@ __global__ __launch_bounds__(kThreads) void absmax_stage2(const uint32_t* __rest
 void launch_absmax_fold(const uint32_t* partial, int nparts, int fmt, float* absmax_out, float* scale_out,
                         hipStream_t st) {
     absmax_stage2<<<1, kThreads, 0, st>>>(partial, nparts, fmt, absmax_out, scale_out);
+}
+
+// Stage 2 folded into the pass that uses the scale (no one-block launch
+// between them): every block of that pass folds the stage-1 partials itself,
+// gets the same maximum, and forms the scale by rule D1/D2; the writer block
+// also stores absmax and scale for the caller.  The barrier at the end hands
+// the scale to every thread and keeps block_max_u32's LDS free for reuse.
+struct JitScale {
+    const uint32_t* parts = nullptr;
+    int nparts = 0;
+    float* absmax_out = nullptr;
+    float* scale_out = nullptr;
+};
+
+__device__ __forceinline__ float jit_block_scale(const uint32_t* __restrict__ parts, int nparts, int fmt,
+                                                 float* __restrict__ absmax_out, float* __restrict__ scale_out,
+                                                 bool writer) {
+    __shared__ float s_scale;
+    const uint32_t m = block_max_u32(fold_parts(parts, nparts));
+    if (threadIdx.x == 0) {
+        const float am = __uint_as_float(m), sc = scale_from_absmax(am, fmt);
+        s_scale = sc;
+        if (writer) {
+            if (absmax_out) absmax_out[0] = am;
+            if (scale_out) scale_out[0] = sc;
+        }
+    }
+    __syncthreads();
+    return s_scale;
 }
 
 __global__ void scale_kernel(const float* __restrict__ absmax, int fmt, float* __restrict__ scale) {
@@ -938,19 +971,25 @@ __global__ __launch_bounds__(kThreads) void amax_history_init_kernel(const float
 }
 
 
-template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false, bool LN = false>
-__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
-                                                                int cols, int ldx, bool vec_ok,
-                                                                const float* __restrict__ scale,
-                                                                uint8_t* __restrict__ q, int ldq,
-                                                                uint8_t* __restrict__ qt, int ldqt,
-                                                                float* __restrict__ colpart,
-                                                                uint32_t* __restrict__ amaxpart = nullptr,
-                                                                LnArgs ln = LnArgs()) {
+// JIT: the scale comes from the absmax partials in jit (jit_block_scale;
+// block (0, 0) writes absmax and scale), not from scale[0].
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX, bool LN, bool JIT>
+__device__ __forceinline__ void q2d_kernel_body(const InT* __restrict__ x, int rows, int cols, int ldx, bool vec_ok,
+                                                const float* __restrict__ scale, uint8_t* __restrict__ q, int ldq,
+                                                uint8_t* __restrict__ qt, int ldqt, float* __restrict__ colpart,
+                                                uint32_t* __restrict__ amaxpart, const LnArgs& ln,
+                                                const JitScale& jit) {
+    static_assert(!JIT || (CODES && !AMAX && !LN), "just-in-time scale: the plain code pass");
     constexpr int RG = kThreads / (kT2 / Ld<InT>::E);
     __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * kT2R];
     __shared__ float csum[COLSUM ? RG : 1][kT2];
-    const QDiv d = make_qdiv(CODES ? scale[0] : 1.0f);
+    float sc = 1.0f;
+    if constexpr (JIT)
+        sc = jit_block_scale(jit.parts, jit.nparts, FMT, jit.absmax_out, jit.scale_out,
+                             blockIdx.x == 0 && blockIdx.y == 0);
+    else if constexpr (CODES)
+        sc = scale[0];
+    const QDiv d = make_qdiv(sc);
     if (!CODES || d.fast)
         q2d_tile<InT, FMT, COLSUM, CODES, AMAX, LN, true, AMAX && !LN, kT2R>(
             x, rows, cols, ldx, vec_ok, d, q, ldq, qt, ldqt, colpart, amaxpart, ln, tile, csum, blockIdx.x,
@@ -961,10 +1000,57 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __rest
             blockIdx.y, gridDim.x);
 }
 
-// ---- several 2-D tensors in three launches (every Linear's weights after
-// an optimizer step): per-tensor absmax partials, one fold block per
-// tensor, then every tensor's tiles.  Each tensor gets the same scale and
-// codes as df_absmax_scale_* followed by df_quantize_2d would give it.
+template <typename InT, int FMT, bool COLSUM, bool CODES, bool AMAX = false, bool LN = false>
+__global__ __launch_bounds__(kThreads) void quantize_2d_kernel(const InT* __restrict__ x, int rows,
+                                                                int cols, int ldx, bool vec_ok,
+                                                                const float* __restrict__ scale,
+                                                                uint8_t* __restrict__ q, int ldq,
+                                                                uint8_t* __restrict__ qt, int ldqt,
+                                                                float* __restrict__ colpart,
+                                                                uint32_t* __restrict__ amaxpart = nullptr,
+                                                                LnArgs ln = LnArgs()) {
+    q2d_kernel_body<InT, FMT, COLSUM, CODES, AMAX, LN, false>(x, rows, cols, ldx, vec_ok, scale, q, ldq, qt, ldqt,
+                                                              colpart, amaxpart, ln, JitScale());
+}
+
+// The just-in-time pass (df_quantize_2d_jit), x contiguous.  The _w5 form
+// holds it to five waves per SIMD, the occupancy of the same pass without the
+// fold (the fold's registers are dead before the tile pass); fp32 with column
+// sums has four either way and takes the plain form.
+template <typename InT, int FMT, bool COLSUM>
+__global__ __launch_bounds__(kThreads) void quantize_2d_jit_kernel(const InT* __restrict__ x, int rows, int cols,
+                                                                    bool vec_ok, uint8_t* __restrict__ q, int ldq,
+                                                                    uint8_t* __restrict__ qt, int ldqt,
+                                                                    float* __restrict__ colpart, JitScale jit) {
+    q2d_kernel_body<InT, FMT, COLSUM, true, false, false, true>(x, rows, cols, cols, vec_ok, nullptr, q, ldq, qt,
+                                                                ldqt, colpart, nullptr, LnArgs(), jit);
+}
+
+template <typename InT, int FMT, bool COLSUM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void quantize_2d_jit_w5_kernel(
+    const InT* __restrict__ x, int rows, int cols, bool vec_ok, uint8_t* __restrict__ q, int ldq,
+    uint8_t* __restrict__ qt, int ldqt, float* __restrict__ colpart, JitScale jit) {
+    q2d_kernel_body<InT, FMT, COLSUM, true, false, false, true>(x, rows, cols, cols, vec_ok, nullptr, q, ldq, qt,
+                                                                ldqt, colpart, nullptr, LnArgs(), jit);
+}
+
+template <typename InT, int FMT, bool COLSUM>
+static void launch_q2d_jit(dim3 grid, hipStream_t st, const InT* x, int rows, int cols, bool vec_ok, uint8_t* q,
+                           int ldq, uint8_t* qt, int ldqt, float* colpart, const JitScale& jit) {
+    if constexpr (sizeof(InT) == 2 || !COLSUM)
+        quantize_2d_jit_w5_kernel<InT, FMT, COLSUM><<<grid, kThreads, 0, st>>>(x, rows, cols, vec_ok, q, ldq, qt,
+                                                                                ldqt, colpart, jit);
+    else
+        quantize_2d_jit_kernel<InT, FMT, COLSUM><<<grid, kThreads, 0, st>>>(x, rows, cols, vec_ok, q, ldq, qt, ldqt,
+                                                                             colpart, jit);
+}
+
+// ---- several 2-D tensors in two launches (every Linear's weights after an
+// optimizer step): per-tensor absmax partials, then every tensor's tiles,
+// each tile block folding its tensor's partials (a launch holding an empty
+// tensor runs one fold block per tensor in between).  Each tensor gets the
+// same scale and codes as df_absmax_scale_* followed by df_quantize_2d
+// would give it.
 constexpr int kBatchMax = 32;  // tensors per launch
 // Input bytes of one launch beyond which its absmax pass has pushed the
 // first tensors out of the 256 MB Infinity Cache before the tile pass
@@ -1026,9 +1112,16 @@ __global__ __launch_bounds__(kThreads) void scale_batch_kernel(const float* __re
     for (int t = threadIdx.x; t < count; t += kThreads) scale_out[t] = scale_from_absmax(absmax[t], fmt);
 }
 
-template <typename InT, int FMT, bool NT>
-__global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const BatchArgs B,
-                                                                      const float* __restrict__ scale) {
+// SRC 0: tensor t's scale is scale[t].  SRC 1: folded from its absmax
+// partials, partial[blk_first[t] ..] (jit_block_scale); SRC 2: formed from
+// absmax_in[t].  With SRC 1 and 2 the tensor's first tile block writes
+// scale_out[t] (and absmax_out[t]).  Five waves per SIMD: the occupancy of
+// the SRC 0 form (the fold's registers are dead before the tile pass).
+template <typename InT, int FMT, bool NT, int SRC = 0>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void quantize_2d_batch_kernel(
+    const BatchArgs B, const float* __restrict__ scale, const uint32_t* __restrict__ partial = nullptr,
+    const float* __restrict__ absmax_in = nullptr, float* __restrict__ absmax_out = nullptr,
+    float* __restrict__ scale_out = nullptr) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kT2 * kT2];
     __shared__ float csum[1][kT2];
     const int t = batch_owner(B.tile_first, B.count, blockIdx.x);
@@ -1037,7 +1130,17 @@ __global__ __launch_bounds__(kThreads) void quantize_2d_batch_kernel(const Batch
     const InT* x = static_cast<const InT*>(B.x[t]);
     const int rows = B.rows[t], cols = B.cols[t];
     const bool vec_ok = B.vec_ok[t] != 0;
-    const QDiv d = make_qdiv(scale[t]);
+    float sc;
+    if constexpr (SRC == 1) {
+        sc = jit_block_scale(partial + B.blk_first[t], B.blk_first[t + 1] - B.blk_first[t], FMT,
+                             absmax_out ? absmax_out + t : nullptr, scale_out + t, lt == 0);
+    } else if constexpr (SRC == 2) {
+        sc = scale_from_absmax(absmax_in[t], FMT);
+        if (lt == 0 && threadIdx.x == 0) scale_out[t] = sc;
+    } else {
+        sc = scale[t];
+    }
+    const QDiv d = make_qdiv(sc);
     if (d.fast)
         q2d_tile<InT, FMT, false, true, false, false, true, NT>(x, rows, cols, cols, vec_ok, d, B.q[t], B.ldq[t], B.qt[t],
                                                             B.ldqt[t], nullptr, nullptr, LnArgs(), tile, csum, bx, by,
@@ -1202,6 +1305,21 @@ extern "C" int df_hbm_probe(int read_bytes, int write_bytes, const void* src, in
     return DF_ERR_UNSUPPORTED;
 }
 
+// One partial maximum per block into part[0 .. blocks), blocks <= cap <=
+// kMaxReduceBlocks (x 16-byte aligned, dtype already checked); returns blocks.
+static int launch_absmax_stage1(int in_dtype, const void* x, int64_t n, uint32_t* part, hipStream_t st,
+                                int cap = kMaxReduceBlocks) {
+    const int per = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 8;
+    const int blocks = grid_for((n / per + kU - 1) / kU, cap);
+    if (in_dtype == DF_DTYPE_FLOAT32)
+        absmax_f32_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), n, part);
+    else if (in_dtype == DF_DTYPE_BFLOAT16)
+        absmax_bf16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
+    else
+        absmax_f16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
+    return blocks;
+}
+
 static int absmax_impl(int in_dtype, const void* x, int64_t n, int fmt, float* absmax_dev,
                        float* scale_dev, void* ws, size_t ws_bytes, void* stream) {
     clear_error();
@@ -1213,18 +1331,11 @@ static int absmax_impl(int in_dtype, const void* x, int64_t n, int fmt, float* a
              "absmax: workspace %zu bytes < %zu", ws_bytes, df_absmax_workspace_bytes());
     DF_CHECK(fmt == E4M3 || fmt == E5M2, DF_ERR_UNSUPPORTED, "absmax: bad fp8 format %d", fmt);
     DF_CHECK(aligned16(x) && aligned4(ws), DF_ERR_ALIGN, "absmax: x must be 16-byte aligned");
+    DF_CHECK(in_dtype == DF_DTYPE_FLOAT32 || in_dtype == DF_DTYPE_BFLOAT16 || in_dtype == DF_DTYPE_HALF,
+             DF_ERR_UNSUPPORTED, "absmax: dtype %d not supported", in_dtype);
     hipStream_t st = as_stream(stream);
     uint32_t* part = static_cast<uint32_t*>(ws);
-    const int per = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 8;
-    int blocks = grid_for((n / per + kU - 1) / kU, kMaxReduceBlocks);
-    if (in_dtype == DF_DTYPE_FLOAT32)
-        absmax_f32_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const float*>(x), n, part);
-    else if (in_dtype == DF_DTYPE_BFLOAT16)
-        absmax_bf16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
-    else if (in_dtype == DF_DTYPE_HALF)
-        absmax_f16_stage1<<<blocks, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part);
-    else
-        DF_CHECK(false, DF_ERR_UNSUPPORTED, "absmax: dtype %d not supported", in_dtype);
+    const int blocks = launch_absmax_stage1(in_dtype, x, n, part, st);
     absmax_stage2<<<1, kThreads, 0, st>>>(part, blocks, fmt, absmax_dev, scale_dev);
     return launch_status("absmax");
 }
@@ -1363,6 +1474,19 @@ extern "C" size_t df_quantize_2d_workspace_bytes(int rows, int cols) {
     return (size_t)((rows + kT2R - 1) / kT2R) * (size_t)cols * sizeof(float);
 }
 
+// df_quantize_2d_jit's workspace: the column-sum partials (when asked), then
+// the absmax partials at *parts_off (16-byte aligned).
+static size_t jit_ws_layout(int rows, int cols, bool colsum, size_t* parts_off) {
+    const size_t cs = colsum ? (df_quantize_2d_workspace_bytes(rows, cols) + 15) & ~(size_t)15 : 0;
+    if (parts_off) *parts_off = cs;
+    return cs + kMaxReduceBlocks * sizeof(uint32_t);
+}
+
+extern "C" size_t df_quantize_2d_jit_workspace_bytes(int rows, int cols, int colsum) {
+    if (rows < 0 || cols < 0) return 0;
+    return jit_ws_layout(rows, cols, colsum != 0, nullptr);
+}
+
 // Tile grid of a 2-D quantize (tiles of tr rows and kT2 columns): covers the
 // codes' padded extents.
 static dim3 q2d_grid(int rows, int cols, const uint8_t* q, int ldq, const uint8_t* qt, int ldqt, int tr) {
@@ -1384,7 +1508,8 @@ static size_t delayed_ws_layout(int rows, int cols, int ldq, int ldqt, bool cols
 static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int rows, int cols, int ldx,
                             int fmt, const float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt,
                             float* colsum, void* ws, size_t ws_bytes, void* stream,
-                            float* history = nullptr, int hist_len = 0, float* next_scale = nullptr) {
+                            float* history = nullptr, int hist_len = 0, float* next_scale = nullptr,
+                            bool jit = false, float* jit_absmax = nullptr) {
     clear_error();
     DF_CHECK(rows >= 0 && cols >= 0 && (ldx >= cols || rows == 0), DF_ERR_INVALID,
              "%s: bad shape rows=%d cols=%d ldx=%d", name, rows, cols, ldx);
@@ -1403,8 +1528,16 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
         DF_CHECK(aligned16(qt), DF_ERR_ALIGN, "%s: qt must be 16-byte aligned", name);
     }
     const bool delayed = history != nullptr;
-    size_t amax_off = 0;
-    if (delayed) {
+    size_t amax_off = 0, jit_off = 0;
+    if (jit) {  // scale_dev is an output here
+        DF_CHECK(q || qt || empty, DF_ERR_INVALID, "%s: no code output", name);
+        DF_CHECK(ldx == cols, DF_ERR_INVALID, "%s: x must be contiguous (ldx=%d, cols=%d)", name, ldx, cols);
+        DF_CHECK(aligned4(scale_dev) && aligned4(jit_absmax), DF_ERR_ALIGN, "%s: absmax/scale misaligned", name);
+        DF_CHECK(aligned16(x), DF_ERR_ALIGN, "%s: x must be 16-byte aligned", name);
+        const size_t need = jit_ws_layout(rows, cols, colsum != nullptr, &jit_off);
+        DF_CHECK(ws && aligned16(ws), DF_ERR_WORKSPACE, "%s: needs a 16-byte aligned workspace", name);
+        DF_CHECK(ws_bytes >= need, DF_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu", name, ws_bytes, need);
+    } else if (delayed) {
         DF_CHECK(q || qt || empty, DF_ERR_INVALID, "%s: no code output", name);
         DF_CHECK(hist_len >= 1 && hist_len <= kMaxHistory, DF_ERR_INVALID, "%s: history length %d not in [1, %d]",
                  name, hist_len, kMaxHistory);
@@ -1428,6 +1561,10 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
             amax_history_kernel<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, history, hist_len, next_scale);
             return launch_status(name);
         }
+        if (jit) {  // absmax 0, scale 1
+            absmax_stage2<<<1, kThreads, 0, st>>>(nullptr, 0, fmt, jit_absmax, const_cast<float*>(scale_dev));
+            return launch_status(name);
+        }
         return DF_OK;
     }
     DF_CHECK(grid.y <= 65535, DF_ERR_INVALID, "%s: rows=%d too large", name, rows);
@@ -1435,9 +1572,20 @@ static int quantize_2d_impl(const char* name, int in_dtype, const void* x, int r
     uint32_t* amaxpart = delayed ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + amax_off) : nullptr;
     const int esz = in_dtype == DF_DTYPE_FLOAT32 ? 4 : 2;
     const bool vec_ok = aligned16(x) && ((int64_t)ldx * esz) % 16 == 0;
+    JitScale J;
+    if (jit) {
+        uint32_t* jparts = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + jit_off);
+        J.nparts = launch_absmax_stage1(in_dtype, x, (int64_t)rows * cols, jparts, st, kJitParts);
+        J.parts = jparts;
+        J.absmax_out = jit_absmax;
+        J.scale_out = const_cast<float*>(scale_dev);
+    }
 #define DF_Q2D(T, F, CS)                                                                                        \
     do {                                                                                                        \
-        if (delayed)                                                                                            \
+        if (jit)                                                                                                \
+            launch_q2d_jit<T, F, CS>(grid, st, static_cast<const T*>(x), rows, cols, vec_ok, q, ldq, qt, ldqt,   \
+                                     part, J);                                                                  \
+        else if (delayed)                                                                                       \
             quantize_2d_kernel<T, F, CS, true, true><<<grid, kThreads, 0, st>>>(                                \
                 static_cast<const T*>(x), rows, cols, ldx, vec_ok, scale_dev, q, ldq, qt, ldqt, part, amaxpart); \
         else                                                                                                    \
@@ -1572,6 +1720,15 @@ extern "C" int df_quantize_2d_colsum(int in_dtype, const void* x, int rows, int 
                             ldqt, colsum, ws, ws_bytes, stream);
 }
 
+extern "C" int df_quantize_2d_jit(int in_dtype, const void* x, int rows, int cols, int fmt, float* absmax_dev,
+                                  float* scale_dev, uint8_t* q, int ldq, uint8_t* qt, int ldqt, float* colsum,
+                                  void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    DF_CHECK(scale_dev, DF_ERR_INVALID, "df_quantize_2d_jit: scale_dev is NULL");
+    return quantize_2d_impl("df_quantize_2d_jit", in_dtype, x, rows, cols, cols, fmt, scale_dev, q, ldq, qt, ldqt,
+                            colsum, ws, ws_bytes, stream, nullptr, 0, nullptr, true, absmax_dev);
+}
+
 extern "C" int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx, float* out, void* ws,
                          size_t ws_bytes, void* stream) {
     // column sums alone: the same tile pass with no code outputs
@@ -1622,11 +1779,17 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
     for (int t0 = 0; t0 < count; t0 += kBatchMax) {
         BatchArgs B{};
         B.count = std::min(count - t0, kBatchMax);
+        // Each tensor's tile blocks form its scale themselves (no launch
+        // between the passes) when every tensor has a tile to write it;
+        // otherwise a separate fold or scale launch does.
+        bool fold = true;
+        for (int i = 0; i < B.count; ++i) fold = fold && rows[t0 + i] > 0 && cols[t0 + i] > 0;
         // absmax blocks in proportion to the tensors' sizes, at least one
-        // each, at most kMaxReduceBlocks in all
+        // each, at most kMaxReduceBlocks in all (kJitParts when every tile
+        // block folds its tensor's partials)
         int64_t total = 0;
         for (int i = 0; i < B.count; ++i) total += (int64_t)rows[t0 + i] * cols[t0 + i];
-        const int64_t budget = kMaxReduceBlocks - B.count;
+        const int64_t budget = (fold ? kJitParts : kMaxReduceBlocks) - B.count;
         int bf = 0, tf = 0;
         for (int i = 0; i < B.count; ++i) {
             const int t = t0 + i;
@@ -1652,28 +1815,47 @@ static int batch_impl(const char* name, int in_dtype, int count, const void* con
         B.tile_first[B.count] = tf;
         float* am = absmax_dev ? absmax_dev + t0 : nullptr;
         float* sc = scale_dev + t0;
-        if (absmax_in) {
-            scale_batch_kernel<<<1, kThreads, 0, st>>>(absmax_in + t0, B.count, fmt, sc);
-        } else {
+        if (!absmax_in) {
             if (in_dtype == DF_DTYPE_FLOAT32) absmax_batch_stage1<float><<<bf, kThreads, 0, st>>>(B, part);
             else absmax_batch_stage1<uint16_t><<<bf, kThreads, 0, st>>>(B, part);
-            absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
+            if (!fold) absmax_batch_stage2<<<B.count, kThreads, 0, st>>>(B, part, fmt, am, sc);
+        } else if (!fold) {
+            scale_batch_kernel<<<1, kThreads, 0, st>>>(absmax_in + t0, B.count, fmt, sc);
         }
+        const float* ain = absmax_in ? absmax_in + t0 : nullptr;
         // non-temporal tiles where x is not in cache: no pass has just read it
         // (the caller's absmax), or the absmax pass read more than it holds
-        auto tiles = [&](auto nt) {
+        auto tiles = [&](auto nt, auto src) {
             constexpr bool NT = decltype(nt)::value;
+            constexpr int SRC = decltype(src)::value;
             if (in_dtype == DF_DTYPE_FLOAT32) {
-                if (fmt == E4M3) quantize_2d_batch_kernel<float, E4M3, NT><<<tf, kThreads, 0, st>>>(B, sc);
-                else quantize_2d_batch_kernel<float, E5M2, NT><<<tf, kThreads, 0, st>>>(B, sc);
+                if (fmt == E4M3)
+                    quantize_2d_batch_kernel<float, E4M3, NT, SRC><<<tf, kThreads, 0, st>>>(B, sc, part, ain, am, sc);
+                else
+                    quantize_2d_batch_kernel<float, E5M2, NT, SRC><<<tf, kThreads, 0, st>>>(B, sc, part, ain, am, sc);
             } else {
-                if (fmt == E4M3) quantize_2d_batch_kernel<uint16_t, E4M3, NT><<<tf, kThreads, 0, st>>>(B, sc);
-                else quantize_2d_batch_kernel<uint16_t, E5M2, NT><<<tf, kThreads, 0, st>>>(B, sc);
+                if (fmt == E4M3)
+                    quantize_2d_batch_kernel<uint16_t, E4M3, NT, SRC><<<tf, kThreads, 0, st>>>(B, sc, part, ain, am,
+                                                                                            sc);
+                else
+                    quantize_2d_batch_kernel<uint16_t, E5M2, NT, SRC><<<tf, kThreads, 0, st>>>(B, sc, part, ain, am,
+                                                                                            sc);
             }
         };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
         if (tf > 0) {
-            if (absmax_in || total * esz > kBatchColdBytes) tiles(std::true_type());
-            else tiles(std::false_type());
+            if (!fold) {
+                if (absmax_in || total * esz > kBatchColdBytes) tiles(std::true_type(), S0());
+                else tiles(std::false_type(), S0());
+            } else if (absmax_in) {
+                tiles(std::true_type(), S2());
+            } else if (total * esz > kBatchColdBytes) {
+                tiles(std::true_type(), S1());
+            } else {
+                tiles(std::false_type(), S1());
+            }
         }
         if (int rc = launch_status(name)) return rc;
     }

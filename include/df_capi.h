@@ -148,6 +148,19 @@ int df_quantize_2d_colsum(int in_dtype, const void* x, int rows, int cols, int l
                           int fmt, const float* scale_dev, uint8_t* q, int ldq,
                           uint8_t* qt, int ldqt, float* colsum,
                           void* ws, size_t ws_bytes, void* stream);
+/* Just-in-time quantize in one call (new; the reference has no quantizer,
+ * README.md:16): df_absmax_scale_* of x, then df_quantize_2d (colsum NULL)
+ * or df_quantize_2d_colsum at that scale, with the same absmax, scale, codes
+ * and column sums, bit for bit.  *scale_dev (required) and *absmax_dev (may
+ * be NULL) are outputs.  x is contiguous [rows, cols] and 16-byte aligned.
+ * The tile pass forms the scale from the absmax partials itself, so no
+ * one-block launch sits between the two passes.  ws:
+ * df_quantize_2d_jit_workspace_bytes(rows, cols, colsum != NULL). */
+size_t df_quantize_2d_jit_workspace_bytes(int rows, int cols, int colsum);
+int df_quantize_2d_jit(int in_dtype, const void* x, int rows, int cols, int fmt,
+                       float* absmax_dev, float* scale_dev, uint8_t* q, int ldq,
+                       uint8_t* qt, int ldqt, float* colsum,
+                       void* ws, size_t ws_bytes, void* stream);
 
 /* ---- column sums alone (replaces fc_backward_bias,
  * dnn/layers/fully_connected_layer.cu:91-106) ----
@@ -157,8 +170,9 @@ int df_colsum(int in_dtype, const void* x, int rows, int cols, int ldx,
               float* out, void* ws, size_t ws_bytes, void* stream);
 
 /* Several contiguous 2-D tensors x[t] [rows[t], cols[t]] (every Linear's
- * weights after an optimizer step) in three launches instead of three per
- * tensor: per-tensor absmax and scale into absmax_dev[t] (device array, or
+ * weights after an optimizer step) in two launches (three when a tensor is
+ * empty) instead of three per tensor: per-tensor absmax and scale into
+ * absmax_dev[t] (device array, or
  * NULL) and scale_dev[t] (device array), then row codes q[t] [rows, ldq[t]]
  * and transposed codes qt[t] [cols, ldqt[t]] (either pointer array, or any
  * entry, may be NULL), zero-padded like df_quantize_2d.  Each tensor gets

@@ -108,6 +108,17 @@ def test_argument_errors():
     assert "timestep" in err()
     assert status("df_adam_update_f32", ok, ok, (P * 1)(FAKE + 8), ok, one, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1,
                   None, 0.0, None) == -4
+    # just-in-time quantize: scale output required, x aligned, codes asked for, workspace size
+    BF = int(DType.BFLOAT16)
+    wb = df.lib().df_quantize_2d_jit_workspace_bytes(64, 64, 0)
+    assert wb >= 2048 * 4 and df.lib().df_quantize_2d_jit_workspace_bytes(256, 64, 1) >= wb + 2 * 64 * 4
+    jit = lambda *a: status("df_quantize_2d_jit", BF, *a)
+    assert jit(FAKE, 64, 64, 0, FAKE, None, FAKE, 64, None, 0, None, FAKE, wb, None) == -1  # no scale output
+    assert jit(FAKE + 2, 64, 64, 0, None, FAKE, FAKE, 64, None, 0, None, FAKE, wb, None) == -4
+    assert jit(FAKE, 64, 64, 0, None, FAKE, None, 0, None, 0, FAKE, FAKE, wb, None) == -1  # column sums only
+    assert jit(FAKE, 64, 64, 3, None, FAKE, FAKE, 64, None, 0, None, FAKE, wb, None) == -2
+    assert jit(FAKE, 64, 64, 0, None, FAKE, FAKE, 64, None, 0, None, FAKE, wb - 4, None) == -5
+    assert jit(FAKE, 64, 64, 0, None, FAKE, FAKE, 64, None, 0, FAKE, FAKE, wb, None) == -5  # + column sums
 
 
 def test_error_raises_in_python_binding():

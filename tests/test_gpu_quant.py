@@ -249,18 +249,23 @@ def test_quantize_2d_layouts(dev, fmt):
 BATCH_SHAPES = [(4800, 1600), (1600, 1600), (0, 5), (1, 1), (129, 257), (6400, 1600), (3, 40), (1600, 6400)]
 
 
+@pytest.mark.parametrize("with_empty", [True, False], ids=["with_empty", "no_empty"])
 @pytest.mark.parametrize("given_absmax", [False, True], ids=["own_absmax", "given_absmax"])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("fmt", [Fmt.E4M3, Fmt.E5M2])
-def test_quantize_2d_batch_matches_single_calls(dev, dtype, fmt, given_absmax):
+def test_quantize_2d_batch_matches_single_calls(dev, dtype, fmt, given_absmax, with_empty):
     """df_quantize_2d_batch gives every tensor the absmax, scale, row codes
     and transposed codes that df_absmax_scale + df_quantize_2d give it alone
-    (ragged shapes, an empty tensor, a 1x1, the GPT-2 XL weights).  With the
-    absmax given (df_quantize_2d_batch_absmax) the tile pass runs its
-    non-temporal instantiation, for both dtypes and formats."""
+    (ragged shapes, a 1x1, the GPT-2 XL weights).  With the absmax given
+    (df_quantize_2d_batch_absmax) the tile pass runs its non-temporal
+    instantiation, for both dtypes and formats.  Without an empty tensor every
+    tensor's tile blocks form its scale themselves (the folded form); an
+    empty tensor, which has no tile block, keeps the separate fold launch."""
     rng = np.random.default_rng(7)
     ts = []
     for i, (r, c) in enumerate(BATCH_SHAPES):
+        if r * c == 0 and not with_empty:
+            continue
         x = (rng.standard_normal((r, c)) * (0.02 * (i + 1))).astype(np.float32)
         if x.size:
             x.reshape(-1)[rng.integers(0, x.size)] = 50.0 * (i + 1)  # an outlier sets each tensor's scale
