@@ -83,21 +83,16 @@ void FullyConnectedLayer<TT>::initialize_weights() {
 }
 
 // absmax -> scale (written to scale_dev) -> 2-D codes (row copy q, transposed
-// copy qt, optional fp32 column sums), all stream ordered.
+// copy qt, optional fp32 column sums) in one stream-ordered call
+// (df_quantize_2d_jit: the same results as the absmax call followed by the
+// 2-D quantize, without the one-block launch between them).
 template <typename TT>
 void FullyConnectedLayer<TT>::quantize_operand(const TT* x, int rows, int cols, int fmt, float* scale_dev, uint8_t* q,
                                                int ldq, uint8_t* qt, int ldqt, float* colsum) {
     constexpr int dt = dtype_traits<TT>::value;
-    const size_t ab = df_absmax_workspace_bytes();
-    uint8_t* aws = absmax_ws_.get(ab);
-    absmax_of(x, (int64_t)rows * cols, fmt, nullptr, scale_dev, aws, ab);
-    if (colsum) {
-        const size_t cb = df_quantize_2d_workspace_bytes(rows, cols);
-        CHECK_DF_EX(df_quantize_2d_colsum(dt, x, rows, cols, cols, fmt, scale_dev, q, ldq, qt, ldqt, colsum,
-                                          colsum_ws_.get(cb), cb, st()));
-    } else {
-        CHECK_DF_EX(df_quantize_2d(dt, x, rows, cols, cols, fmt, scale_dev, q, ldq, qt, ldqt, st()));
-    }
+    const size_t wb = df_quantize_2d_jit_workspace_bytes(rows, cols, colsum ? 1 : 0);
+    CHECK_DF_EX(df_quantize_2d_jit(dt, x, rows, cols, fmt, nullptr, scale_dev, q, ldq, qt, ldqt, colsum,
+                                   colsum_ws_.get(wb), wb, st()));
 }
 
 template <typename TT>
