@@ -158,8 +158,10 @@ class StreamedStack:
                    for _ in range(nl)]
         # per layer and Linear: absmax X, scale X, absmax dY, scale dY
         self.sc = torch.empty((self.layers, L, 4), dtype=torch.float32, device=dev)
-        self.cws = torch.empty(max(lib().df_quantize_2d_workspace_bytes(M, N) for _, _, N in self.linears),
-                               dtype=torch.uint8, device=dev)
+        # one-call quantize (df_quantize_2d_jit): absmax partials, and the
+        # column-sum partials of dY
+        self.cws = torch.empty(max(lib().df_quantize_2d_jit_workspace_bytes(M, max(K, N), 1)
+                                   for _, K, N in self.linears), dtype=torch.uint8, device=dev)
         gws_b = max(max(lib().df_fp8_gemm_workspace_bytes(M, n, k), lib().df_fp8_gemm_bwd_workspace_bytes(M, n, k))
                     for _, k, n in self.linears)
         self.gws = torch.empty(max(gws_b, 16), dtype=torch.uint8, device=dev)
@@ -209,10 +211,8 @@ class StreamedStack:
         for i, (_, K, N) in enumerate(self.linears):
             s = self.sc_ptr(l, i)
             x, xq = self.acts[l][i], self.xq[o][i]
-            call("df_absmax_scale_bf16", x.data_ptr(), x.numel(), E4, s, s + 4, self.ws.data_ptr(), self.ws.numel(),
-                 cur)
-            call("df_quantize_2d", BF, x.data_ptr(), M, K, K, E4, s + 4, xq.data_ptr(), xq.stride(0),
-                 self.xt[l][i].data_ptr(), self.Mp, cur)
+            call("df_quantize_2d_jit", BF, x.data_ptr(), M, K, E4, s, s + 4, xq.data_ptr(), xq.stride(0),
+                 self.xt[l][i].data_ptr(), self.Mp, None, self.cws.data_ptr(), self.cws.numel(), cur)
             Y = self.Y[o][i]
             call("df_fp8_gemm_fwd", xq.data_ptr(), xq.stride(0), base + self.fwd_off[i], round16(K), M, N, K, s + 4,
                  self.sw_ptr(l, i), BF, self.bias[i].data_ptr(), self._dt(Y), Y.data_ptr(), N, self.gws.data_ptr(),
@@ -226,9 +226,7 @@ class StreamedStack:
         for i, (_, K, N) in enumerate(self.linears):
             s = self.sc_ptr(l, i)
             g, dyq, dyt = self.grads[l][i], self.dyq[o][i], self.dyt[o][i]
-            call("df_absmax_scale_bf16", g.data_ptr(), g.numel(), E5, s + 8, s + 12, self.ws.data_ptr(),
-                 self.ws.numel(), cur)
-            call("df_quantize_2d_colsum", BF, g.data_ptr(), M, N, N, E5, s + 12, dyq.data_ptr(), dyq.stride(0),
+            call("df_quantize_2d_jit", BF, g.data_ptr(), M, N, E5, s + 8, s + 12, dyq.data_ptr(), dyq.stride(0),
                  dyt.data_ptr(), self.Mp, self.db[o][i].data_ptr(), self.cws.data_ptr(), self.cws.numel(), cur)
             # dX and dW in one launch; dW reads the transposed X codes that
             # layer l's forward cached in xt[l], at that pass's scale s + 4
