@@ -1527,47 +1527,30 @@ def producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10):
 
 
 def gemm_producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10, rounds=7):
-    """The reference block's fc1 -> fc2 hand-off (transformer_block.cu:79-81:
-    fc1's bf16 Y is fc2's X, so fc2's just-in-time scale is Y's absmax) at the
-    config-4 fc shape (M x 1600 -> M x 6400), up to fc2's codes: fc1 GEMM, then
-    absmax pass over Y, then quantize Y (unfused) against the GEMM that folds
-    |Y| in its epilogue, then quantize Y (fused).  fc2's GEMM is the same in
-    both and is left out.  The absmax pass the fusion removes reads 2 bytes
-    per Y element."""
+    """The GEMM producer at the config-4 fc shapes, both directions, up to the
+    next Linear's codes.  The reference block passes fc1's bf16 Y to fc2 and,
+    in the backward, fc2's dX to fc1 as its output gradient
+    (transformer_block.cu:79-81, :127-134), so each next scale is an absmax
+    of a GEMM output.
+    - forward (M x 1600 -> M x 6400): fc1 GEMM, absmax pass over Y, quantize
+      Y (two calls; or the one-call quantize, "unfused_jit") against the GEMM
+      that folds |Y| in its epilogue, then the quantize at its scale;
+    - backward (fc2: dY M x 1600, W 1600 x 6400): the grouped dX + dW GEMM,
+      then fc1's dY quantize with the bias gradient's column sums (absmax
+      pass + quantize, or the one-call quantize) against the grouped GEMM
+      that folds |dX|, then the quantize at its scale.
+    The absmax pass the fusions remove reads 2 bytes per output element.
+    Every variant is timed in rounds that rotate their order; medians."""
     from deepfuse_amd import DType, Fmt
-    BF, E4 = int(DType.BFLOAT16), int(Fmt.E4M3)
+    BF, F32, E4, E5 = int(DType.BFLOAT16), int(DType.FLOAT32), int(Fmt.E4M3), int(Fmt.E5M2)
     N = 4 * C
-    xs = torch.from_numpy(synth.normal((M, C), 1.0, seed=1710)).to(dev).to(torch.bfloat16)
-    ws_ = torch.from_numpy(synth.normal((N, C), 0.02, seed=1711)).to(dev).to(torch.bfloat16)
-    _, sx = df.absmax_scale(xs, Fmt.E4M3)
-    _, sw = df.absmax_scale(ws_, Fmt.E4M3)
-    xq, _ = df.quantize_2d(xs, sx, Fmt.E4M3)
-    wq, _ = df.quantize_2d(ws_, sw, Fmt.E4M3)
-    del xs, ws_
-    Kp, Np, Mp = df.round16(C), df.round16(N), df.round16(M)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    q = torch.empty((M, Np), dtype=torch.uint8, device=dev)
-    qt = torch.empty((N, Mp), dtype=torch.uint8, device=dev)
-    sc = torch.empty(4, dtype=torch.float32, device=dev)
-    gws_b = max(int(df.lib().df_fp8_gemm_fwd_absmax_workspace_bytes(M, N, C)),
-                int(df.lib().df_fp8_gemm_workspace_bytes(M, N, C)), int(df.lib().df_absmax_workspace_bytes()))
-    gws = torch.empty(gws_b, dtype=torch.uint8, device=dev)
-    p = sc.data_ptr()
+    L = df.lib()
 
-    def gemm():
-        df.call("df_fp8_gemm_fwd", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, C, sx.data_ptr(), sw.data_ptr(),
-                int(DType.FLOAT32), None, BF, y.data_ptr(), N, gws.data_ptr(), gws_b, stream)
-
-    def absmax():
-        df.call("df_absmax_scale_bf16", y.data_ptr(), y.numel(), E4, None, p, gws.data_ptr(), gws_b, stream)
-
-    def fused_gemm():
-        df.call("df_fp8_gemm_fwd_absmax", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, C, sx.data_ptr(),
-                sw.data_ptr(), int(DType.FLOAT32), None, BF, y.data_ptr(), N, E4, None, p, gws.data_ptr(), gws_b,
-                stream)
-
-    def quant():
-        df.call("df_quantize_2d", BF, y.data_ptr(), M, N, N, E4, p, q.data_ptr(), Np, qt.data_ptr(), Mp, stream)
+    def operand(shape, std, seed, fmt, want_q, want_qt):
+        x = torch.from_numpy(synth.normal(shape, std, seed=seed)).to(dev).to(torch.bfloat16)
+        _, s = df.absmax_scale(x, fmt)
+        q_, qt_ = df.quantize_2d(x, s, fmt, want_q=want_q, want_qt=want_qt)
+        return q_, qt_, s
 
     def timed(fn):
         torch.cuda.synchronize()
@@ -1579,24 +1562,102 @@ def gemm_producer_bench(torch, df, synth, dev, stream, M=16384, C=1600, reps=10,
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps
 
-    # the variants in turn, over rounds that rotate their order, median per
-    # variant: back-to-back blocks of one variant drift with the clock
-    variants = (("gemm", gemm), ("absmax_pass", absmax), ("gemm_absmax", fused_gemm), ("quantize", quant),
-                ("unfused", lambda: (gemm(), absmax(), quant())), ("fused", lambda: (fused_gemm(), quant())))
-    for _, fn in variants:
-        fn()
-    times = {name: [] for name, _ in variants}
-    for r in range(rounds):
-        for j in range(len(variants)):
-            name, fn = variants[(j + r) % len(variants)]
-            times[name].append(timed(fn))
-    res = {"shape": [M, C, N], "y_dtype": "bf16", "note": f"median of {rounds} rotated rounds of {reps} calls"}
-    for name, _ in variants:
-        res[name + "_ms"] = round(sorted(times[name])[rounds // 2], 4)
-    res["epilogue_fold_ms"] = round(res["gemm_absmax_ms"] - res["gemm_ms"], 4)  # with the partials' fold
-    res["absmax_pass_gbs"] = round(M * N * 2 / (res["absmax_pass_ms"] * 1e-3) / 1e9, 1)
-    res["saved_ms"] = round(res["unfused_ms"] - res["fused_ms"], 4)
-    return res
+    def rotated(variants):
+        # back-to-back blocks of one variant drift with the clock
+        for _, fn in variants:
+            fn()
+        times = {name: [] for name, _ in variants}
+        for r in range(rounds):
+            for j in range(len(variants)):
+                name, fn = variants[(j + r) % len(variants)]
+                times[name].append(timed(fn))
+        return {name + "_ms": round(sorted(t)[rounds // 2], 4) for name, t in times.items()}
+
+    Kp, Np, Mp = df.round16(C), df.round16(N), df.round16(M)
+    sc = torch.empty(8, dtype=torch.float32, device=dev)
+    p = sc.data_ptr()
+    # ---- forward: fc1
+    xq, _, sx = operand((M, C), 1.0, 1710, Fmt.E4M3, True, False)
+    wq, _, sw = operand((N, C), 0.02, 1711, Fmt.E4M3, True, False)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    q = torch.empty((M, Np), dtype=torch.uint8, device=dev)
+    qt = torch.empty((N, Mp), dtype=torch.uint8, device=dev)
+    gws_b = max(int(L.df_fp8_gemm_fwd_absmax_workspace_bytes(M, N, C)), int(L.df_fp8_gemm_workspace_bytes(M, N, C)),
+                int(L.df_absmax_workspace_bytes()), int(L.df_quantize_2d_jit_workspace_bytes(M, N, 1)),
+                int(L.df_fp8_gemm_bwd_absmax_workspace_bytes(M, C, N)))
+    gws = torch.empty(gws_b, dtype=torch.uint8, device=dev)
+
+    def gemm():
+        df.call("df_fp8_gemm_fwd", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, C, sx.data_ptr(), sw.data_ptr(),
+                F32, None, BF, y.data_ptr(), N, gws.data_ptr(), gws_b, stream)
+
+    def absmax():
+        df.call("df_absmax_scale_bf16", y.data_ptr(), y.numel(), E4, None, p, gws.data_ptr(), gws_b, stream)
+
+    def fused_gemm():
+        df.call("df_fp8_gemm_fwd_absmax", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, C, sx.data_ptr(),
+                sw.data_ptr(), F32, None, BF, y.data_ptr(), N, E4, None, p, gws.data_ptr(), gws_b, stream)
+
+    def quant():
+        df.call("df_quantize_2d", BF, y.data_ptr(), M, N, N, E4, p, q.data_ptr(), Np, qt.data_ptr(), Mp, stream)
+
+    def quant_jit():
+        df.call("df_quantize_2d_jit", BF, y.data_ptr(), M, N, E4, None, p, q.data_ptr(), Np, qt.data_ptr(), Mp,
+                None, gws.data_ptr(), gws_b, stream)
+
+    fwd = {"shape": [M, C, N], "y_dtype": "bf16"}
+    fwd.update(rotated((("gemm", gemm), ("absmax_pass", absmax), ("gemm_absmax", fused_gemm), ("quantize", quant),
+                        ("unfused", lambda: (gemm(), absmax(), quant())),
+                        ("unfused_jit", lambda: (gemm(), quant_jit())),
+                        ("fused", lambda: (fused_gemm(), quant())))))
+    fwd["epilogue_fold_ms"] = round(fwd["gemm_absmax_ms"] - fwd["gemm_ms"], 4)  # with the partials' fold
+    fwd["absmax_pass_gbs"] = round(M * N * 2 / (fwd["absmax_pass_ms"] * 1e-3) / 1e9, 1)
+    fwd["saved_ms"] = round(fwd["unfused_ms"] - fwd["fused_ms"], 4)
+    fwd["saved_vs_jit_ms"] = round(fwd["unfused_jit_ms"] - fwd["fused_ms"], 4)
+    del xq, wq
+    # ---- backward: fc2 (dY [M, C] e5m2, W [C, N] e4m3, X = fc1's Y [M, N]); dX [M, N] is fc1's dY
+    dyq, dyt, sdy = operand((M, C), 1e-3, 1712, Fmt.E5M2, True, True)
+    _, wt, sw2 = operand((C, N), 0.02, 1713, Fmt.E4M3, False, True)
+    _, xt, sx2 = operand((M, N), 1.0, 1714, Fmt.E4M3, False, True)
+    dX = y  # [M, N] bf16
+    dW = torch.empty((C, N), dtype=torch.float32, device=dev)
+    db = torch.empty(N, dtype=torch.float32, device=dev)
+    bws_b = int(L.df_fp8_gemm_bwd_workspace_bytes(M, C, N))
+    cws = torch.empty(int(L.df_quantize_2d_workspace_bytes(M, N)), dtype=torch.uint8, device=dev)
+
+    def bwd():
+        df.call("df_fp8_gemm_bwd", dyq.data_ptr(), dyq.stride(0), wt.data_ptr(), wt.stride(0), dyt.data_ptr(),
+                dyt.stride(0), xt.data_ptr(), xt.stride(0), M, C, N, sdy.data_ptr(), sw2.data_ptr(), sx2.data_ptr(),
+                BF, dX.data_ptr(), N, F32, dW.data_ptr(), N, gws.data_ptr(), bws_b, stream)
+
+    def absmax_dx():
+        df.call("df_absmax_scale_bf16", dX.data_ptr(), dX.numel(), E5, None, p + 4, gws.data_ptr(), gws_b, stream)
+
+    def fused_bwd():
+        df.call("df_fp8_gemm_bwd_absmax", dyq.data_ptr(), dyq.stride(0), wt.data_ptr(), wt.stride(0),
+                dyt.data_ptr(), dyt.stride(0), xt.data_ptr(), xt.stride(0), M, C, N, sdy.data_ptr(), sw2.data_ptr(),
+                sx2.data_ptr(), BF, dX.data_ptr(), N, F32, dW.data_ptr(), N, E5, None, p + 4, gws.data_ptr(), gws_b,
+                stream)
+
+    def quant_dy():
+        df.call("df_quantize_2d_colsum", BF, dX.data_ptr(), M, N, N, E5, p + 4, q.data_ptr(), Np, qt.data_ptr(), Mp,
+                db.data_ptr(), cws.data_ptr(), cws.numel(), stream)
+
+    def quant_dy_jit():
+        df.call("df_quantize_2d_jit", BF, dX.data_ptr(), M, N, E5, None, p + 4, q.data_ptr(), Np, qt.data_ptr(), Mp,
+                db.data_ptr(), gws.data_ptr(), gws_b, stream)
+
+    bw = {"shape": [M, C, N], "dx_dtype": "bf16", "dw_dtype": "fp32",
+          "grouped_plan": list(df.gemm_bwd_plan(M, C, N))}
+    bw.update(rotated((("gemm_bwd", bwd), ("absmax_pass", absmax_dx), ("gemm_bwd_absmax", fused_bwd),
+                       ("quantize_colsum", quant_dy),
+                       ("unfused", lambda: (bwd(), absmax_dx(), quant_dy())),
+                       ("unfused_jit", lambda: (bwd(), quant_dy_jit())),
+                       ("fused", lambda: (fused_bwd(), quant_dy())))))
+    bw["epilogue_fold_ms"] = round(bw["gemm_bwd_absmax_ms"] - bw["gemm_bwd_ms"], 4)
+    bw["saved_ms"] = round(bw["unfused_ms"] - bw["fused_ms"], 4)
+    bw["saved_vs_jit_ms"] = round(bw["unfused_jit_ms"] - bw["fused_ms"], 4)
+    return {"note": f"median of {rounds} rotated rounds of {reps} calls", "forward": fwd, "backward": bw}
 
 
 def optimizer_bench(torch, df, dev, stream, layers=48, reps=5):

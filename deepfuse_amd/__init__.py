@@ -110,6 +110,10 @@ _SIGS = {
     "df_fp8_gemm_bwd_plan": (_c_int, [_c_int, _c_int, _c_int, _c_sz, _vp, _vp]),
     "df_fp8_gemm_bwd": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
                                  _vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+    "df_fp8_gemm_bwd_absmax_workspace_bytes": (_c_sz, [_c_int, _c_int, _c_int]),
+    "df_fp8_gemm_bwd_absmax": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
+                                        _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp, _vp,
+                                        _vp, _c_sz, _vp]),
     "df_fill": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp]),
     "df_add": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _vp]),
     "df_convert": (_c_int, [_c_int, _vp, _c_int, _vp, _c_i64, _vp]),
@@ -430,6 +434,26 @@ def quantize_2d_batch(tensors, fmt: Fmt, want_q=True, want_qt=True, absmax=None)
     else:
         call("df_quantize_2d_batch_absmax", *head, *tail, _stream())
     return am, sc, qs, qts
+
+
+def gemm_bwd_absmax(dy_q, wt_q, dyt_q, xt_q, M: int, N: int, K: int, sdy, sw, sx, dx_dtype=None, dw_dtype=None,
+                    next_fmt: Fmt = Fmt.E5M2):
+    """gemm_bwd whose dX also gives its absmax and the rule-D1/D2 scale for
+    next_fmt (df_fp8_gemm_bwd_absmax): returns (dX, dW, absmax, scale)."""
+    torch = _torch()
+    dx_dtype = dx_dtype or torch.bfloat16
+    dw_dtype = dw_dtype or torch.float32
+    dev = dy_q.device
+    dX = torch.empty((M, K), dtype=dx_dtype, device=dev)
+    dW = torch.empty((N, K), dtype=dw_dtype, device=dev)
+    am = torch.empty(1, dtype=torch.float32, device=dev)
+    sc = torch.empty(1, dtype=torch.float32, device=dev)
+    dt = lambda t: int(_in_dtype(torch.empty(0, dtype=t)))
+    ws = _scratch(dev, max(int(lib().df_fp8_gemm_bwd_absmax_workspace_bytes(M, N, K)), 16), "gemm_bwd_absmax")
+    call("df_fp8_gemm_bwd_absmax", _ptr(dy_q), dy_q.stride(0), _ptr(wt_q), wt_q.stride(0), _ptr(dyt_q),
+         dyt_q.stride(0), _ptr(xt_q), xt_q.stride(0), M, N, K, _ptr(sdy), _ptr(sw), _ptr(sx), dt(dx_dtype), _ptr(dX),
+         K, dt(dw_dtype), _ptr(dW), K, int(next_fmt), _ptr(am), _ptr(sc), _ptr(ws), ws.numel(), _stream())
+    return dX, dW, am, sc
 
 
 def gemm_bwd_plan(M: int, N: int, K: int, ws_bytes: int | None = None):

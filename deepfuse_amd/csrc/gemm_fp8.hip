@@ -531,11 +531,12 @@ template <typename T> struct Tag { using type = T; };
 // block's start ([0]) and, for its tile t, at the tile's first half-step
 // ([1 + 3t]), before its epilogue ([2 + 3t]) and after it ([3 + 3t]), while
 // 1 + 3t + 2 < tl_per_block; every other instantiation compiles none of it.
-// AMAX_OUT (df_fp8_gemm_fwd_absmax; one problem, unsplit, bf16 or fp32 C):
+// AMAX_OUT (df_fp8_gemm_fwd_absmax: one problem, unsplit; df_fp8_gemm_bwd_absmax:
+// grouped, the second problem's (dX's) tiles only; bf16 or fp32 output):
 // the epilogue also folds |C| over the finite values it stores, as stored
-// (after the conversion to OutT), with the compare-free biased folds, and
-// after its last tile wave w of block bl writes its maximum (a binary32
-// pattern) to amax_part[bl * 8 + w].
+// (after the conversion to the output type), with the compare-free biased
+// folds, and after its last tile wave w of block bl writes its maximum (a
+// binary32 pattern) to amax_part[bl * 8 + w].
 template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS, bool SPLIT, typename OutT1, bool NARROW,
           bool TIMELINE = false, bool AMAX_OUT = false>
 __device__ __forceinline__ void persistent_body(
@@ -545,9 +546,11 @@ __device__ __forceinline__ void persistent_body(
     uint64_t* __restrict__ tl = nullptr, int tl_per_block = 0, uint32_t* __restrict__ amax_part = nullptr) {
     constexpr bool GROUPED = !std::is_void<OutT1>::value;
     static_assert(!NARROW || (!GROUPED && !SPLIT), "narrow tiles: one problem, unsplit");
-    static_assert(!AMAX_OUT || (!GROUPED && !SPLIT && !NARROW &&
-                                (std::is_same<OutT, uint16_t>::value || std::is_same<OutT, float>::value)),
-                  "output absmax: one problem, unsplit, 256x256 tiles, bf16 or fp32 output");
+    using FoldT = typename std::conditional<GROUPED, OutT1, OutT>::type;
+    static_assert(!AMAX_OUT || (!NARROW && (GROUPED || !SPLIT) &&
+                                (std::is_same<FoldT, uint16_t>::value || std::is_same<FoldT, float>::value)),
+                  "output absmax: 256x256 tiles, the unsplit single problem or a grouped launch's second "
+                  "problem, bf16 or fp32 output");
     using Out1 = typename std::conditional<GROUPED, OutT1, OutT>::type;
     constexpr int FM = NARROW ? 2 : 4, FN = 2;    // 32x32 MFMA tiles per wave
     constexpr int BN = NARROW ? 128 : kPBN;       // tile columns
@@ -840,11 +843,12 @@ __device__ __forceinline__ void persistent_body(
     // always inlined: when both problems store the same type this lambda is
     // called from two places, and an outlined copy would take acc by
     // reference, i.e. through scratch memory
-    auto store_tile = [&](auto tag, auto with_bias, typename decltype(tag)::type* const Cu, int Mo, int No,
-                          int ldco, int veco, float sabo, int tile, int tm0,
+    auto store_tile = [&](auto tag, auto with_bias, auto fold, typename decltype(tag)::type* const Cu, int Mo,
+                          int No, int ldco, int veco, float sabo, int tile, int tm0,
                           int tn0) __attribute__((always_inline)) {
         using T = typename decltype(tag)::type;
         constexpr bool BIAS = decltype(with_bias)::value;
+        constexpr bool FOLD = AMAX_OUT && decltype(fold)::value;  // this problem's |C| goes into am_acc
         constexpr int ES = (int)sizeof(T);
         constexpr int SR = EpiGeom<ES>::SR, SROW = EpiGeom<ES>::SROW;
         constexpr int NPASS = EpiGeom<ES>::NPASS, SPP = EpiGeom<ES>::SPP;
@@ -954,12 +958,12 @@ __device__ __forceinline__ void persistent_body(
                                 __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
                             else
                                 *reinterpret_cast<u32x4*>(dst) = val;
-                            if constexpr (AMAX_OUT && ES == 2) {
+                            if constexpr (FOLD && ES == 2) {
                                 am_acc = fold_bf16x2_biased(am_acc, val.x);
                                 am_acc = fold_bf16x2_biased(am_acc, val.y);
                                 am_acc = fold_bf16x2_biased(am_acc, val.z);
                                 am_acc = fold_bf16x2_biased(am_acc, val.w);
-                            } else if constexpr (AMAX_OUT) {
+                            } else if constexpr (FOLD) {
                                 am_acc = fold_f32_biased(am_acc, val.x); am_acc = fold_f32_biased(am_acc, val.y);
                                 am_acc = fold_f32_biased(am_acc, val.z); am_acc = fold_f32_biased(am_acc, val.w);
                             }
@@ -969,10 +973,10 @@ __device__ __forceinline__ void persistent_body(
                             for (int x = 0; x < 16 / ES; ++x)
                                 if (scol + x < No) {
                                     dst[x] = ev[x];
-                                    if constexpr (AMAX_OUT && ES == 2)  // the value in the low half
+                                    if constexpr (FOLD && ES == 2)  // the value in the low half
                                         am_acc = fold_bf16x2_biased(
                                             am_acc, (uint32_t)reinterpret_cast<const uint16_t*>(ev)[x]);
-                                    else if constexpr (AMAX_OUT)
+                                    else if constexpr (FOLD)
                                         am_acc = fold_f32_biased(am_acc, reinterpret_cast<const uint32_t*>(ev)[x]);
                                 }
                         }
@@ -989,10 +993,11 @@ __device__ __forceinline__ void persistent_body(
         tile_mn(tile, tp, tm0, tn0, tkb, tnku, tslot);
         bool whole;
         if (GROUPED && tp)
-            whole = store_tile(Tag<Out1>{}, std::false_type{}, static_cast<Out1*>(p1.C), p1.M, p1.N, p1.ldc,
-                               p1.vec_out, sab1, tile, tm0, tn0);
+            whole = store_tile(Tag<Out1>{}, std::false_type{}, std::true_type{}, static_cast<Out1*>(p1.C), p1.M,
+                               p1.N, p1.ldc, p1.vec_out, sab1, tile, tm0, tn0);
         else
             whole = store_tile(Tag<OutT>{}, std::integral_constant<bool, HAS_BIAS>{},
+                               std::integral_constant<bool, !GROUPED>{},
                                SPLIT ? C + (int64_t)tslot * M * N : C, M, N, ldc, vec_out, sab, tile, tm0, tn0);
         after_epi = whole ? 1 : 2;
     };
@@ -1030,7 +1035,7 @@ __device__ __forceinline__ void persistent_body(
         stamp(3 + 3 * tile);
     }
     if constexpr (AMAX_OUT) {  // every block, tiles or none, writes its 8 partials
-        uint32_t m = sizeof(OutT) == 2 ? unbias_bf16x2(am_acc) : unbias_f32(am_acc);
+        uint32_t m = sizeof(FoldT) == 2 ? unbias_bf16x2(am_acc) : unbias_f32(am_acc);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
         if (lane == 0) amax_part[bl * 8 + w] = m;
@@ -1064,6 +1069,16 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persistent_amax_kernel(
     OutT* __restrict__ C, int ldc, int vec_out, uint32_t* __restrict__ amax_part) {
     persistent_body<FA, FB, OutT, BiasT, HAS_BIAS, false, void, false, false, true>(
         A, lda, B, ldb, M, N, K, sa, sb, bias, C, ldc, vec_out, 0, 1, PProb{}, nullptr, 0, amax_part);
+}
+
+// The grouped dX + dW launch that also folds |dX| (df_fp8_gemm_bwd_absmax).
+template <int FA, int FB, typename OutT, bool SPLIT, typename OutT1>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persistent_grouped_amax_kernel(
+    const uint8_t* __restrict__ A, int lda, const uint8_t* __restrict__ B, int ldb, int M, int N, int K,
+    const float* __restrict__ sa, const float* __restrict__ sb, OutT* __restrict__ C, int ldc, int vec_out,
+    int ksteps, int nsplit, PProb p1, uint32_t* __restrict__ amax_part) {
+    persistent_body<FA, FB, OutT, float, false, SPLIT, OutT1, false, false, true>(
+        A, lda, B, ldb, M, N, K, sa, sb, nullptr, C, ldc, vec_out, ksteps, nsplit, p1, nullptr, 0, amax_part);
 }
 
 template <int FA, int FB, typename OutT, typename BiasT, bool HAS_BIAS>
@@ -1428,20 +1443,42 @@ static GroupPlan grouped_plan(const GemmArgs& dw, const GemmArgs& dx, size_t ws_
     return best;
 }
 
+// amax_part non-NULL: the launch also folds |dX| into 8 partials per block
+// (grid = cus), for df_fp8_gemm_bwd_absmax.
 template <typename DwT, typename DxT>
-static void launch_grouped(const GemmArgs& dw, const GemmArgs& dx, const GroupPlan& gp, int cus) {
+static void launch_grouped(const GemmArgs& dw, const GemmArgs& dx, const GroupPlan& gp, int cus,
+                           uint32_t* amax_part = nullptr) {
     const PProb p1{dx.A, dx.B, dx.C, dx.sa, dx.sb, dx.lda, dx.ldb, dx.M, dx.N, dx.K, dx.ldc,
                    epi_store_mode(dx.C, (int64_t)dx.ldc * (int64_t)sizeof(DxT))};
+    constexpr bool FOLDS = std::is_same<DxT, uint16_t>::value || std::is_same<DxT, float>::value;
     if (gp.S == 1) {
         const int vec_out = epi_store_mode(dw.C, (int64_t)dw.ldc * (int64_t)sizeof(DwT));
+        if constexpr (FOLDS) {
+            if (amax_part) {
+                gemm_nt_persistent_grouped_amax_kernel<E5M2, E4M3, DwT, false, DxT><<<cus, 512, 0, dw.st>>>(
+                    dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, static_cast<DwT*>(dw.C), dw.ldc,
+                    vec_out, 0, 1, p1, amax_part);
+                return;
+            }
+        }
         gemm_nt_persistent_kernel<E5M2, E4M3, DwT, float, false, false, DxT><<<cus, 512, 0, dw.st>>>(
             dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, static_cast<DwT*>(dw.C), dw.ldc,
             vec_out, 0, 1, p1);
         return;
     }
-    gemm_nt_persistent_kernel<E5M2, E4M3, float, float, false, true, DxT><<<cus, 512, 0, dw.st>>>(
-        dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, dw.ws, dw.N,
-        epi_store_mode(dw.ws, (int64_t)dw.N * 4), gp.L, gp.S, p1);
+    bool launched = false;
+    if constexpr (FOLDS) {
+        if (amax_part) {
+            gemm_nt_persistent_grouped_amax_kernel<E5M2, E4M3, float, true, DxT><<<cus, 512, 0, dw.st>>>(
+                dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, dw.ws, dw.N,
+                epi_store_mode(dw.ws, (int64_t)dw.N * 4), gp.L, gp.S, p1, amax_part);
+            launched = true;
+        }
+    }
+    if (!launched)
+        gemm_nt_persistent_kernel<E5M2, E4M3, float, float, false, true, DxT><<<cus, 512, 0, dw.st>>>(
+            dw.A, dw.lda, dw.B, dw.ldb, dw.M, dw.N, dw.K, dw.sa, dw.sb, nullptr, dw.ws, dw.N,
+            epi_store_mode(dw.ws, (int64_t)dw.N * 4), gp.L, gp.S, p1);
     const int64_t total = (int64_t)dw.M * dw.N;
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
     const bool vec_red = (dw.N % 4 == 0) && ((int64_t)dw.ldc * (int64_t)sizeof(DwT)) % 16 == 0 && aligned16(dw.C);
@@ -1704,11 +1741,12 @@ extern "C" int df_fp8_gemm_bwd_plan(int M, int N, int K, size_t ws_bytes, int* g
     return DF_OK;
 }
 
-extern "C" int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, const uint8_t* dYtq,
-                               int ldyt, const uint8_t* Xtq, int ldxt, int M, int N, int K, const float* sdy_dev,
-                               const float* sw_dev, const float* sx_dev, int dx_dtype, void* dX, int lddx,
-                               int dw_dtype, void* dW, int lddw, void* ws, size_t ws_bytes, void* stream) {
-    clear_error();
+// df_fp8_gemm_bwd; with amax_part (room for 8 partials per CU), a grouped
+// plan also folds |dX| into it and *folded is set.
+static int bwd_impl(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, const uint8_t* dYtq, int ldyt,
+                    const uint8_t* Xtq, int ldxt, int M, int N, int K, const float* sdy_dev, const float* sw_dev,
+                    const float* sx_dev, int dx_dtype, void* dX, int lddx, int dw_dtype, void* dW, int lddw,
+                    void* ws, size_t ws_bytes, void* stream, uint32_t* amax_part, bool* folded) {
     GemmArgs dx, dw;
     bool ex = false, ew = false;
     int st = nt_args("df_fp8_gemm_bwd (dX)", DF_FMT_E5M2, dYq, lddy, DF_FMT_E4M3, Wtq, ldwt, M, K, N, sdy_dev,
@@ -1732,10 +1770,72 @@ extern "C" int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq,
                                   stream);
     }
     const bool dw32 = dw_dtype == DF_DTYPE_FLOAT32, dx32 = dx_dtype == DF_DTYPE_FLOAT32;
-    if (h_dx) launch_grouped<f16_t, f16_t>(dw, dx, gp, cus);
+    if (amax_part && !h_dx) {
+        if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus, amax_part);
+        else if (dw32) launch_grouped<float, uint16_t>(dw, dx, gp, cus, amax_part);
+        else if (dx32) launch_grouped<uint16_t, float>(dw, dx, gp, cus, amax_part);
+        else launch_grouped<uint16_t, uint16_t>(dw, dx, gp, cus, amax_part);
+        *folded = true;
+    } else if (h_dx) launch_grouped<f16_t, f16_t>(dw, dx, gp, cus);
     else if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus);
     else if (dw32) launch_grouped<float, uint16_t>(dw, dx, gp, cus);
     else if (dx32) launch_grouped<uint16_t, float>(dw, dx, gp, cus);
     else launch_grouped<uint16_t, uint16_t>(dw, dx, gp, cus);
     return launch_status("df_fp8_gemm_bwd");
+}
+
+extern "C" int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, const uint8_t* dYtq,
+                               int ldyt, const uint8_t* Xtq, int ldxt, int M, int N, int K, const float* sdy_dev,
+                               const float* sw_dev, const float* sx_dev, int dx_dtype, void* dX, int lddx,
+                               int dw_dtype, void* dW, int lddw, void* ws, size_t ws_bytes, void* stream) {
+    clear_error();
+    return bwd_impl(dYq, lddy, Wtq, ldwt, dYtq, ldyt, Xtq, ldxt, M, N, K, sdy_dev, sw_dev, sx_dev, dx_dtype, dX, lddx,
+                    dw_dtype, dW, lddw, ws, ws_bytes, stream, nullptr, nullptr);
+}
+
+// The backward whose dX also yields its absmax and the next quantize's
+// scale.  The first kBwdAmaxReserve bytes of ws hold the absmax partials
+// (8 per block of the grouped launch, one block per CU, or the absmax pass's
+// partials); the rest is df_fp8_gemm_bwd's workspace.
+constexpr int kBwdAmaxMaxCus = 1024;
+constexpr size_t kBwdAmaxReserve = (size_t)kBwdAmaxMaxCus * 8 * sizeof(uint32_t);
+
+extern "C" size_t df_fp8_gemm_bwd_absmax_workspace_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return kBwdAmaxReserve + df_fp8_gemm_bwd_workspace_bytes(M, N, K);
+}
+
+extern "C" int df_fp8_gemm_bwd_absmax(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
+                                      const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ldxt, int M, int N,
+                                      int K, const float* sdy_dev, const float* sw_dev, const float* sx_dev,
+                                      int dx_dtype, void* dX, int lddx, int dw_dtype, void* dW, int lddw,
+                                      int next_fmt, float* dx_absmax_dev, float* dx_scale_dev, void* ws,
+                                      size_t ws_bytes, void* stream) {
+    clear_error();
+    static const char* name = "df_fp8_gemm_bwd_absmax";
+    DF_CHECK(dx_dtype == DF_DTYPE_BFLOAT16 || dx_dtype == DF_DTYPE_FLOAT32, DF_ERR_UNSUPPORTED,
+             "%s: dX dtype %d (bf16 or fp32 only)", name, dx_dtype);
+    DF_CHECK(next_fmt == E4M3 || next_fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad fp8 format %d", name, next_fmt);
+    DF_CHECK(dx_absmax_dev || dx_scale_dev, DF_ERR_INVALID, "%s: no absmax or scale output", name);
+    DF_CHECK(lddx == K, DF_ERR_INVALID, "%s: dX must be contiguous (lddx=%d, K=%d)", name, lddx, K);
+    DF_CHECK(ws && aligned16(ws) && ws_bytes >= kBwdAmaxReserve, DF_ERR_WORKSPACE,
+             "%s: needs a 16-byte aligned workspace of at least %zu bytes", name, kBwdAmaxReserve);
+    hipStream_t s = as_stream(stream);
+    uint32_t* parts = static_cast<uint32_t*>(ws);
+    const int cus = device_cu_count();
+    bool folded = false;
+    int st = bwd_impl(dYq, lddy, Wtq, ldwt, dYtq, ldyt, Xtq, ldxt, M, N, K, sdy_dev, sw_dev, sx_dev, dx_dtype, dX,
+                      lddx, dw_dtype, dW, lddw, static_cast<char*>(ws) + kBwdAmaxReserve, ws_bytes - kBwdAmaxReserve,
+                      stream, cus > 0 && cus <= kBwdAmaxMaxCus ? parts : nullptr, &folded);
+    if (st != DF_OK) return st;
+    if (folded) {
+        launch_absmax_fold(parts, cus * 8, next_fmt, dx_absmax_dev, dx_scale_dev, s);
+        return launch_status(name);
+    }
+    const int64_t n = (int64_t)M * K;
+    return dx_dtype == DF_DTYPE_BFLOAT16
+               ? df_absmax_scale_bf16(static_cast<const uint16_t*>(dX), n, next_fmt, dx_absmax_dev, dx_scale_dev,
+                                      ws, kBwdAmaxReserve, stream)
+               : df_absmax_scale_f32(static_cast<const float*>(dX), n, next_fmt, dx_absmax_dev, dx_scale_dev, ws,
+                                     kBwdAmaxReserve, stream);
 }

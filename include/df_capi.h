@@ -407,6 +407,27 @@ int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
                     const float* sx_dev, int dx_dtype, void* dX, int lddx,
                     int dw_dtype, void* dW, int lddw,
                     void* ws, size_t ws_bytes, void* stream);
+/* df_fp8_gemm_bwd whose dX also gives the absmax the upstream Linear's
+ * just-in-time dY scale needs (new; no counterpart in the reference, whose
+ * TransformerBlock backward passes fc2's input gradient straight to fc1 as
+ * its output gradient, dnn/layers/transformer_block.cu:127-134).  dX (bf16
+ * or fp32, contiguous: lddx == K, 16-byte aligned) and dW are bit-identical
+ * to df_fp8_gemm_bwd's with a workspace of df_fp8_gemm_bwd_workspace_bytes.
+ * *dx_absmax_dev gets the absmax over the finite values of dX as stored and
+ * *dx_scale_dev the rule-D1/D2 scale for next_fmt (either may be NULL, not
+ * both): what df_absmax_scale_bf16 / _f32 give on dX.  When the plan is the
+ * grouped launch, its dX tiles fold |dX| in their epilogue and one block
+ * folds the partials; otherwise dX is read again by the absmax pass.  ws:
+ * df_fp8_gemm_bwd_absmax_workspace_bytes(M, N, K) (its first part holds the
+ * partials, the rest is df_fp8_gemm_bwd's workspace). */
+size_t df_fp8_gemm_bwd_absmax_workspace_bytes(int M, int N, int K);
+int df_fp8_gemm_bwd_absmax(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
+                           const uint8_t* dYtq, int ldyt, const uint8_t* Xtq, int ldxt,
+                           int M, int N, int K, const float* sdy_dev, const float* sw_dev,
+                           const float* sx_dev, int dx_dtype, void* dX, int lddx,
+                           int dw_dtype, void* dW, int lddw, int next_fmt,
+                           float* dx_absmax_dev, float* dx_scale_dev,
+                           void* ws, size_t ws_bytes, void* stream);
 
 /* ---- layer weight streaming (new: the reference describes layer-serialized
  * execution, README.md:212-226, and has its host-side pieces in the NVMe

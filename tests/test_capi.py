@@ -82,6 +82,16 @@ def test_argument_errors():
     assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, f32, FAKE, 8, 0, FAKE, None, FAKE, 4096, None) == -1
     assert "contiguous" in err()
     assert df.lib().df_fp8_gemm_fwd_absmax_workspace_bytes(16384, 6400, 1600) >= 64 * 25 * 8 * 4
+    # backward with dX's absmax: bf16 / fp32 dX, a known format, an output, contiguous dX, room for the partials
+    ba = lambda dxt, lddx, fmt, am, sc, wsb: status(
+        "df_fp8_gemm_bwd_absmax", FAKE, 16, FAKE, 16, FAKE, 16, FAKE, 16, 16, 16, 16, FAKE, FAKE, FAKE, dxt, FAKE, lddx,
+        f32, FAKE, 16, fmt, am, sc, FAKE, wsb, None)
+    assert ba(int(DType.HALF), 16, 1, FAKE, FAKE, 1 << 20) == -2
+    assert ba(bf, 16, 9, FAKE, FAKE, 1 << 20) == -2
+    assert ba(bf, 16, 1, None, None, 1 << 20) == -1
+    assert ba(f32, 32, 1, FAKE, None, 1 << 20) == -1
+    assert "contiguous" in err()
+    assert ba(bf, 16, 1, None, FAKE, 1024) == -5
     # tensor utilities
     assert status("df_fill", FAKE, 4, 3, ctypes.byref(ctypes.c_int(0)), None) == -2
     assert status("df_add", 99, FAKE, FAKE, FAKE, 4, None) == -2

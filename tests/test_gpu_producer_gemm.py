@@ -1,5 +1,6 @@
-"""GPU parity of df_fp8_gemm_fwd_absmax: the forward GEMM whose Y also gives
-its absmax and the next quantize's scale.
+"""GPU parity of df_fp8_gemm_fwd_absmax and df_fp8_gemm_bwd_absmax: the
+forward GEMM whose Y, and the backward whose dX, also gives its absmax and
+the next quantize's scale.
 
 The reference's TransformerBlock feeds fc1's output straight into fc2
 (dnn/layers/transformer_block.cu:79-81), so fc2's just-in-time scale is the
@@ -13,6 +14,9 @@ absmax of fc1's Y.  Bars:
   ragged and long-K shapes take the two-pass path, with the same results;
 - the codes the next Linear quantizes from Y at that scale equal the
   oracle's codes of Y.
+The backward (second half of the file): dX and dW bit-identical to
+df_fp8_gemm_bwd's, on the grouped plans (dW unsplit and in K slices) and the
+separate launches, and dX's absmax and scale to df_absmax_scale_* of dX.
 """
 import numpy as np
 import pytest
@@ -121,3 +125,97 @@ def test_fused_fold_skips_inf_and_nan(dev, out):
         assert am.view(torch.int32).item() == am_ref.view(torch.int32).item()
         assert sc.view(torch.int32).item() == sc_ref.view(torch.int32).item()
     assert am.item() == 0.0
+
+
+# ---- the backward mirror: df_fp8_gemm_bwd_absmax.  The reference block's
+# backward passes fc2's input gradient straight to fc1 as its output
+# gradient (dnn/layers/transformer_block.cu:127-134), so fc1's just-in-time
+# dY scale is the absmax of fc2's dX.
+
+def _operand(dev, shape, std, seed, fmt, want_q, want_qt):
+    x = torch.from_numpy(synth.normal(shape, std, seed=seed)).to(dev)
+    _, s = df.absmax_scale(x, fmt)
+    q, qt = df.quantize_2d(x, s, fmt, want_q=want_q, want_qt=want_qt)
+    return q, qt, s
+
+
+def _bwd_operands(dev, M, K, N, seed):
+    dyq, dyt, sdy = _operand(dev, (M, N), 1e-3, seed, Fmt.E5M2, True, True)
+    _, wt, sw = _operand(dev, (N, K), 0.02, seed + 1, Fmt.E4M3, False, True)
+    _, xt, sx = _operand(dev, (M, K), 1.0, seed + 2, Fmt.E4M3, False, True)
+    return dyq, wt, dyt, xt, sdy, sw, sx
+
+
+BWD_CASES = [
+    # M, K, N: the config-4 Linears (grouped; dW unsplit or in K slices, as the plan decides), a
+    # config-3 one, small and ragged ones (grouped too), and small dX with long reductions, whose
+    # dX would be cut into K slices: those take the two separate launches
+    (16384, 1600, 4800), (16384, 1600, 1600), (16384, 1600, 6400), (16384, 6400, 1600),
+    (8192, 768, 2304), (129, 272, 257), (1, 4, 3), (1407, 53, 3584), (300, 64, 8192),
+]
+
+
+@pytest.mark.parametrize("M,K,N", BWD_CASES)
+def test_bwd_absmax_matches_separate_passes(dev, M, K, N):
+    print(f"bwd absmax {M}x{K}x{N} plan {df.gemm_bwd_plan(M, N, K)}", flush=True)
+    dyq, wt, dyt, xt, sdy, sw, sx = _bwd_operands(dev, M, K, N, seed=7100 + M + 3 * K + 5 * N)
+    for dx_dt, dw_dt, fmt in ((torch.bfloat16, torch.float32, Fmt.E5M2), (torch.float32, torch.bfloat16, Fmt.E4M3)):
+        dX, dW, am, sc = df.gemm_bwd_absmax(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, dx_dtype=dx_dt, dw_dtype=dw_dt,
+                                            next_fmt=fmt)
+        dX1, dW1 = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, dx_dtype=dx_dt, dw_dtype=dw_dt)
+        bits = lambda t: t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
+        assert torch.equal(bits(dX), bits(dX1)), f"{M}x{K}x{N}: dX"
+        assert torch.equal(bits(dW), bits(dW1)), f"{M}x{K}x{N}: dW"
+        am1, sc1 = df.absmax_scale(dX1, fmt)
+        assert am.view(torch.int32).item() == am1.view(torch.int32).item(), f"{M}x{K}x{N}: absmax"
+        assert sc.view(torch.int32).item() == sc1.view(torch.int32).item(), f"{M}x{K}x{N}: scale"
+
+
+def test_bwd_absmax_cases_cover_every_plan(dev):
+    """The cases above include a grouped launch with dW unsplit, one with dW
+    in K slices (the fold runs in both kernels) and the separate launches."""
+    kinds = set()
+    for M, K, N in BWD_CASES:
+        grouped, slices = df.gemm_bwd_plan(M, N, K)
+        kinds.add("separate" if not grouped else "split" if slices > 1 else "grouped")
+    assert kinds == {"separate", "grouped", "split"}, kinds
+
+
+def test_fc1_dy_codes_from_fused_scale(dev):
+    """fc2's backward -> fc1's dY as the reference block chains them: fc1's
+    dY codes at the fused scale, with the bias gradient's column sums, equal
+    the oracle's of fc2's dX."""
+    M, K, N = 2048, 6400, 1600
+    dyq, wt, dyt, xt, sdy, sw, sx = _bwd_operands(dev, M, K, N, seed=93)
+    dX, _, am, sc = df.gemm_bwd_absmax(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, dx_dtype=torch.bfloat16,
+                                       next_fmt=Fmt.E5M2)
+    q, qt = df.quantize_2d(dX, sc, Fmt.E5M2, want_q=True, want_qt=True)
+    vals = orc.bf16_to_f32(dX.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(M, K)
+    s = orc.scale(orc.absmax(vals), int(Fmt.E5M2))
+    assert sc.item() == np.float32(s)
+    flat = orc.quantize(vals, s, int(Fmt.E5M2))
+    assert np.array_equal(q.cpu().numpy()[:, :K], flat)
+    assert np.array_equal(qt.cpu().numpy()[:, :M], np.ascontiguousarray(flat.T))
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_bwd_fold_skips_inf_and_nan(dev, out):
+    """On a grouped plan: dX with NaN rows (a NaN code in dY) and overflowed
+    values gives the absmax of its finite values only."""
+    M, K, N = 16384, 1600, 6400
+    assert df.gemm_bwd_plan(M, N, K)[0]
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    bits = torch.int16 if out == "bf16" else torch.int32
+    dyq, wt, dyt, xt, sdy, sw, sx = _bwd_operands(dev, M, K, N, seed=95)
+    top = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx)[0].abs().max().item()
+    f = 2.0 * 3.4e38 / top
+    f1 = 2.0 ** int(np.log2(f) / 2)
+    sdy2, sw2 = sdy * f1, sw * (f / f1)
+    dyq[77, 3] = 0x7F  # e5m2 NaN
+    dX, dW, am, sc = df.gemm_bwd_absmax(dyq, wt, dyt, xt, M, N, K, sdy2, sw2, sx, dx_dtype=dt, next_fmt=Fmt.E5M2)
+    dX1, _ = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy2, sw2, sx, dx_dtype=dt)
+    assert torch.equal(dX.view(bits), dX1.view(bits))
+    assert torch.isnan(dX1).any() and torch.isinf(dX1).any() and torch.isfinite(dX1).any()
+    am1, sc1 = df.absmax_scale(dX1, Fmt.E5M2)
+    assert am.view(torch.int32).item() == am1.view(torch.int32).item()
+    assert sc.view(torch.int32).item() == sc1.view(torch.int32).item()
