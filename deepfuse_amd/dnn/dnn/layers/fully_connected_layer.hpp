@@ -23,6 +23,7 @@
 #include <iostream>
 #include <optional>
 #include <string>
+#include <type_traits>
 
 #include "dnn/core/layer.hpp"
 #include "dnn/layers/layer_norm_layer.hpp"
@@ -44,7 +45,21 @@ public:
     // unfused pair.  norm records its input for its own backward as
     // norm.forward would.
     tensor<TT> forward(const tensor<TT>& input, LayerNormLayer<TT>& norm);
+    // forward(prev.forward(input)) where prev's output feeds this layer with
+    // nothing in between (the reference block's fc1 -> fc2,
+    // transformer_block.cu:79-81): prev's GEMM also gives the absmax of its
+    // output (df_fp8_gemm_fwd_absmax), which sets this layer's input scale,
+    // so the output is not read again for it.  Same values as the unfused
+    // pair; prev caches for its backward as prev.forward would.  With
+    // delayed scaling on this layer, or TT = __half, it is the unfused pair.
+    tensor<TT> forward(FullyConnectedLayer<TT>& prev, const tensor<TT>& input);
     tensor<TT> backward(const tensor<TT>& grad_output) override;
+    // backward(next.backward(grad_output)) where next is the layer this one
+    // feeds (transformer_block.cu:127-134): next's backward GEMM also gives
+    // the absmax of its input gradient (df_fp8_gemm_bwd_absmax), this
+    // layer's output gradient, which sets its dY scale.  Same values as the
+    // unfused pair, and the same fallback.
+    tensor<TT> backward(FullyConnectedLayer<TT>& next, const tensor<TT>& grad_output);
 
     std::string name() const override { return "FullyConnected"; }
     void initialize_weights() override;
@@ -94,7 +109,21 @@ private:
     // when norm is given; returns the device pointer of their scale
     const float* quantize_input(const tensor<TT>& input, int N, const LayerNormLayer<TT>* norm, uint8_t* xq, int Kp,
                                 uint8_t* xt, int Np, float* jit_scale);
-    tensor<TT> forward_impl(const tensor<TT>& input, LayerNormLayer<TT>* norm);
+    // in_scale: the input's scale is already in input_scale_slot(N) (written
+    // by the layer that produced the input); out_scale: the GEMM also writes
+    // the e4m3 scale of the output there, for the layer it feeds
+    tensor<TT> forward_impl(const tensor<TT>& input, LayerNormLayer<TT>* norm, const float* in_scale = nullptr,
+                            float* out_scale = nullptr);
+    // dy_scale: grad_output's e5m2 scale is already there; dx_scale: the
+    // backward GEMM also writes the e5m2 scale of the input gradient there
+    tensor<TT> backward_impl(const tensor<TT>& grad_output, const float* dy_scale = nullptr,
+                             float* dx_scale = nullptr);
+    // where the scale of an N-row input's codes lives (beside the cached X^T
+    // codes when training)
+    float* input_scale_slot(int N);
+    // where grad_output's scale lives
+    float* grad_scale_slot();
+    static constexpr bool kChains = !std::is_same_v<TT, __half>;  // the fused chain takes bf16 / fp32
 
     int in_features_;
     int out_features_;

@@ -199,7 +199,34 @@ tensor<TT> FullyConnectedLayer<TT>::forward(const tensor<TT>& input, LayerNormLa
 }
 
 template <typename TT>
-tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerNormLayer<TT>* norm) {
+float* FullyConnectedLayer<TT>::input_scale_slot(int N) {
+    if (!this->training_enabled_) return reinterpret_cast<float*>(scales_.get(4 * sizeof(float)));
+    const std::vector<int> xt_shape{in_features_, round16(N)};
+    if (!xt_cache_ || xt_cache_->shape() != xt_shape) xt_cache_.emplace(xt_shape);
+    return xt_cache_->scale_data();
+}
+
+template <typename TT>
+float* FullyConnectedLayer<TT>::grad_scale_slot() {
+    return reinterpret_cast<float*>(scales_.get(4 * sizeof(float))) + 2;
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::forward(FullyConnectedLayer<TT>& prev, const tensor<TT>& input) {
+    if (prev.out_features_ != in_features_)
+        throw std::invalid_argument("FullyConnectedLayer::forward: a layer of " + std::to_string(prev.out_features_) +
+                                    " outputs feeds a layer of " + std::to_string(in_features_) + " inputs");
+    if (!kChains || history_len_ > 0 || &prev == this) return forward(prev.forward(input));
+    const auto& sh = input.shape();
+    const int N = sh.size() == 2 ? sh[0] : 0;  // prev checks the shape
+    float* slot = input_scale_slot(N);
+    const tensor<TT> hidden = prev.forward_impl(input, nullptr, nullptr, slot);
+    return forward_impl(hidden, nullptr, slot);
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerNormLayer<TT>* norm,
+                                                 const float* in_scale, float* out_scale) {
     const auto& sh = input.shape();
     int N;
     if (norm) {
@@ -224,7 +251,14 @@ tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerN
         xt = reinterpret_cast<uint8_t*>(xt_cache_->data());
         sx_jit = xt_cache_->scale_data();
     }
-    const float* sx = quantize_input(input, N, norm, xq, Kp, xt, Np, sx_jit);
+    const float* sx = sx_jit;
+    if (in_scale) {  // the producer of `input` wrote its scale into sx_jit
+        if (in_scale != sx_jit) throw std::logic_error("FullyConnectedLayer: input scale outside its slot");
+        CHECK_DF_EX(df_quantize_2d(dt, input.data(), N, in_features_, in_features_, DF_FMT_E4M3, in_scale, xq, Kp, xt,
+                                   xt ? Np : 0, st()));
+    } else {
+        sx = quantize_input(input, N, norm, xq, Kp, xt, Np, sx_jit);
+    }
     uint8_t* wq = codes_b_.get((size_t)out_features_ * Kp);
     // in training, the same pass also writes W's transposed codes for the
     // backward's dX GEMM (the weights cannot change before the backward that
@@ -245,15 +279,39 @@ tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerN
     // a training forward has just written W^T codes of the current weights
     // (at the scale sw), so a load() before it no longer leaves them stale
     if (wt) wt_stale_ = false;
-    const size_t gb = df_fp8_gemm_workspace_bytes(N, out_features_, in_features_);
-    CHECK_DF_EX(df_fp8_gemm_fwd(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sw, dt, this->bias_.data(), dt,
-                                output.data(), out_features_, gemm_ws_.get(gb), gb, st()));
+    if (out_scale) {
+        const size_t gb = df_fp8_gemm_fwd_absmax_workspace_bytes(N, out_features_, in_features_);
+        CHECK_DF_EX(df_fp8_gemm_fwd_absmax(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sw, dt,
+                                           this->bias_.data(), dt, output.data(), out_features_, DF_FMT_E4M3, nullptr,
+                                           out_scale, gemm_ws_.get(gb), gb, st()));
+    } else {
+        const size_t gb = df_fp8_gemm_workspace_bytes(N, out_features_, in_features_);
+        CHECK_DF_EX(df_fp8_gemm_fwd(xq, Kp, wq, Kp, N, out_features_, in_features_, sx, sw, dt, this->bias_.data(),
+                                    dt, output.data(), out_features_, gemm_ws_.get(gb), gb, st()));
+    }
     cached_n_ = this->training_enabled_ ? N : -1;
     return output;
 }
 
 template <typename TT>
 tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
+    return backward_impl(grad_output);
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::backward(FullyConnectedLayer<TT>& next, const tensor<TT>& grad_output) {
+    if (next.in_features_ != out_features_)
+        throw std::invalid_argument("FullyConnectedLayer::backward: a layer of " + std::to_string(out_features_) +
+                                    " outputs feeds a layer of " + std::to_string(next.in_features_) + " inputs");
+    if (!kChains || history_len_ > 0 || &next == this) return backward(next.backward(grad_output));
+    float* slot = grad_scale_slot();
+    const tensor<TT> grad_hidden = next.backward_impl(grad_output, nullptr, slot);
+    return backward_impl(grad_hidden, slot);
+}
+
+template <typename TT>
+tensor<TT> FullyConnectedLayer<TT>::backward_impl(const tensor<TT>& grad_output, const float* dy_scale,
+                                                  float* dx_scale) {
     if (!this->training_enabled_)
         throw std::runtime_error("FullyConnectedLayer: backward called without input argument in stateless mode");
     if (!xt_cache_ || cached_n_ < 0)
@@ -285,7 +343,12 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
         wt_stale_ = false;
         sw_used_ = nullptr;  // these codes are at the just-in-time scale sc + 1
     }
-    if (history_len_ > 0 && sx_used_) {
+    if (dy_scale) {  // the layer this one feeds wrote grad_output's scale into sc + 2
+        if (dy_scale != sc + 2) throw std::logic_error("FullyConnectedLayer: gradient scale outside its slot");
+        const size_t cb = df_quantize_2d_workspace_bytes(N, out_features_);
+        CHECK_DF_EX(df_quantize_2d_colsum(dt, grad_output.data(), N, out_features_, out_features_, DF_FMT_E5M2,
+                                          dy_scale, dyq, Op, dyt, Np, db, colsum_ws_.get(cb), cb, st()));
+    } else if (history_len_ > 0 && sx_used_) {
         sdy = quantize_delayed(ddy_, grad_output.data(), N, out_features_, DF_FMT_E5M2, dyq, Op, dyt, Np, db);
         if (sw_used_) sw = sw_used_;
         sx = sx_used_;
@@ -294,11 +357,19 @@ tensor<TT> FullyConnectedLayer<TT>::backward(const tensor<TT>& grad_output) {
     }
     tensor<TT> grad_input({N, in_features_});
     // dX (fc_backward_input) and dW (fc_backward_weights) in one launch
-    const size_t gb = df_fp8_gemm_bwd_workspace_bytes(N, out_features_, in_features_);
-    uint8_t* gws = gemm_ws_.get(gb);
-    CHECK_DF_EX(df_fp8_gemm_bwd(dyq, Op, wt, Op, dyt, Np, reinterpret_cast<const uint8_t*>(xt_cache_->data()), Np, N,
-                                out_features_, in_features_, sdy, sw, sx, dt, grad_input.data(), in_features_, dt,
-                                this->grad_weights_.data(), in_features_, gws, gb, st()));
+    const uint8_t* xtc = reinterpret_cast<const uint8_t*>(xt_cache_->data());
+    if (dx_scale) {
+        const size_t gb = df_fp8_gemm_bwd_absmax_workspace_bytes(N, out_features_, in_features_);
+        CHECK_DF_EX(df_fp8_gemm_bwd_absmax(dyq, Op, wt, Op, dyt, Np, xtc, Np, N, out_features_, in_features_, sdy, sw,
+                                           sx, dt, grad_input.data(), in_features_, dt, this->grad_weights_.data(),
+                                           in_features_, DF_FMT_E5M2, nullptr, dx_scale, gemm_ws_.get(gb), gb,
+                                           st()));
+    } else {
+        const size_t gb = df_fp8_gemm_bwd_workspace_bytes(N, out_features_, in_features_);
+        CHECK_DF_EX(df_fp8_gemm_bwd(dyq, Op, wt, Op, dyt, Np, xtc, Np, N, out_features_, in_features_, sdy, sw, sx, dt,
+                                    grad_input.data(), in_features_, dt, this->grad_weights_.data(), in_features_,
+                                    gemm_ws_.get(gb), gb, st()));
+    }
     CHECK_DF_EX(df_convert(DF_DTYPE_FLOAT32, db, dt, this->grad_bias_.data(), out_features_, st()));
     return grad_input;
 }

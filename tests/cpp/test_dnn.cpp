@@ -1139,6 +1139,72 @@ TEST_F(FullyConnectedLayerTest, LayerNormFusedEqualsUnfused) {
     }
 }
 
+// fc1 -> fc2 chained as the reference block's MLP runs them
+// (transformer_block.cu:79-81, :127-134): fc2.forward(fc1, x) and
+// fc1.backward(fc2, gy) equal the unfused pairs bit for bit -- output, input
+// gradient, both layers' weight and bias gradients -- over two training
+// steps, on a small shape (the fused GEMMs' two-pass form) and on one whose
+// fc1 output takes the persistent kernel that folds the absmax; with delayed
+// scaling on the layers they are the unfused pairs.
+template <typename TT>
+std::vector<float> chain_dl(const tensor<TT>& t) {
+    if constexpr (std::is_same_v<TT, float>) return download(t);
+    else return download_f(t);
+}
+
+template <typename TT>
+void chain_up(tensor<TT>& t, const std::vector<float>& v) {
+    if constexpr (std::is_same_v<TT, float>) t.upload(v.data());
+    else upload_bf16(t, v);
+}
+
+template <typename TT>
+void chain_case(int N, int in_f, int hid, int out_f, int hist, uint64_t seed) {
+    SCOPED_TRACE("N=" + std::to_string(N) + " " + std::to_string(in_f) + "->" + std::to_string(hid) + "->" +
+                 std::to_string(out_f) + " hist=" + std::to_string(hist));
+    FullyConnectedLayer<TT> a1(in_f, hid, true), a2(hid, out_f, true), b1(in_f, hid, true), b2(hid, out_f, true);
+    const auto w1 = uniform((size_t)hid * in_f, -0.1f, 0.1f, seed), w2 = uniform((size_t)out_f * hid, -0.05f, 0.05f,
+                                                                                  seed + 1);
+    const auto c1 = uniform(hid, -0.5f, 0.5f, seed + 2), c2 = uniform(out_f, -0.5f, 0.5f, seed + 3);
+    for (auto* l : {&a1, &b1}) {
+        chain_up(*l->weights(), w1);
+        chain_up(*l->bias(), c1);
+        l->set_delayed_scaling(hist);
+    }
+    for (auto* l : {&a2, &b2}) {
+        chain_up(*l->weights(), w2);
+        chain_up(*l->bias(), c2);
+        l->set_delayed_scaling(hist);
+    }
+    for (int step = 0; step < 2; ++step) {
+        tensor<TT> x({N, in_f}), gy({N, out_f});
+        chain_up(x, uniform((size_t)N * in_f, -2.0f, 2.0f, seed + 10 + step));
+        chain_up(gy, uniform((size_t)N * out_f, -0.1f, 0.1f, seed + 20 + step));
+        EXPECT_TRUE(chain_dl(a2.forward(a1.forward(x))) == chain_dl(b2.forward(b1, x)));
+        EXPECT_TRUE(chain_dl(a1.backward(a2.backward(gy))) == chain_dl(b1.backward(b2, gy)));
+        EXPECT_TRUE(chain_dl(*a1.grad_weights()) == chain_dl(*b1.grad_weights()));
+        EXPECT_TRUE(chain_dl(*a2.grad_weights()) == chain_dl(*b2.grad_weights()));
+        EXPECT_TRUE(chain_dl(*a1.grad_bias()) == chain_dl(*b1.grad_bias()));
+        EXPECT_TRUE(chain_dl(*a2.grad_bias()) == chain_dl(*b2.grad_bias()));
+    }
+}
+
+TEST_F(FullyConnectedLayerTest, ChainedPairEqualsUnfused) {
+    chain_case<float>(48, 160, 96, 72, 0, 300);
+    chain_case<bfloat16>(48, 160, 96, 72, 0, 310);
+    chain_case<float>(48, 160, 96, 72, 4, 320);
+    chain_case<float>(4096, 512, 4096, 512, 0, 330);
+    chain_case<bfloat16>(4096, 512, 4096, 512, 0, 340);
+}
+
+TEST_F(FullyConnectedLayerTest, ChainedPairChecksSizes) {
+    FullyConnectedLayer<float> a(16, 32, true), b(48, 8, true);
+    tensor<float> x({4, 16});
+    EXPECT_THROW(b.forward(a, x), std::invalid_argument);
+    tensor<float> g({4, 8});
+    EXPECT_THROW(a.backward(b, g), std::invalid_argument);
+}
+
 // ---- AdamOptimizer: the reference's cases (adam_optimizer_test.cu:21-214),
 // plus exact agreement with the oracle's step ----
 TEST_F(AdamOptimizerTest, BasicUpdate) {
