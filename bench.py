@@ -543,6 +543,10 @@ EXTRA_STATS = (
     ("stats_producer", "prof_producer", "layernorm_quantize_kernel_stats.md",
      "LayerNorm + e4m3 codes, 16384 x 1600 bf16 (unfused chain, fused, fused delayed)",
      ("ln_stats_kernel", "true>(unsigned short const*", "amax_history_kernel")),
+    ("stats_producer", "prof_producer", "gemm_producer_kernel_stats.md",
+     "GEMMs that also fold their output's absmax: fc1's forward and fc2's grouped backward at the config-4 fc "
+     "shapes (the producer leg's gemm_producer variants)",
+     ("persistent_amax_kernel", "grouped_amax_kernel")),
 )
 # GEMM families whose C-ABI call is exactly one kernel, by the persistent
 # kernel's template arguments: <A format, B format, output, bias type, bias,
@@ -1009,8 +1013,8 @@ def timeline_summary(out_dir, prof):
 LIMITER_KERNELS = (
     ("gemm_fwd", "void dfk::gemm_nt_persistent_kernel<0, 0, unsigned short, unsigned short, true, false, void>"),
     ("gemm_bwd (dW unsplit)", "void dfk::gemm_nt_persistent_kernel<1, 0, float, float, false, false, unsigned short>"),
-    ("quantize X", "void dfk::quantize_2d_kernel<unsigned short, 0, false, true, false, false>"),
-    ("quantize dY + db", "void dfk::quantize_2d_kernel<unsigned short, 1, true, true, false, false>"),
+    ("quantize X", "void dfk::quantize_2d_jit_w5_kernel<unsigned short, 0, false>"),
+    ("quantize dY + db", "void dfk::quantize_2d_jit_w5_kernel<unsigned short, 1, true>"),
 )
 
 
