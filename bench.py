@@ -2130,7 +2130,7 @@ def streaming_bench(torch, df, synth, dev, layers=48, tokens=8192, slots=6, step
 
 
 def cpu_baseline(tokens):
-    """The reference's host path timed on this host (BASELINE.md's plan):
+    """The reference's host path timed on this host, as the CPU baseline:
     plain C restatements of the reference's FC loops -- (i) the GTest helper's
     bias-first forward (tests/layers/fully_connected_layer_test.cu:29-46;
     its backward helpers are the kernel's loop order for dX and a one-sample
