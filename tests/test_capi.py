@@ -198,3 +198,26 @@ def test_flat_wrappers_refuse_binary16():
         df.quantize(torch.zeros(8, dtype=torch.float16), None, Fmt.E4M3)
     with pytest.raises(TypeError):
         df.dequantize(torch.zeros(8, dtype=torch.uint8), None, Fmt.E4M3, torch.float16)
+
+
+def test_error_message_is_per_thread():
+    """df_last_error_string is thread-local: two threads that fail different
+    checks at the same time each read their own message (no GPU work: each
+    call fails its argument checks first)."""
+    import threading
+    L = df.lib()
+    go = threading.Barrier(2)
+    seen = {}
+
+    def worker(tag, fn):
+        go.wait()
+        rc = fn()
+        go.wait()  # both calls have returned before either reads its message
+        seen[tag] = (rc, L.df_last_error_string().decode())
+
+    t1 = threading.Thread(target=worker, args=("fmt", lambda: L.df_quantize_2d(
+        int(DType.BFLOAT16), FAKE, 4, 4, 4, 9, FAKE, FAKE, 16, None, 0, None)))
+    t2 = threading.Thread(target=worker, args=("n", lambda: L.df_quantize_bf16_e5m2(None, -3, None, None, None)))
+    t1.start(); t2.start(); t1.join(); t2.join()
+    assert seen["fmt"][0] == -2 and "format" in seen["fmt"][1]
+    assert seen["n"][0] == -1 and "n < 0" in seen["n"][1]
