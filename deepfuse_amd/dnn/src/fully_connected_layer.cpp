@@ -218,7 +218,12 @@ tensor<TT> FullyConnectedLayer<TT>::forward(FullyConnectedLayer<TT>& prev, const
                                     " outputs feeds a layer of " + std::to_string(in_features_) + " inputs");
     if (!kChains || history_len_ > 0 || &prev == this) return forward(prev.forward(input));
     const auto& sh = input.shape();
-    const int N = sh.size() == 2 ? sh[0] : 0;  // prev checks the shape
+    // checked before input_scale_slot may replace this layer's cached X^T
+    if (sh.size() != 2 || sh[1] != prev.in_features_)
+        throw std::invalid_argument("FullyConnectedLayer::forward: input must be [N, " +
+                                    std::to_string(prev.in_features_) + "], got " + input.to_string());
+    const int N = sh[0];
+    cached_n_ = -1;  // until this forward completes, backward has no input to use
     float* slot = input_scale_slot(N);
     const tensor<TT> hidden = prev.forward_impl(input, nullptr, nullptr, slot);
     return forward_impl(hidden, nullptr, slot);
@@ -237,8 +242,15 @@ tensor<TT> FullyConnectedLayer<TT>::forward_impl(const tensor<TT>& input, LayerN
                                         std::to_string(in_features_) + "], got " + input.to_string());
         N = sh[0];
     }
+    // A forward that throws past this point may have replaced the cached X^T
+    // (another N) or overwritten its codes: backward then refuses rather than
+    // reading it at the old N.
+    cached_n_ = -1;
     tensor<TT> output({N, out_features_});
-    if (N == 0) return output;
+    if (N == 0) {  // an empty batch: its backward has zero weight and bias gradients
+        cached_n_ = this->training_enabled_ ? 0 : -1;
+        return output;
+    }
     constexpr int dt = dtype_traits<TT>::value;
     const int Kp = round16(in_features_), Np = round16(N);
     float* sc = reinterpret_cast<float*>(scales_.get(4 * sizeof(float)));
@@ -314,13 +326,18 @@ tensor<TT> FullyConnectedLayer<TT>::backward_impl(const tensor<TT>& grad_output,
                                                   float* dx_scale) {
     if (!this->training_enabled_)
         throw std::runtime_error("FullyConnectedLayer: backward called without input argument in stateless mode");
-    if (!xt_cache_ || cached_n_ < 0)
+    if (cached_n_ < 0 || (cached_n_ > 0 && !xt_cache_))
         throw std::runtime_error("FullyConnectedLayer: input_cache_ not set for backward");
     const int N = cached_n_;
     const auto& sh = grad_output.shape();
     if (sh.size() != 2 || sh[0] != N || sh[1] != out_features_)
         throw std::invalid_argument("FullyConnectedLayer::backward: grad_output must be [" + std::to_string(N) + ", " +
                                     std::to_string(out_features_) + "], got " + grad_output.to_string());
+    if (N == 0) {  // sums over no rows; dx_scale stays unwritten, as no empty dX is quantized
+        this->grad_weights_.zero();
+        this->grad_bias_.zero();
+        return tensor<TT>({0, in_features_});
+    }
     constexpr int dt = dtype_traits<TT>::value;
     const int Np = round16(N), Op = round16(out_features_);
     float* sc = reinterpret_cast<float*>(scales_.get(4 * sizeof(float)));

@@ -1205,6 +1205,47 @@ TEST_F(FullyConnectedLayerTest, ChainedPairChecksSizes) {
     EXPECT_THROW(a.backward(b, g), std::invalid_argument);
 }
 
+// A chained forward refused for its input's shape leaves the layer as it
+// was: the backward that follows uses the last completed forward (its cached
+// X^T codes were neither replaced nor resized).
+TEST_F(FullyConnectedLayerTest, RefusedChainedForwardKeepsTheLayer) {
+    FullyConnectedLayer<float> a(16, 32, true), b(32, 8, true);
+    tensor<float> x({4, 16}), g({4, 8});
+    x.upload(uniform(64, -1.0f, 1.0f, 950).data());
+    g.upload(uniform(32, -1.0f, 1.0f, 951).data());
+    (void)b.forward(a, x);
+    const auto dx = download(b.backward(g));
+    const auto dw = download(*b.grad_weights());
+    tensor<float> x3({4, 4, 16}), wide({4, 17});
+    EXPECT_THROW(b.forward(a, x3), std::invalid_argument);
+    EXPECT_THROW(b.forward(a, wide), std::invalid_argument);
+    EXPECT_TRUE(download(b.backward(g)) == dx);
+    EXPECT_TRUE(download(*b.grad_weights()) == dw);
+}
+
+// An empty batch: forward gives [0, out], backward gives [0, in] and zero
+// weight and bias gradients (sums over no rows), alone and chained.
+TEST_F(FullyConnectedLayerTest, EmptyBatchForwardBackward) {
+    FullyConnectedLayer<float> a(16, 32, true), b(32, 8, true);
+    tensor<float> x({4, 16}), g({4, 8});
+    x.upload(uniform(64, -1.0f, 1.0f, 960).data());
+    g.upload(uniform(32, -1.0f, 1.0f, 961).data());
+    (void)b.forward(a, x);  // non-zero gradients first
+    (void)a.backward(b, g);
+    tensor<float> x0({0, 16}), g0({0, 8});
+    EXPECT_TRUE(b.forward(a, x0).shape() == std::vector<int>({0, 8}));
+    EXPECT_TRUE(a.backward(b, g0).shape() == std::vector<int>({0, 16}));
+    for (auto* l : {&a, &b}) {
+        for (float v : download(*l->grad_weights())) EXPECT_EQ(v, 0.0f);
+        for (float v : download(*l->grad_bias())) EXPECT_EQ(v, 0.0f);
+    }
+    EXPECT_TRUE(a.forward(x0).shape() == std::vector<int>({0, 32}));
+    tensor<float> gh0({0, 32});
+    EXPECT_TRUE(a.backward(gh0).shape() == std::vector<int>({0, 16}));
+    tensor<float> gbad({1, 32});
+    EXPECT_THROW(a.backward(gbad), std::invalid_argument);
+}
+
 // ---- AdamOptimizer: the reference's cases (adam_optimizer_test.cu:21-214),
 // plus exact agreement with the oracle's step ----
 TEST_F(AdamOptimizerTest, BasicUpdate) {
@@ -1403,4 +1444,15 @@ TEST_F(ClipGradNormTest, MatchesOracleOnLayerGradients) {
     }
 }
 
-int main(int argc, char** argv) { return mini_test::run_all(argc, argv); }
+int main(int argc, char** argv) {
+    const int rc = mini_test::run_all(argc, argv);
+#ifdef DNN_TESTS_SKIP_TEARDOWN
+    // The sanitized build (make asan) ends here, once every result is
+    // printed: at static teardown the ROCm runtime's own finalizers free
+    // memory after the runtime has unloaded, which the sanitizer's device
+    // allocator aborts on.
+    std::cout.flush();
+    std::_Exit(rc);
+#endif
+    return rc;
+}
