@@ -224,9 +224,18 @@ _ABSMAX_SCALE = {DType.FLOAT32: "df_absmax_scale_f32", DType.BFLOAT16: "df_absma
 _WS = {}
 
 
+def _ws_key(device, tag: str):
+    """Cached workspaces are kept per device and per stream (the current
+    torch stream, the one the calls go to).  Calls on different streams
+    never share one.  A workspace replaced by a larger one was allocated
+    while its stream was current, and only that stream used it, so torch's
+    allocator reuses its memory in that stream's order."""
+    return (str(device), tag, _stream())
+
+
 def _workspace(device):
     torch = _torch()
-    key = str(device)
+    key = _ws_key(device, "absmax")
     if key not in _WS:
         _WS[key] = torch.empty(lib().df_absmax_workspace_bytes(), dtype=torch.uint8, device=device)
     return _WS[key]
@@ -272,7 +281,7 @@ def round16(v: int) -> int:
 
 def _scratch(device, nbytes: int, tag: str):
     torch = _torch()
-    key = (str(device), tag)
+    key = _ws_key(device, tag)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
@@ -322,10 +331,11 @@ def quantize_2d_jit(x, fmt: Fmt, want_q=True, want_qt=False, colsum=False):
 
 
 def gemm_workspace(M: int, N: int, K: int, device):
-    """Device workspace sized so split-K is never limited (cached per size)."""
+    """Device workspace sized so split-K is never limited (cached per device
+    and current stream, grown as needed)."""
     torch = _torch()
     nbytes = int(lib().df_fp8_gemm_workspace_bytes(M, N, K))
-    key = (str(device), "gemm")
+    key = _ws_key(device, "gemm")
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)

@@ -101,3 +101,40 @@ def test_two_streams_match_sequential(dev):
     for i, j in enumerate(jobs):
         for name, got, exp in zip(names, j.outputs(), expect[i]):
             assert torch.equal(got.view(torch.uint8), exp.view(torch.uint8)), f"job {i}: {name}"
+
+
+def test_python_wrappers_keep_a_workspace_per_stream(dev):
+    """The package's wrappers cache their workspaces per device and stream:
+    two streams get different ones, and wrapper calls queued on two streams
+    without synchronisation (their kernels free to overlap) give the results
+    of the same calls made one after another, bit for bit."""
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        w1 = df._scratch(dev, 1 << 20, "jit")
+    with torch.cuda.stream(s2):
+        w2 = df._scratch(dev, 1 << 20, "jit")
+    assert w1.data_ptr() != w2.data_ptr()
+    bf = lambda shape, std, s: torch.from_numpy(synth.normal(shape, std, seed=s)).to(dev).to(torch.bfloat16)
+    xs = [bf((4096, 1600), 1.0, 8300), bf((2048, 6400), 1.0, 8301)]
+    ws_ = [bf((1600, 1600), 0.02, 8302), bf((768, 6400), 0.02, 8303)]
+
+    def job(i):
+        am, sc, q, qt, cs = df.quantize_2d_jit(xs[i], Fmt.E5M2, want_q=True, want_qt=True, colsum=True)
+        _, sw, wq, _ = df.quantize_2d_jit(ws_[i], Fmt.E4M3)
+        y = df.gemm_nt(q, Fmt.E5M2, wq, Fmt.E4M3, xs[i].shape[1], sc, sw, out_dtype=torch.float32)
+        return [am, sc, q, qt, cs, y]
+
+    expect = [job(0), job(1)]
+    torch.cuda.synchronize()
+    got = [[], []]
+    for s in (s1, s2):
+        s.wait_stream(torch.cuda.current_stream())
+    for _ in range(3):  # queued back to back on both streams, no synchronisation between
+        for i, s in enumerate((s1, s2)):
+            with torch.cuda.stream(s):
+                got[i] = job(i)
+    torch.cuda.synchronize()
+    names = ("absmax", "scale", "q", "qt", "colsum", "y")
+    for i in range(2):
+        for name, g, e in zip(names, got[i], expect[i]):
+            assert torch.equal(g.view(torch.uint8), e.view(torch.uint8)), f"stream {i}: {name}"
