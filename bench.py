@@ -487,7 +487,7 @@ def measured_traffic(kernel_family):
 PROFILE_COMMANDS = {
     "stats": ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_bench -o bench -- "
               "python3 bench.py --steps 20 --warmup 3 --no-cpu-baseline --no-conversion --no-streaming "
-              "--no-optimizer --no-producer --no-delayed --no-config3"),
+              "--no-optimizer --no-producer --no-delayed --no-config3 > gpurun_out/prof_bench_line.json"),
     "fetch": ("timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv "
               "-d gpurun_out/pmc_fetch -o bench -- python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline "
               "--no-conversion --no-streaming --no-optimizer --no-producer --no-delayed --no-config3 --no-graph "
@@ -590,9 +590,59 @@ def _short_kernel(name):
     return name
 
 
-def config4_summaries(out_dir, prof):
-    """profiles/bench_config4_kernel_stats.md, hbm_traffic_config4.md and
-    hbm_traffic.json from the stats / fetch / write runs."""
+def line_kernel_check(out_dir):
+    """Lines comparing, within the stats run, the bench line's per-launch
+    time of its dominant kernel (HIP events in the eager per-kernel pass)
+    with rocprof's durations of the same dispatches: that pass is the last
+    use of the kernel in the run, so they are the kernel's last
+    steps x launches_per_step dispatches in the trace.  [] when the run's
+    line or trace is missing."""
+    import csv
+
+    line_path = os.path.join(out_dir, "prof_bench_line.json")
+    trace = os.path.join(out_dir, "prof_bench", "bench_kernel_trace.csv")
+    if not (os.path.exists(line_path) and os.path.exists(trace)):
+        return []
+    with open(line_path) as fh:
+        lines = [ln for ln in fh.read().splitlines() if ln.strip().startswith("{")]
+    if not lines:
+        return []
+    d = json.loads(lines[-1])
+    roof = d["roofline"]
+    dom = roof["kernel"]
+    pats = TRAFFIC_FAMILIES.get(dom)
+    if not pats:
+        return []
+    n = d["steps"] * d["kernels"][dom]["launches_per_step"]
+    with open(trace) as fh:
+        disp = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(fh)
+                if any(_short_kernel(r["Kernel_Name"]).endswith(p) for p in pats)]
+    disp.sort()
+    last = disp[-n:]
+    if len(last) < n or n == 0:
+        return []
+    prof_ms = sum(e - b for b, e in last) / n / 1e6
+    ev_ms = roof["avg_launch_ms"]
+    work = roof["work_per_launch"]
+    peak = roof["peak"]
+    f_ev, f_pr = work / (ev_ms * 1e-3) / 1e12 / peak, work / (prof_ms * 1e-3) / 1e12 / peak
+    return ["", "## The bench line's dominant kernel, within this run", "",
+            f"The run's own JSON line (stdout, kept as `gpurun_out/prof_bench_line.json`) names `{dom}` "
+            f"(`{pats[0]}`) with `roofline.avg_launch_ms` = {ev_ms:.4f}: HIP events around each of its {n} "
+            "launches in the eager per-kernel pass.  Those launches are the kernel's last "
+            f"{n} dispatches in this run's kernel trace.", "",
+            "| source | ms per launch | TFLOP/s | fraction of 5.0 PF |", "|---|---|---|---|",
+            f"| HIP events (the line) | {ev_ms:.4f} | {work / (ev_ms * 1e-3) / 1e12:.1f} | {f_ev:.4f} |",
+            f"| rocprof, same {n} dispatches | {prof_ms:.4f} | {work / (prof_ms * 1e-3) / 1e12:.1f} | "
+            f"{f_pr:.4f} |", "",
+            f"They differ by {abs(prof_ms / ev_ms - 1) * 100:.1f}%.  The table above averages every dispatch of the "
+            "run (graph replays, the separate-launch comparison and the per-kernel pass); between boxes the "
+            "same kernels vary by about 4%, with the shader clock they hold."]
+
+
+def config4_stats_summary(out_dir, prof):
+    """profiles/bench_config4_kernel_stats.md from the stats run (and the
+    bench line it printed)."""
     import csv
 
     stats_csv = os.path.join(out_dir, "prof_bench", "bench_kernel_stats.csv")
@@ -610,8 +660,16 @@ def config4_summaries(out_dir, prof):
     for r in rows:
         lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                      f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    lines += line_kernel_check(out_dir)
     with open(os.path.join(prof, "bench_config4_kernel_stats.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
+    return rows
+
+
+def config4_traffic_summary(out_dir, prof):
+    """profiles/hbm_traffic_config4.md and hbm_traffic.json from the fetch
+    and write runs."""
+    import csv
 
     def counters(which, counter):
         path = os.path.join(out_dir, "pmc_" + which, "bench_counter_collection.csv")
@@ -669,7 +727,7 @@ def config4_summaries(out_dir, prof):
         lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:.1f} | {write[k][0]:.1f} | {mb:.1f} |")
     with open(os.path.join(prof, "hbm_traffic_config4.md"), "w") as fh:
         fh.write("\n".join(lines) + "\n")
-    return rows, fams
+    return fams
 
 
 def summarize_profiles():
@@ -683,9 +741,11 @@ def summarize_profiles():
     os.makedirs(prof, exist_ok=True)
 
     rows, fams = [], {}
-    if os.path.exists(os.path.join(out_dir, "prof_bench", "bench_kernel_stats.csv")) and \
-            os.path.exists(os.path.join(out_dir, "pmc_fetch", "bench_counter_collection.csv")):
-        rows, fams = config4_summaries(out_dir, prof)
+    if os.path.exists(os.path.join(out_dir, "prof_bench", "bench_kernel_stats.csv")):
+        rows = config4_stats_summary(out_dir, prof)
+    if os.path.exists(os.path.join(out_dir, "pmc_fetch", "bench_counter_collection.csv")) and \
+            os.path.exists(os.path.join(out_dir, "pmc_write", "bench_counter_collection.csv")):
+        fams = config4_traffic_summary(out_dir, prof)
     extra = []
     if conversion_summary(out_dir, prof):
         extra.append("conversion_config2_kernels.md")

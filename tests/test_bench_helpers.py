@@ -10,6 +10,10 @@
   Both are checked on hand-made logs.
 - bench.py --gpus 2 exits with status 2 and says that this build runs on one
   GPU, before touching the GPU.
+- line_kernel_check (the stats summary's comparison of the line's event time
+  with rocprof's) takes the dominant kernel's last steps x launches_per_step
+  dispatches of the trace, and no other kernel's; checked on a hand-made
+  line and trace.
 """
 import os
 import subprocess
@@ -74,3 +78,25 @@ def test_more_than_one_gpu_exits():
                        text=True, timeout=120, cwd=ROOT)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_line_kernel_check_uses_the_last_dispatches(tmp_path):
+    import json
+    grouped = "void dfk::" + bench.TRAFFIC_FAMILIES["gemm_bwd"][0] + "(unsigned char const*, int)"
+    line = {"steps": 2, "kernels": {"gemm_bwd": {"launches_per_step": 3}},
+            "roofline": {"kernel": "gemm_bwd", "avg_launch_ms": 0.3, "work_per_launch": 6e11, "peak": 5000.0}}
+    (tmp_path / "prof_bench_line.json").write_text("rocprofv3 noise\n" + json.dumps(line) + "\n")
+    (tmp_path / "prof_bench").mkdir()
+    rows = ["Kernel_Name,Start_Timestamp,End_Timestamp"]
+    t = 1_000_000
+    for i in range(10):  # 4 early dispatches of 0.5 ms, then the pass's 6 of 0.303 ms
+        dur = 500_000 if i < 4 else 303_000
+        rows.append(f'"{grouped}",{t},{t + dur}')
+        rows.append(f'"void dfk::other_kernel<int>(int)",{t + dur},{t + dur + 900_000}')
+        t += 2_000_000
+    (tmp_path / "prof_bench" / "bench_kernel_trace.csv").write_text("\n".join(rows) + "\n")
+    out = "\n".join(bench.line_kernel_check(str(tmp_path)))
+    assert "| rocprof, same 6 dispatches | 0.3030 |" in out
+    assert "| HIP events (the line) | 0.3000 |" in out
+    assert "They differ by 1.0%." in out
+    assert bench.line_kernel_check(str(tmp_path / "missing")) == []
