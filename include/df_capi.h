@@ -501,7 +501,9 @@ int df_streamer_copy_log(df_streamer* s, float* start_ms, float* end_ms, int cap
  * clip_norm_dev non-NULL, grad is first multiplied by max_norm / norm when
  * norm = clip_norm_dev[0] > max_norm: the same values as
  * df_clip_grad_norm_f32 followed by this call, without rewriting the
- * gradients. */
+ * gradients.  Under HIP graph capture, lr and the two bias corrections
+ * (from `timestep`) are fixed when the call is captured (they are kernel
+ * arguments): every replay repeats that step's values. */
 size_t df_grad_norm_workspace_bytes(int count, const int64_t* sizes);
 int df_grad_norm_f32(const float* const* grads, const int64_t* sizes, int count,
                      float* norm_dev, void* ws, size_t ws_bytes, void* stream);
