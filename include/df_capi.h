@@ -449,7 +449,10 @@ int df_fp8_gemm_bwd_absmax(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int
  * Issue load(l + slots - 2) right after layer l's launches: the thread then
  * blocks only until layer l-2 has finished, with layers l-1 and l queued.
  * Loading into a slot that was loaded but not released is DF_ERR_INVALID.
- * One streamer is used by one host thread at a time. */
+ * One streamer is used by one host thread at a time.  The streamer is driven
+ * from the host (df_streamer_load waits on events there), so it is not for
+ * use inside HIP graph capture; the GEMM and quantize calls of each layer
+ * are. */
 typedef struct df_streamer_s df_streamer;
 int df_host_alloc(size_t bytes, void** host_ptr);  /* pinned host memory (hipHostMalloc) */
 int df_host_free(void* host_ptr);
