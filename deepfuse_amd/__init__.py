@@ -362,7 +362,7 @@ def gemm_nt(a_q, fmt_a: Fmt, b_q, fmt_b: Fmt, K: int, sa, sb, bias=None, out_dty
 def gemm_fwd_absmax(x_q, w_q, K: int, sx, sw, bias=None, out_dtype=None, next_fmt: Fmt = Fmt.E4M3):
     """Y = X . W^T * sx * sw + bias (df_fp8_gemm_fwd_absmax): returns (Y,
     absmax of Y as stored, the rule-D1/D2 scale of Y for next_fmt); Y is
-    bf16 (default) or fp32."""
+    bf16 (default), float16 or fp32."""
     torch = _torch()
     out_dtype = out_dtype or torch.bfloat16
     M, N = x_q.shape[0], w_q.shape[0]

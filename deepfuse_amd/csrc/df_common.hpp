@@ -295,6 +295,19 @@ struct f16_t {
 };
 static_assert(sizeof(f16_t) == 2, "f16_t is two bytes");
 
+// The biased fold above for two binary16 values: |x| + 0x0400 takes +inf
+// and every NaN (0x7C00 and up) to a negative int16, which the signed max
+// skips; finite values keep their order.  unbias_f16x2 gives the binary32
+// bits of the largest finite |x| folded (0 if none).
+__device__ __forceinline__ uint32_t fold_f16x2_biased(uint32_t m, uint32_t w) {
+    const df_short2 u = __builtin_bit_cast(df_short2, (w & 0x7FFF7FFFu) + 0x04000400u);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(df_short2, m), u));
+}
+__device__ __forceinline__ uint32_t unbias_f16x2(uint32_t m) {
+    const int hi = (int)(int16_t)(m >> 16), lo = (int)(int16_t)(m & 0xFFFFu);
+    return __float_as_uint(f16_to_f32((uint32_t)max(max(hi, lo) - 0x400, 0)));
+}
+
 // ------------------------------------------------------------- host side --
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();

@@ -548,9 +548,10 @@ __device__ __forceinline__ void persistent_body(
     static_assert(!NARROW || (!GROUPED && !SPLIT), "narrow tiles: one problem, unsplit");
     using FoldT = typename std::conditional<GROUPED, OutT1, OutT>::type;
     static_assert(!AMAX_OUT || (!NARROW && (GROUPED || !SPLIT) &&
-                                (std::is_same<FoldT, uint16_t>::value || std::is_same<FoldT, float>::value)),
+                                (std::is_same<FoldT, uint16_t>::value || std::is_same<FoldT, f16_t>::value ||
+                                 std::is_same<FoldT, float>::value)),
                   "output absmax: 256x256 tiles, the unsplit single problem or a grouped launch's second "
-                  "problem, bf16 or fp32 output");
+                  "problem, bf16, f16 or fp32 output");
     using Out1 = typename std::conditional<GROUPED, OutT1, OutT>::type;
     constexpr int FM = NARROW ? 2 : 4, FN = 2;    // 32x32 MFMA tiles per wave
     constexpr int BN = NARROW ? 128 : kPBN;       // tile columns
@@ -958,7 +959,12 @@ __device__ __forceinline__ void persistent_body(
                                 __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
                             else
                                 *reinterpret_cast<u32x4*>(dst) = val;
-                            if constexpr (FOLD && ES == 2) {
+                            if constexpr (FOLD && std::is_same<T, f16_t>::value) {
+                                am_acc = fold_f16x2_biased(am_acc, val.x);
+                                am_acc = fold_f16x2_biased(am_acc, val.y);
+                                am_acc = fold_f16x2_biased(am_acc, val.z);
+                                am_acc = fold_f16x2_biased(am_acc, val.w);
+                            } else if constexpr (FOLD && ES == 2) {
                                 am_acc = fold_bf16x2_biased(am_acc, val.x);
                                 am_acc = fold_bf16x2_biased(am_acc, val.y);
                                 am_acc = fold_bf16x2_biased(am_acc, val.z);
@@ -973,7 +979,10 @@ __device__ __forceinline__ void persistent_body(
                             for (int x = 0; x < 16 / ES; ++x)
                                 if (scol + x < No) {
                                     dst[x] = ev[x];
-                                    if constexpr (FOLD && ES == 2)  // the value in the low half
+                                    if constexpr (FOLD && std::is_same<T, f16_t>::value)  // low half
+                                        am_acc = fold_f16x2_biased(
+                                            am_acc, (uint32_t)reinterpret_cast<const uint16_t*>(ev)[x]);
+                                    else if constexpr (FOLD && ES == 2)  // the value in the low half
                                         am_acc = fold_bf16x2_biased(
                                             am_acc, (uint32_t)reinterpret_cast<const uint16_t*>(ev)[x]);
                                     else if constexpr (FOLD)
@@ -1035,7 +1044,10 @@ __device__ __forceinline__ void persistent_body(
         stamp(3 + 3 * tile);
     }
     if constexpr (AMAX_OUT) {  // every block, tiles or none, writes its 8 partials
-        uint32_t m = sizeof(FoldT) == 2 ? unbias_bf16x2(am_acc) : unbias_f32(am_acc);
+        uint32_t m;
+        if constexpr (std::is_same<FoldT, f16_t>::value) m = unbias_f16x2(am_acc);
+        else if constexpr (sizeof(FoldT) == 2) m = unbias_bf16x2(am_acc);
+        else m = unbias_f32(am_acc);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
         if (lane == 0) amax_part[bl * 8 + w] = m;
@@ -1450,7 +1462,8 @@ static void launch_grouped(const GemmArgs& dw, const GemmArgs& dx, const GroupPl
                            uint32_t* amax_part = nullptr) {
     const PProb p1{dx.A, dx.B, dx.C, dx.sa, dx.sb, dx.lda, dx.ldb, dx.M, dx.N, dx.K, dx.ldc,
                    epi_store_mode(dx.C, (int64_t)dx.ldc * (int64_t)sizeof(DxT))};
-    constexpr bool FOLDS = std::is_same<DxT, uint16_t>::value || std::is_same<DxT, float>::value;
+    constexpr bool FOLDS =
+        std::is_same<DxT, uint16_t>::value || std::is_same<DxT, f16_t>::value || std::is_same<DxT, float>::value;
     if (gp.S == 1) {
         const int vec_out = epi_store_mode(dw.C, (int64_t)dw.ldc * (int64_t)sizeof(DwT));
         if constexpr (FOLDS) {
@@ -1639,8 +1652,8 @@ extern "C" int df_fp8_gemm_fwd_absmax(const uint8_t* Xq, int ldx, const uint8_t*
                                       float* y_scale_dev, void* ws, size_t ws_bytes, void* stream) {
     clear_error();
     static const char* name = "df_fp8_gemm_fwd_absmax";
-    DF_CHECK(y_dtype == DF_DTYPE_BFLOAT16 || y_dtype == DF_DTYPE_FLOAT32, DF_ERR_UNSUPPORTED,
-             "%s: Y dtype %d (bf16 or fp32 only)", name, y_dtype);
+    DF_CHECK(y_dtype == DF_DTYPE_BFLOAT16 || y_dtype == DF_DTYPE_HALF || y_dtype == DF_DTYPE_FLOAT32,
+             DF_ERR_UNSUPPORTED, "%s: Y dtype %d (bf16, f16 or fp32 only)", name, y_dtype);
     DF_CHECK(next_fmt == E4M3 || next_fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad fp8 format %d", name, next_fmt);
     DF_CHECK(y_absmax_dev || y_scale_dev, DF_ERR_INVALID, "%s: no absmax or scale output", name);
     DF_CHECK(ldy == N, DF_ERR_INVALID, "%s: Y must be contiguous (ldy=%d, N=%d)", name, ldy, N);
@@ -1651,13 +1664,13 @@ extern "C" int df_fp8_gemm_fwd_absmax(const uint8_t* Xq, int ldx, const uint8_t*
     if (st != DF_OK) return st;
     DF_CHECK(ws && ws_bytes >= df_absmax_workspace_bytes(), DF_ERR_WORKSPACE,
              "%s: workspace %zu bytes < %zu", name, ws_bytes, df_absmax_workspace_bytes());
-    const bool bf16_out = y_dtype == DF_DTYPE_BFLOAT16;
+    const bool bf16_out = y_dtype == DF_DTYPE_BFLOAT16, f16_out = y_dtype == DF_DTYPE_HALF;
     const NtPlan p = empty ? NtPlan{} : nt_plan(g);
     if (!empty && p.kind == DF_GEMM_KERNEL_PERSISTENT && p.split == 1 &&
         ws_bytes >= (size_t)p.grid * 8 * sizeof(uint32_t)) {
         uint32_t* parts = static_cast<uint32_t*>(ws);
-        const int vec_out = epi_store_mode(g.C, (int64_t)g.ldc * (bf16_out ? 2 : 4));
-        const bool bbf = bias && bias_dtype == DF_DTYPE_BFLOAT16;
+        const int vec_out = epi_store_mode(g.C, (int64_t)g.ldc * (bf16_out || f16_out ? 2 : 4));
+        const bool bbf = bias && bias_dtype == DF_DTYPE_BFLOAT16, bhf = bias && bias_dtype == DF_DTYPE_HALF;
 #define DF_AMAX_LAUNCH(OutT, BiasT, HB)                                                                          \
     gemm_nt_persistent_amax_kernel<E4M3, E4M3, OutT, BiasT, HB><<<p.grid, 512, 0, g.st>>>(                      \
         g.A, g.lda, g.B, g.ldb, g.M, g.N, g.K, g.sa, g.sb, static_cast<const BiasT*>(g.bias),                     \
@@ -1666,6 +1679,10 @@ extern "C" int df_fp8_gemm_fwd_absmax(const uint8_t* Xq, int ldx, const uint8_t*
             if (!bias) DF_AMAX_LAUNCH(uint16_t, float, false);
             else if (bbf) DF_AMAX_LAUNCH(uint16_t, uint16_t, true);
             else DF_AMAX_LAUNCH(uint16_t, float, true);
+        } else if (f16_out) {  // nt_args admits an fp32 or f16 bias here
+            if (!bias) DF_AMAX_LAUNCH(f16_t, float, false);
+            else if (bhf) DF_AMAX_LAUNCH(f16_t, f16_t, true);
+            else DF_AMAX_LAUNCH(f16_t, float, true);
         } else {
             if (!bias) DF_AMAX_LAUNCH(float, float, false);
             else if (bbf) DF_AMAX_LAUNCH(float, uint16_t, true);
@@ -1681,6 +1698,9 @@ extern "C" int df_fp8_gemm_fwd_absmax(const uint8_t* Xq, int ldx, const uint8_t*
                          stream);
     if (st != DF_OK) return st;
     const int64_t n = (int64_t)M * N;
+    if (f16_out)
+        return df_absmax_scale_f16(static_cast<const uint16_t*>(Y), n, next_fmt, y_absmax_dev, y_scale_dev, ws,
+                                   ws_bytes, stream);
     return bf16_out ? df_absmax_scale_bf16(static_cast<const uint16_t*>(Y), n, next_fmt, y_absmax_dev, y_scale_dev,
                                            ws, ws_bytes, stream)
                     : df_absmax_scale_f32(static_cast<const float*>(Y), n, next_fmt, y_absmax_dev, y_scale_dev, ws,
@@ -1770,8 +1790,9 @@ static int bwd_impl(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt, 
                                   stream);
     }
     const bool dw32 = dw_dtype == DF_DTYPE_FLOAT32, dx32 = dx_dtype == DF_DTYPE_FLOAT32;
-    if (amax_part && !h_dx) {
-        if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus, amax_part);
+    if (amax_part) {
+        if (h_dx) launch_grouped<f16_t, f16_t>(dw, dx, gp, cus, amax_part);
+        else if (dw32 && dx32) launch_grouped<float, float>(dw, dx, gp, cus, amax_part);
         else if (dw32) launch_grouped<float, uint16_t>(dw, dx, gp, cus, amax_part);
         else if (dx32) launch_grouped<uint16_t, float>(dw, dx, gp, cus, amax_part);
         else launch_grouped<uint16_t, uint16_t>(dw, dx, gp, cus, amax_part);
@@ -1813,8 +1834,8 @@ extern "C" int df_fp8_gemm_bwd_absmax(const uint8_t* dYq, int lddy, const uint8_
                                       size_t ws_bytes, void* stream) {
     clear_error();
     static const char* name = "df_fp8_gemm_bwd_absmax";
-    DF_CHECK(dx_dtype == DF_DTYPE_BFLOAT16 || dx_dtype == DF_DTYPE_FLOAT32, DF_ERR_UNSUPPORTED,
-             "%s: dX dtype %d (bf16 or fp32 only)", name, dx_dtype);
+    DF_CHECK(dx_dtype == DF_DTYPE_BFLOAT16 || dx_dtype == DF_DTYPE_HALF || dx_dtype == DF_DTYPE_FLOAT32,
+             DF_ERR_UNSUPPORTED, "%s: dX dtype %d (bf16, f16 or fp32 only)", name, dx_dtype);
     DF_CHECK(next_fmt == E4M3 || next_fmt == E5M2, DF_ERR_UNSUPPORTED, "%s: bad fp8 format %d", name, next_fmt);
     DF_CHECK(dx_absmax_dev || dx_scale_dev, DF_ERR_INVALID, "%s: no absmax or scale output", name);
     DF_CHECK(lddx == K, DF_ERR_INVALID, "%s: dX must be contiguous (lddx=%d, K=%d)", name, lddx, K);
@@ -1833,6 +1854,9 @@ extern "C" int df_fp8_gemm_bwd_absmax(const uint8_t* dYq, int lddy, const uint8_
         return launch_status(name);
     }
     const int64_t n = (int64_t)M * K;
+    if (dx_dtype == DF_DTYPE_HALF)
+        return df_absmax_scale_f16(static_cast<const uint16_t*>(dX), n, next_fmt, dx_absmax_dev, dx_scale_dev, ws,
+                                   kBwdAmaxReserve, stream);
     return dx_dtype == DF_DTYPE_BFLOAT16
                ? df_absmax_scale_bf16(static_cast<const uint16_t*>(dX), n, next_fmt, dx_absmax_dev, dx_scale_dev,
                                       ws, kBwdAmaxReserve, stream)

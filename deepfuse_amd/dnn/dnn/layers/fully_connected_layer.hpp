@@ -51,7 +51,7 @@ public:
     // output (df_fp8_gemm_fwd_absmax), which sets this layer's input scale,
     // so the output is not read again for it.  Same values as the unfused
     // pair; prev caches for its backward as prev.forward would.  With
-    // delayed scaling on this layer, or TT = __half, it is the unfused pair.
+    // delayed scaling on this layer it is the unfused pair.
     tensor<TT> forward(FullyConnectedLayer<TT>& prev, const tensor<TT>& input);
     tensor<TT> backward(const tensor<TT>& grad_output) override;
     // backward(next.backward(grad_output)) where next is the layer this one
@@ -123,7 +123,6 @@ private:
     float* input_scale_slot(int N);
     // where grad_output's scale lives
     float* grad_scale_slot();
-    static constexpr bool kChains = !std::is_same_v<TT, __half>;  // the fused chain takes bf16 / fp32
 
     int in_features_;
     int out_features_;

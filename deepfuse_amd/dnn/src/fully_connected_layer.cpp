@@ -216,7 +216,7 @@ tensor<TT> FullyConnectedLayer<TT>::forward(FullyConnectedLayer<TT>& prev, const
     if (prev.out_features_ != in_features_)
         throw std::invalid_argument("FullyConnectedLayer::forward: a layer of " + std::to_string(prev.out_features_) +
                                     " outputs feeds a layer of " + std::to_string(in_features_) + " inputs");
-    if (!kChains || history_len_ > 0 || &prev == this) return forward(prev.forward(input));
+    if (history_len_ > 0 || &prev == this) return forward(prev.forward(input));
     const auto& sh = input.shape();
     // checked before input_scale_slot may replace this layer's cached X^T
     if (sh.size() != 2 || sh[1] != prev.in_features_)
@@ -315,7 +315,7 @@ tensor<TT> FullyConnectedLayer<TT>::backward(FullyConnectedLayer<TT>& next, cons
     if (next.in_features_ != out_features_)
         throw std::invalid_argument("FullyConnectedLayer::backward: a layer of " + std::to_string(out_features_) +
                                     " outputs feeds a layer of " + std::to_string(next.in_features_) + " inputs");
-    if (!kChains || history_len_ > 0 || &next == this) return backward(next.backward(grad_output));
+    if (history_len_ > 0 || &next == this) return backward(next.backward(grad_output));
     float* slot = grad_scale_slot();
     const tensor<TT> grad_hidden = next.backward_impl(grad_output, nullptr, slot);
     return backward_impl(grad_hidden, slot);

@@ -350,10 +350,10 @@ int df_fp8_gemm_fwd_timeline(const uint8_t* Xq, int ldx, const uint8_t* Wq, int 
 /* The forward GEMM of df_fp8_gemm_fwd whose Y also gives the absmax the next
  * Linear's just-in-time scale needs (new; no counterpart in the reference,
  * whose TransformerBlock feeds fc1's output straight into fc2,
- * dnn/layers/transformer_block.cu:79-81).  Y (bf16 or fp32, contiguous:
+ * dnn/layers/transformer_block.cu:79-81).  Y (bf16, f16 or fp32, contiguous:
  * ldy == N) is bit-identical to df_fp8_gemm_fwd's.  *y_absmax_dev gets the
  * absmax over the finite values of Y as stored, and *y_scale_dev the rule-D1/D2
- * scale for next_fmt, exactly what df_absmax_scale_bf16 / _f32 give on Y
+ * scale for next_fmt, exactly what df_absmax_scale_bf16 / _f16 / _f32 give on Y
  * (either output may be NULL, not both).  On the unsplit 256x256 plan the
  * kernel folds |Y| in its epilogue and one block folds the partials, so Y
  * is not read again; other plans run the two passes.  ws:
@@ -410,14 +410,15 @@ int df_fp8_gemm_bwd(const uint8_t* dYq, int lddy, const uint8_t* Wtq, int ldwt,
 /* df_fp8_gemm_bwd whose dX also gives the absmax the upstream Linear's
  * just-in-time dY scale needs (new; no counterpart in the reference, whose
  * TransformerBlock backward passes fc2's input gradient straight to fc1 as
- * its output gradient, dnn/layers/transformer_block.cu:127-134).  dX (bf16
- * or fp32, contiguous: lddx == K, 16-byte aligned) and dW are bit-identical
+ * its output gradient, dnn/layers/transformer_block.cu:127-134).  dX (bf16,
+ * f16 or fp32, contiguous: lddx == K, 16-byte aligned) and dW are bit-identical
  * to df_fp8_gemm_bwd's with a workspace of df_fp8_gemm_bwd_workspace_bytes.
  * *dx_absmax_dev gets the absmax over the finite values of dX as stored and
  * *dx_scale_dev the rule-D1/D2 scale for next_fmt (either may be NULL, not
- * both): what df_absmax_scale_bf16 / _f32 give on dX.  When the plan is the
- * grouped launch, its dX tiles fold |dX| in their epilogue and one block
- * folds the partials; otherwise dX is read again by the absmax pass.  ws:
+ * both): what df_absmax_scale_bf16 / _f16 / _f32 give on dX.  When the plan
+ * is the grouped launch (an f16 dX groups with an f16 dW only), its dX
+ * tiles fold |dX| in their epilogue and one block folds the partials;
+ * otherwise dX is read again by the absmax pass.  ws:
  * df_fp8_gemm_bwd_absmax_workspace_bytes(M, N, K) (its first part holds the
  * partials, the rest is df_fp8_gemm_bwd's workspace). */
 size_t df_fp8_gemm_bwd_absmax_workspace_bytes(int M, int N, int K);

@@ -1143,9 +1143,10 @@ TEST_F(FullyConnectedLayerTest, LayerNormFusedEqualsUnfused) {
 // (transformer_block.cu:79-81, :127-134): fc2.forward(fc1, x) and
 // fc1.backward(fc2, gy) equal the unfused pairs bit for bit -- output, input
 // gradient, both layers' weight and bias gradients -- over two training
-// steps, on a small shape (the fused GEMMs' two-pass form) and on one whose
-// fc1 output takes the persistent kernel that folds the absmax; with delayed
-// scaling on the layers they are the unfused pairs.
+// steps, for float, bf16 and binary16 layers, on a small shape (the fused
+// GEMMs' two-pass form) and on one whose fc1 output takes the persistent
+// kernel that folds the absmax; with delayed scaling on the layers they are
+// the unfused pairs.
 template <typename TT>
 std::vector<float> chain_dl(const tensor<TT>& t) {
     if constexpr (std::is_same_v<TT, float>) return download(t);
@@ -1155,6 +1156,7 @@ std::vector<float> chain_dl(const tensor<TT>& t) {
 template <typename TT>
 void chain_up(tensor<TT>& t, const std::vector<float>& v) {
     if constexpr (std::is_same_v<TT, float>) t.upload(v.data());
+    else if constexpr (std::is_same_v<TT, __half>) upload_f16(t, v);
     else upload_bf16(t, v);
 }
 
@@ -1195,6 +1197,8 @@ TEST_F(FullyConnectedLayerTest, ChainedPairEqualsUnfused) {
     chain_case<float>(48, 160, 96, 72, 4, 320);
     chain_case<float>(4096, 512, 4096, 512, 0, 330);
     chain_case<bfloat16>(4096, 512, 4096, 512, 0, 340);
+    chain_case<__half>(48, 160, 96, 72, 0, 350);
+    chain_case<__half>(4096, 512, 4096, 512, 0, 360);
 }
 
 TEST_F(FullyConnectedLayerTest, ChainedPairChecksSizes) {

@@ -7,7 +7,7 @@ The reference's TransformerBlock feeds fc1's output straight into fc2
 absmax of fc1's Y.  Bars:
 - Y bit-identical to df_fp8_gemm_fwd's on the same codes, bias and output
   type (the fused epilogue only adds a fold);
-- absmax and scale bit-identical to df_absmax_scale_bf16 / _f32 over that Y
+- absmax and scale bit-identical to df_absmax_scale_bf16 / _f16 / _f32 over that Y
   (finite values only, as stored, rule D1/D2 for the next format);
 - on the config-4 shapes the planner takes the unsplit 256x256 persistent
   kernel (the fused path, asserted through df_fp8_gemm_nt_plan); small,
@@ -29,6 +29,13 @@ from oracle import pyoracle as orc
 pytestmark = pytest.mark.gpu
 
 
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _bits(t):
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
 def _codes(rows, cols, std, seed, dev):
     x = torch.from_numpy(synth.normal((rows, cols), std, seed=seed)).to(dev).to(torch.bfloat16)
     _, s = df.absmax_scale(x, Fmt.E4M3)
@@ -46,6 +53,9 @@ CASES = [
     (129, 272, 257, "f32", "bf16"),
     (1407, 53, 3584, "bf16", "f32"),
     (300, 8192, 200, "bf16", "bf16"),  # a long reduction on a small output
+    (16384, 1600, 6400, "f16", "f16"),  # binary16 output (the reference's FP16 layer line)
+    (4096, 768, 3072, "f16", None),
+    (129, 272, 257, "f16", "f32"),
 ]
 
 
@@ -56,14 +66,12 @@ def test_fwd_absmax_matches_separate_passes(dev, M, K, N, out, bias):
     wq, sw = _codes(N, K, 0.02, seed + 1, dev)
     b = None
     if bias is not None:
-        b = torch.from_numpy(synth.normal((N,), 0.1, seed=seed + 2)).to(dev)
-        b = b.to(torch.bfloat16) if bias == "bf16" else b
-    dt = torch.bfloat16 if out == "bf16" else torch.float32
+        b = torch.from_numpy(synth.normal((N,), 0.1, seed=seed + 2)).to(dev).to(DT[bias])
+    dt = DT[out]
     for fmt in (Fmt.E4M3, Fmt.E5M2):
         y, am, sc = df.gemm_fwd_absmax(xq, wq, K, sx, sw, bias=b, out_dtype=dt, next_fmt=fmt)
         y_ref = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, bias=b, out_dtype=dt)
-        assert torch.equal(y.view(torch.int16 if out == "bf16" else torch.int32),
-                           y_ref.view(torch.int16 if out == "bf16" else torch.int32)), f"{M}x{K}x{N}: Y"
+        assert torch.equal(_bits(y), _bits(y_ref)), f"{M}x{K}x{N}: Y"
         am_ref, sc_ref = df.absmax_scale(y_ref, fmt)
         assert am.view(torch.int32).item() == am_ref.view(torch.int32).item(), f"{M}x{K}x{N} fmt={int(fmt)}: absmax"
         assert sc.view(torch.int32).item() == sc_ref.view(torch.int32).item(), f"{M}x{K}x{N} fmt={int(fmt)}: scale"
@@ -93,7 +101,7 @@ def test_next_linear_codes_from_fused_scale(dev):
     assert np.array_equal(q.cpu().numpy()[:, :N], orc.quantize(vals, s, int(Fmt.E4M3)))
 
 
-@pytest.mark.parametrize("out", ["bf16", "f32"])
+@pytest.mark.parametrize("out", ["bf16", "f16", "f32"])
 def test_fused_fold_skips_inf_and_nan(dev, out):
     """On the fused plan, a Y with NaN rows (a NaN code in X) and overflowed
     values (+-inf from scales whose product pushes the largest outputs past
@@ -102,12 +110,11 @@ def test_fused_fold_skips_inf_and_nan(dev, out):
     M, K, N = 4096, 768, 3072
     ws = int(df.lib().df_fp8_gemm_fwd_absmax_workspace_bytes(M, N, K))
     assert df.gemm_plan(M, N, K, K, K, None, ws) == (df.GemmKernel.PERSISTENT, 1)
-    dt = torch.bfloat16 if out == "bf16" else torch.float32
-    bits = torch.int16 if out == "bf16" else torch.int32
+    dt = DT[out]
     xq, sx = _codes(M, K, 1.0, 501, dev)
     wq, sw = _codes(N, K, 0.02, 502, dev)
     top = df.gemm_nt(xq, Fmt.E4M3, wq, Fmt.E4M3, K, sx, sw, out_dtype=torch.float32).abs().max().item()
-    f = 2.0 * 3.4e38 / top  # the largest |Y| lands near twice the type's maximum
+    f = 2.0 * torch.finfo(dt).max / top  # the largest |Y| lands near twice the type's maximum
     f1 = 2.0 ** int(np.log2(f) / 2)
     sx2, sw2 = sx * f1, sw * (f / f1)
     xq[123, 5] = 0x7F  # e4m3 NaN
@@ -115,7 +122,7 @@ def test_fused_fold_skips_inf_and_nan(dev, out):
     for xin in (xq, torch.full_like(xq, 0x7F)):
         y, am, sc = df.gemm_fwd_absmax(xin, wq, K, sx2, sw2, out_dtype=dt, next_fmt=Fmt.E4M3)
         y_ref = df.gemm_nt(xin, Fmt.E4M3, wq, Fmt.E4M3, K, sx2, sw2, out_dtype=dt)
-        assert torch.equal(y.view(bits), y_ref.view(bits))
+        assert torch.equal(_bits(y), _bits(y_ref))
         assert torch.isnan(y_ref).any()
         if xin is xq:
             assert torch.isinf(y_ref).any() and torch.isfinite(y_ref).any()
@@ -159,13 +166,13 @@ BWD_CASES = [
 def test_bwd_absmax_matches_separate_passes(dev, M, K, N):
     print(f"bwd absmax {M}x{K}x{N} plan {df.gemm_bwd_plan(M, N, K)}", flush=True)
     dyq, wt, dyt, xt, sdy, sw, sx = _bwd_operands(dev, M, K, N, seed=7100 + M + 3 * K + 5 * N)
-    for dx_dt, dw_dt, fmt in ((torch.bfloat16, torch.float32, Fmt.E5M2), (torch.float32, torch.bfloat16, Fmt.E4M3)):
+    for dx_dt, dw_dt, fmt in ((torch.bfloat16, torch.float32, Fmt.E5M2), (torch.float32, torch.bfloat16, Fmt.E4M3),
+                              (torch.float16, torch.float16, Fmt.E5M2)):
         dX, dW, am, sc = df.gemm_bwd_absmax(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, dx_dtype=dx_dt, dw_dtype=dw_dt,
                                             next_fmt=fmt)
         dX1, dW1 = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx, dx_dtype=dx_dt, dw_dtype=dw_dt)
-        bits = lambda t: t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
-        assert torch.equal(bits(dX), bits(dX1)), f"{M}x{K}x{N}: dX"
-        assert torch.equal(bits(dW), bits(dW1)), f"{M}x{K}x{N}: dW"
+        assert torch.equal(_bits(dX), _bits(dX1)), f"{M}x{K}x{N} {dx_dt}: dX"
+        assert torch.equal(_bits(dW), _bits(dW1)), f"{M}x{K}x{N} {dx_dt}: dW"
         am1, sc1 = df.absmax_scale(dX1, fmt)
         assert am.view(torch.int32).item() == am1.view(torch.int32).item(), f"{M}x{K}x{N}: absmax"
         assert sc.view(torch.int32).item() == sc1.view(torch.int32).item(), f"{M}x{K}x{N}: scale"
@@ -198,23 +205,26 @@ def test_fc1_dy_codes_from_fused_scale(dev):
     assert np.array_equal(qt.cpu().numpy()[:, :M], np.ascontiguousarray(flat.T))
 
 
-@pytest.mark.parametrize("out", ["bf16", "f32"])
+@pytest.mark.parametrize("out", ["bf16", "f16", "f32"])
 def test_bwd_fold_skips_inf_and_nan(dev, out):
     """On a grouped plan: dX with NaN rows (a NaN code in dY) and overflowed
-    values gives the absmax of its finite values only."""
+    values gives the absmax of its finite values only (an f16 dX groups with
+    an f16 dW)."""
     M, K, N = 16384, 1600, 6400
     assert df.gemm_bwd_plan(M, N, K)[0]
-    dt = torch.bfloat16 if out == "bf16" else torch.float32
-    bits = torch.int16 if out == "bf16" else torch.int32
+    dt = DT[out]
+    dwt = torch.float16 if out == "f16" else torch.float32
     dyq, wt, dyt, xt, sdy, sw, sx = _bwd_operands(dev, M, K, N, seed=95)
     top = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy, sw, sx)[0].abs().max().item()
-    f = 2.0 * 3.4e38 / top
+    f = 2.0 * torch.finfo(dt).max / top
     f1 = 2.0 ** int(np.log2(f) / 2)
     sdy2, sw2 = sdy * f1, sw * (f / f1)
     dyq[77, 3] = 0x7F  # e5m2 NaN
-    dX, dW, am, sc = df.gemm_bwd_absmax(dyq, wt, dyt, xt, M, N, K, sdy2, sw2, sx, dx_dtype=dt, next_fmt=Fmt.E5M2)
-    dX1, _ = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy2, sw2, sx, dx_dtype=dt)
-    assert torch.equal(dX.view(bits), dX1.view(bits))
+    dX, dW, am, sc = df.gemm_bwd_absmax(dyq, wt, dyt, xt, M, N, K, sdy2, sw2, sx, dx_dtype=dt, dw_dtype=dwt,
+                                        next_fmt=Fmt.E5M2)
+    dX1, dW1 = df.gemm_bwd(dyq, wt, dyt, xt, M, N, K, sdy2, sw2, sx, dx_dtype=dt, dw_dtype=dwt)
+    assert torch.equal(_bits(dX), _bits(dX1))
+    assert torch.equal(_bits(dW), _bits(dW1))
     assert torch.isnan(dX1).any() and torch.isinf(dX1).any() and torch.isfinite(dX1).any()
     am1, sc1 = df.absmax_scale(dX1, Fmt.E5M2)
     assert am.view(torch.int32).item() == am1.view(torch.int32).item()
