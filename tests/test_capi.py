@@ -72,21 +72,22 @@ def test_argument_errors():
     assert g(0, FAKE, 16, 0, FAKE, 16, 4, 5, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1  # ldc < N
     assert g(0, FAKE, 16, 0, FAKE, 16, -1, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == -1
     assert g(0, FAKE, 16, 0, FAKE, 16, 0, 4, 16, FAKE, FAKE, 0, None, 0, FAKE, 4, None, 0, None) == 0  # M = 0
-    # forward GEMM with Y's absmax: bf16 / fp32 Y only, a known format, an output, contiguous Y
+    # forward GEMM with Y's absmax: bf16 / f16 / fp32 Y only, a known format, an output, contiguous Y
     fa = df.lib().df_fp8_gemm_fwd_absmax
     bf, f32 = int(DType.BFLOAT16), int(DType.FLOAT32)
-    assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, int(DType.HALF), FAKE, 4, 0, FAKE, FAKE, FAKE,
+    assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, int(DType.INT8), FAKE, 4, 0, FAKE, FAKE, FAKE,
               4096, None) == -2
     assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, bf, FAKE, 4, 7, FAKE, FAKE, FAKE, 4096, None) == -2
     assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, bf, FAKE, 4, 0, None, None, FAKE, 4096, None) == -1
     assert fa(FAKE, 16, FAKE, 16, 4, 4, 16, FAKE, FAKE, 0, None, f32, FAKE, 8, 0, FAKE, None, FAKE, 4096, None) == -1
     assert "contiguous" in err()
     assert df.lib().df_fp8_gemm_fwd_absmax_workspace_bytes(16384, 6400, 1600) >= 64 * 25 * 8 * 4
-    # backward with dX's absmax: bf16 / fp32 dX, a known format, an output, contiguous dX, room for the partials
+    # backward with dX's absmax: bf16 / f16 / fp32 dX, a known format, an output, contiguous dX, room for the
+    # partials
     ba = lambda dxt, lddx, fmt, am, sc, wsb: status(
         "df_fp8_gemm_bwd_absmax", FAKE, 16, FAKE, 16, FAKE, 16, FAKE, 16, 16, 16, 16, FAKE, FAKE, FAKE, dxt, FAKE, lddx,
         f32, FAKE, 16, fmt, am, sc, FAKE, wsb, None)
-    assert ba(int(DType.HALF), 16, 1, FAKE, FAKE, 1 << 20) == -2
+    assert ba(int(DType.INT8), 16, 1, FAKE, FAKE, 1 << 20) == -2
     assert ba(bf, 16, 9, FAKE, FAKE, 1 << 20) == -2
     assert ba(bf, 16, 1, None, None, 1 << 20) == -1
     assert ba(f32, 32, 1, FAKE, None, 1 << 20) == -1
